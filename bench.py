@@ -1,0 +1,332 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MOGT scan operator (one GPU).
+
+Headline: the diagonal affine scan core at B=1,
+D=768, L=32768, fp32 I/O.  One "step" = one launch of the single-pass scan
+over one batch with inputs already resident in HBM.  Three input/output sets
+are rotated (906 MB working set) so the 256 MB Infinity Cache cannot serve the
+re-reads.  Timing: HIP events on the launch stream around K launches, after W
+warm-up launches; the roofline uses algorithmic bytes (read a, read b, write h
+= 3 * 4 * D bytes per token) over the average launch duration.
+
+The CPU baseline is the reference's sequential PyTorch scan restated in
+oracle/torch_ref.py (a Python loop over L of torch.bmm, fp32 state), run on the
+host cores over the same folded workload.
+
+Prints ONE JSON line on stdout.  Extra measurements (other lengths, bf16 I/O,
+the coupled mixer scan) go under "extras".
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "scan core ms + HBM GB/s at D768 L=32768; MOGT 4-layer fwd ms"
+HBM_PEAK_GBS = 8000.0
+REF_TRITON_CORE_MS_L4 = 5.48   # reference hybrid core @ L=32768 (R=16, C=48, NVIDIA L4)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true")
+    p.add_argument("--only", choices=["diag", "all"], default="all")
+    p.add_argument("--tile", default=None, help="vec,steps,waves override for the diag scan")
+    p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
+    p.add_argument("--calib-copy", action="store_true",
+                   help="also run a plain 256 MiB device copy (PMC calibration)")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------- helpers
+class EventTimer:
+    """HIP events recorded on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.torch = torch
+        self.stream = stream
+
+    def time(self, fn, steps: int, warmup: int) -> float:
+        torch = self.torch
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(self.stream)
+        for i in range(steps):
+            fn(i)
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps   # ms per launch
+
+
+def diag_launcher(torch, lib, ops, B, L, D, dtype, out_dtype, sets, tile=None, seed=1):
+    """Rotating input/output sets and a closure that launches one scan via the C ABI."""
+    from mogt_amd import synthetic
+
+    a, b = synthetic.diag_inputs(B, L, D, a_mean=3.0, b_std=0.5, seed=seed)
+    dev = torch.device("cuda:0")
+    a0 = torch.from_numpy(a).to(dev).to(dtype)
+    b0 = torch.from_numpy(b).to(dev).to(dtype)
+    bufs = []
+    for _ in range(sets):
+        bufs.append((a0.clone(), b0.clone(), torch.empty(B, L, D, dtype=out_dtype, device=dev)))
+    del a0, b0
+    ic = ops.dtype_code(dtype, "bench")
+    oc = ops.dtype_code(out_dtype, "bench")
+    if tile is None:
+        nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, ic)
+    else:
+        nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, D, *tile)
+    ws = ops.workspace(nbytes, dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    args = [(x.data_ptr(), y.data_ptr(), z.data_ptr()) for x, y, z in bufs]
+    wsp, wsn = ws.data_ptr(), ws.numel()
+
+    if tile is None:
+        fn = lib.mogt_diag_scan_fwd
+
+        def launch(i):
+            pa, pb, ph = args[i % sets]
+            rc = fn(pa, pb, ph, None, B, L, D, ic, oc, wsp, wsn, sh)
+            if rc:
+                raise RuntimeError(lib.mogt_last_error().decode())
+    else:
+        fn = lib.mogt_diag_scan_fwd_cfg
+        v, s, w = tile
+
+        def launch(i):
+            pa, pb, ph = args[i % sets]
+            rc = fn(pa, pb, ph, None, B, L, D, ic, oc, v, s, w, wsp, wsn, sh)
+            if rc:
+                raise RuntimeError(lib.mogt_last_error().decode())
+
+    return launch, stream, bufs
+
+
+def measure_diag(torch, lib, ops, L, dtype, out_dtype, steps, warmup, tile=None, D=768, B=1):
+    esz = 2 if dtype == torch.bfloat16 else 4
+    osz = 2 if out_dtype == torch.bfloat16 else 4
+    total = B * L * D * (2 * esz + osz)
+    sets = max(2, min(6, int((1 << 30) // total) + 1))
+    launch, stream, bufs = diag_launcher(torch, lib, ops, B, L, D, dtype, out_dtype, sets, tile)
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    del bufs
+    return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
+
+
+def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
+    """Model-shaped coupled per-rank gate scan (config 2'): z fp32 [1,L,16],
+    v bf16 [1,L,768] -> h fp32 [1,L,768]."""
+    from mogt_amd import synthetic
+
+    dev = torch.device("cuda:0")
+    z, v = synthetic.coupled_inputs(1, L, r, c, seed=3)
+    zt = torch.from_numpy(z).to(dev)
+    vt = torch.from_numpy(v).to(dev).bfloat16()
+    sets = 4
+    bufs = [(zt.clone(), vt.clone(), torch.empty(1, L, r * c, device=dev)) for _ in range(sets)]
+    nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(1, L, r, c, 1)
+    ws = ops.workspace(nbytes, dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    fn = lib.mogt_coupled_rank_scan_fwd
+
+    def launch(i):
+        zz, vv, hh = bufs[i % sets]
+        rc = fn(zz.data_ptr(), vv.data_ptr(), hh.data_ptr(), 1, L, r, c, 1.0, 0, 1, 0,
+                ws.data_ptr(), ws.numel(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    total = L * (r * 4 + r * c * 2 + r * c * 4)
+    return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline(L=32768, D=768):
+    """Reference CPU PyTorch scan (sequential bmm loop, fp32 state) on the folded
+    R=C=1 workload, on this host's cores."""
+    import torch
+
+    from mogt_amd import synthetic
+    from oracle import torch_ref
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    a, b = synthetic.cfg2_inputs(L, seed=1)
+    U, V = torch_ref.diag_as_affine(torch.from_numpy(a), torch.from_numpy(b))
+    U, V = U.contiguous(), V.contiguous()
+    torch_ref.affine_scan_sequential_torch(U[:, :256], V[:, :256])   # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_ref.affine_scan_sequential_torch(U, V)
+        times.append(time.perf_counter() - t0)
+    t_seq = statistics.median(times)
+    t0 = time.perf_counter()
+    torch_ref.affine_scan_doubling_torch(U, V)
+    t_dbl = time.perf_counter() - t0
+    total = L * D * 12
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": total / t_seq / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"full workload D=768 L={L} fp32, folded R=C=1 (768 sequences): sequential "
+                   f"bmm loop median of 3 = {t_seq * 1e3:.1f} ms; doubling variant "
+                   f"{t_dbl * 1e3:.1f} ms; {cpu}; torch {torch.__version__}"),
+        "ms": t_seq * 1e3,
+        "doubling_ms": t_dbl * 1e3,
+    }
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by a plain copy's counter reading); kept as key=value text."""
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    kv = {}
+    for line in path.read_text().splitlines():
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            kv[k.strip()] = v.strip()
+    try:
+        return float(kv["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the scan is "
+              "single-GPU in this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import mogt_amd
+    from mogt_amd import ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    lib = mogt_amd._lib.load()
+    torch.cuda.init()
+    tile = tuple(int(x) for x in args.tile.split(",")) if args.tile else None
+
+    if args.calib_copy:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy of {n} bytes done (x5)")
+
+    if args.sweep:
+        tiles = [(1, 32, 4), (1, 16, 4), (2, 16, 4), (2, 8, 4), (4, 8, 4), (4, 16, 4), (4, 4, 4),
+                 (1, 32, 8), (2, 16, 8), (4, 8, 8)]
+        for dt in (torch.float32, torch.bfloat16):
+            for t in tiles:
+                r = measure_diag(torch, lib, ops, 32768, dt, dt, args.steps, args.warmup, tile=t)
+                log(f"sweep {dt} tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
+                    f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+
+    log("headline: diag scan fp32 B=1 D=768 L=32768")
+    head = measure_diag(torch, lib, ops, 32768, torch.float32, torch.float32, args.steps,
+                        args.warmup, tile=tile)
+    log(f"headline: {head['ms'] * 1e3:.1f} us/launch, {head['gbs']:.0f} GB/s")
+
+    extras = {}
+    if not args.no_extras and args.only == "all":
+        for L in (8192, 16384):
+            r = measure_diag(torch, lib, ops, L, torch.float32, torch.float32, args.steps,
+                             args.warmup)
+            extras[f"diag_fp32_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        for L in (8192, 32768):
+            r = measure_diag(torch, lib, ops, L, torch.bfloat16, torch.bfloat16, args.steps,
+                             args.warmup)
+            extras[f"diag_bf16_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
+        extras["coupled_rank_scan_r16c48_L32768"] = {
+            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+            "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
+        log(f"extras: {json.dumps(extras)}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (reference sequential torch scan restated, host cores)")
+        cpu = cpu_baseline()
+        log(f"cpu baseline: {cpu['ms']:.0f} ms ({cpu['value']:.3f} GB/s)")
+
+    traffic = read_traffic("diag_scan_d768_l32768_fp32_traffic.txt")
+    achieved = head["gbs"]
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded PCG64; a=sigmoid(N(3,1)), b~N(0,0.5))",
+        "config": {
+            "workload": "diag_affine_scan B=1 D=768 L=32768 fp32 I/O, fp32 state "
+                        "(BASELINE configs[1])",
+            "batch": 1, "features": 768, "seq_len": 32768,
+            "tile": list(tile) if tile else "default",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": ({k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
+                         if cpu else None),
+        "scan_core_us": round(head["ms"] * 1e3, 3),
+        "reference_triton_core_ms_L4": REF_TRITON_CORE_MS_L4,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

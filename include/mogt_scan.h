@@ -1,0 +1,92 @@
+/*
+ * mogt_scan.h — C ABI of the MI355X (gfx950) MOGT scan operator.
+ *
+ * Plain C: device pointers, sizes, dtype codes and an opaque HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream).  No torch types.
+ *
+ * Conventions shared by every entry point
+ *   - Tensors are contiguous row-major device buffers in the layouts named
+ *     below (the reference's layouts: U [B,L,R,R], V/H [B,L,R,C]).
+ *   - Arithmetic and carried state are fp32; I/O may be fp32 or bf16.
+ *   - Work is enqueued on `stream`; calls are asynchronous.
+ *   - Return 0 on success, a negative MOGT_E* code on failure; the message is
+ *     kept per thread and read with mogt_last_error().
+ *   - Nothing here allocates or frees device memory.  Single-pass scans take a
+ *     caller-owned `workspace` of at least *_workspace_bytes(...) bytes.  It
+ *     must be zero-filled before its FIRST use; each launch leaves it ready for
+ *     the next one (no per-call clearing).  Launches that may run concurrently
+ *     (different streams) must use different workspaces.
+ */
+#ifndef MOGT_SCAN_H
+#define MOGT_SCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define MOGT_F32 0
+#define MOGT_BF16 1
+
+/* error codes */
+#define MOGT_OK 0
+#define MOGT_E_INVALID -1   /* bad shape / dtype / argument (reference: ValueError) */
+#define MOGT_E_WORKSPACE -2 /* workspace missing or too small */
+#define MOGT_E_LAUNCH -3    /* HIP launch error */
+
+/* Last error message of the calling thread ("" if none). */
+const char* mogt_last_error(void);
+
+/* ABI version of the loaded library (bumped on incompatible changes). */
+int mogt_abi_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Diagonal affine scan  h_t = a_t * h_{t-1} + b_t,  h_0 = 0, per feature.
+ *
+ * Replaces affine_scan_sequential (affine_scan.py:14-62) in the folded R=C=1
+ * mapping U=a.transpose(1,2).reshape(B*D,L,1,1) that the reference would need
+ * for a per-feature scan, without the fold: a, b, h are [B, L, D].
+ * `a_prefix` (nullable) receives prod_{s<=t} a_s, the R=1 case of the
+ * reference's return_prefix=True U_prefix output (affine_scan.py:43-55).
+ * in_dtype applies to a and b; out_dtype to h and a_prefix.               */
+size_t mogt_diag_scan_workspace_bytes(int64_t batch, int64_t length, int64_t features,
+                                      int in_dtype);
+int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a_prefix,
+                       int64_t batch, int64_t length, int64_t features,
+                       int in_dtype, int out_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Same with an explicit tile configuration (features per lane, steps per
+ * thread, waves per work-group); used for tuning.  The workspace query takes
+ * the same triple.                                                          */
+size_t mogt_diag_scan_workspace_bytes_cfg(int64_t batch, int64_t length, int64_t features,
+                                          int vec, int steps, int waves);
+int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix,
+                           int64_t batch, int64_t length, int64_t features,
+                           int in_dtype, int out_dtype, int vec, int steps, int waves,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Coupled write-forget per-rank scan of the MOGT mixer with identity
+ * connection (model_mogt.py:166-203 with connection_impl="identity",
+ * phi_value_gate of width r, couple_forget_to_value_gate=True):
+ *   g = sigmoid(z[b,t,i]),  a = damping * (1 - g),  v' = v[b,t,i*C+j] * g
+ *   h[b,t,i*C+j] = a * h[b,t-1,i*C+j] + v'
+ * z: gate logits [B, L, R] (fp32 or bf16); v: [B, L, R*C]; h: [B, L, R*C].
+ * When v is bf16, v' is rounded to bf16 exactly as the reference's
+ * `V_t_raw * value_gate.to(V_t_raw.dtype)` does (model_mogt.py:180).       */
+size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t length, int64_t rank,
+                                              int64_t channels, int v_dtype);
+int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
+                               int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                               float damping, int z_dtype, int v_dtype, int out_dtype,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOGT_SCAN_H */

@@ -1,0 +1,86 @@
+"""Build the HIP C-ABI library ``mogt_amd/lib/libmogt_hip.so`` for gfx950.
+
+The library is plain HIP (no torch headers): every ``csrc/*.hip`` file is
+compiled with ``hipcc --offload-arch=gfx950`` and linked into one shared object
+that Python loads through ctypes (``mogt_amd._lib``).  The build is in-tree so
+the ``.so`` travels with the source tree to the GPU host.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "lib"
+LIBNAME = "libmogt_hip.so"
+INCLUDE = PKG.parent / "include"
+
+ARCH = os.environ.get("MOGT_OFFLOAD_ARCH", "gfx950")
+
+# Packed-FP32 VALU forms are switched off for every device compile.
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-rdc",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found: the MOGT HIP library cannot be built")
+    return exe
+
+
+def lib_path() -> Path:
+    return LIBDIR / LIBNAME
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+    noise = [ln for ln in res.stderr.splitlines()
+             if ln.strip() and "packed-fp32-ops" not in ln]
+    if noise:
+        print(f"[mogt build] {src.name}:\n" + "\n".join(noise))
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> Path:
+    """Compile every ``csrc/*.hip`` and link ``lib/libmogt_hip.so``."""
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    objdir = LIBDIR / "obj"
+    objdir.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objs = [objdir / (s.stem + ".o") for s in srcs]
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_compile, srcs, objs))
+    out = lib_path()
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    for o in objs:
+        o.unlink(missing_ok=True)
+    if verbose:
+        print(f"[mogt build] wrote {out}")
+    return out
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,97 @@
+"""ctypes binding of the HIP C-ABI library (``include/mogt_scan.h``).
+
+This is the only place Python touches the native library.  Loading fails
+loudly: there is no CPU or PyTorch fallback behind any public operator.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+from . import _build
+
+MOGT_F32 = 0
+MOGT_BF16 = 1
+ABI_VERSION = 1
+
+_c_void_p = ctypes.c_void_p
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/mogt_scan.h
+SIGNATURES: dict[str, tuple] = {
+    "mogt_last_error": (ctypes.c_char_p, []),
+    "mogt_abi_version": (_c_int, []),
+    "mogt_diag_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "mogt_diag_scan_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+         _c_void_p, _c_size, _c_void_p],
+    ),
+    "mogt_diag_scan_workspace_bytes_cfg": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
+    "mogt_diag_scan_fwd_cfg": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+         _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
+    "mogt_coupled_rank_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "mogt_coupled_rank_scan_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int,
+         _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class MogtError(RuntimeError):
+    """A native entry point returned an error code."""
+
+
+def library_path() -> Path:
+    override = os.environ.get("MOGT_HIP_LIB")
+    return Path(override) if override else _build.lib_path()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the native library; raise if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"MOGT HIP library not built: {path} is missing. "
+                "Run `python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)."
+            )
+        lib = ctypes.CDLL(str(path))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.mogt_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"MOGT HIP library ABI {ver} != expected {ABI_VERSION}: rebuild it")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().mogt_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(f"{what}: {msg}")
+        raise MogtError(f"{what} failed ({rc}): {msg}")
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

@@ -1,0 +1,201 @@
+"""PyTorch custom ops (``torch.ops.mogt.*``) over the HIP C-ABI library.
+
+Each op validates its inputs with the reference's ``ValueError`` conditions,
+allocates outputs through the PyTorch caching allocator, and enqueues the HIP
+kernel on the current stream.  The native library never allocates: single-pass
+scans get a persistent, zero-initialised workspace per (device, stream) that
+the kernels leave reusable after every launch.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.MOGT_F32, torch.bfloat16: _lib.MOGT_BF16}
+
+_ws_lock = threading.Lock()
+_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def dtype_code(dt: torch.dtype, what: str) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise ValueError(f"{what}: dtype {dt} not supported (float32 or bfloat16)") from None
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Zero-initialised scratch of at least ``nbytes`` for the current stream.
+
+    Kernels using the look-back protocol restore the buffer's reusable state at
+    the end of every launch, so it is zero-filled only when first allocated or
+    grown.  One buffer per (device, stream) keeps concurrent streams apart.
+    """
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _stream_handle(device))
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(int(nbytes), 1 << 16)
+            if buf is not None:
+                size = max(size, 2 * buf.numel())
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+        return buf
+
+
+def workspace_faults() -> int:
+    """Number of bounded look-back waits that gave up, summed over every cached
+    workspace (header word 3).  Always 0 unless the protocol was violated;
+    synchronises the device."""
+    with _ws_lock:
+        bufs = list(_ws_cache.values())
+    total = 0
+    for buf in bufs:
+        total += int(buf[12:16].view(torch.int32).item())
+    return total
+
+
+def require_cuda(what: str, *tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError(f"{what} requires CUDA tensors")
+
+
+# ---------------------------------------------------------------------------
+# diag_scan: h_t = a_t * h_{t-1} + b_t over [B, L, D]
+# ---------------------------------------------------------------------------
+def _diag_scan_launch(a: torch.Tensor, b: torch.Tensor, h: torch.Tensor,
+                      prefix: torch.Tensor | None, cfg: tuple[int, int, int] | None = None) -> None:
+    lib = _lib.load()
+    B, L, D = a.shape
+    in_code = dtype_code(a.dtype, "diag_scan")
+    out_code = dtype_code(h.dtype, "diag_scan")
+    if cfg is None:
+        nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, in_code)
+    else:
+        nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, D, *cfg)
+    ws = workspace(nbytes, a.device)
+    pre = prefix.data_ptr() if prefix is not None else None
+    stream = _stream_handle(a.device)
+    if cfg is None:
+        rc = lib.mogt_diag_scan_fwd(a.data_ptr(), b.data_ptr(), h.data_ptr(), pre, B, L, D,
+                                    in_code, out_code, ws.data_ptr(), ws.numel(), stream)
+    else:
+        rc = lib.mogt_diag_scan_fwd_cfg(a.data_ptr(), b.data_ptr(), h.data_ptr(), pre, B, L, D,
+                                        in_code, out_code, cfg[0], cfg[1], cfg[2],
+                                        ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "mogt_diag_scan_fwd")
+
+
+def _check_diag_inputs(a: torch.Tensor, b: torch.Tensor) -> None:
+    require_cuda("diag_scan", a, b)
+    if a.ndim != 3 or b.ndim != 3:
+        raise ValueError("a and b must be rank-3 tensors [B, L, D]")
+    if a.shape != b.shape:
+        raise ValueError("a and b must have the same shape [B, L, D]")
+    if a.dtype != b.dtype:
+        raise ValueError("a and b must have the same dtype")
+    dtype_code(a.dtype, "diag_scan")
+
+
+@torch.library.custom_op("mogt::diag_scan", mutates_args=())
+def _diag_scan_op(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    a = a.contiguous()
+    b = b.contiguous()
+    h = torch.empty(a.shape, dtype=out_dtype, device=a.device)
+    _diag_scan_launch(a, b, h, None)
+    return h
+
+
+@_diag_scan_op.register_fake
+def _(a, b, out_dtype):
+    return a.new_empty(a.shape, dtype=out_dtype)
+
+
+@torch.library.custom_op("mogt::diag_scan_prefix", mutates_args=())
+def _diag_scan_prefix_op(a: torch.Tensor, b: torch.Tensor,
+                         out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    a = a.contiguous()
+    b = b.contiguous()
+    h = torch.empty(a.shape, dtype=out_dtype, device=a.device)
+    pre = torch.empty(a.shape, dtype=out_dtype, device=a.device)
+    _diag_scan_launch(a, b, h, pre)
+    return pre, h
+
+
+@_diag_scan_prefix_op.register_fake
+def _(a, b, out_dtype):
+    return a.new_empty(a.shape, dtype=out_dtype), a.new_empty(a.shape, dtype=out_dtype)
+
+
+def diag_scan(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype | None = None,
+              return_prefix: bool = False):
+    """h_t = a_t * h_{t-1} + b_t (h_0 = 0) over ``[B, L, D]`` on the GPU.
+
+    fp32 state and arithmetic; ``out_dtype`` defaults to ``b.dtype`` (the
+    reference's ``output_dtype or V.dtype``, affine_scan.py:34).  With
+    ``return_prefix`` also returns ``prod_{s<=t} a_s`` first, like the
+    reference's ``(U_prefix, H)`` pair (affine_scan.py:57-62).
+    """
+    _check_diag_inputs(a, b)
+    out_dtype = out_dtype or b.dtype
+    dtype_code(out_dtype, "diag_scan")
+    if return_prefix:
+        return torch.ops.mogt.diag_scan_prefix(a, b, out_dtype)
+    return torch.ops.mogt.diag_scan(a, b, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# coupled_rank_scan: MOGT mixer scan with identity connection and rank gate
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("mogt::coupled_rank_scan", mutates_args=())
+def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: float,
+                          out_dtype: torch.dtype) -> torch.Tensor:
+    lib = _lib.load()
+    z = z.contiguous()
+    v = v.contiguous()
+    B, L, D = v.shape
+    C = D // rank
+    h = torch.empty(v.shape, dtype=out_dtype, device=v.device)
+    zc = dtype_code(z.dtype, "coupled_rank_scan")
+    vc = dtype_code(v.dtype, "coupled_rank_scan")
+    oc = dtype_code(out_dtype, "coupled_rank_scan")
+    nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, vc)
+    ws = workspace(nbytes, v.device)
+    rc = lib.mogt_coupled_rank_scan_fwd(z.data_ptr(), v.data_ptr(), h.data_ptr(), B, L, rank, C,
+                                        float(damping), zc, vc, oc, ws.data_ptr(), ws.numel(),
+                                        _stream_handle(v.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_fwd")
+    return h
+
+
+@_coupled_rank_scan_op.register_fake
+def _(z, v, rank, damping, out_dtype):
+    return v.new_empty(v.shape, dtype=out_dtype)
+
+
+def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,
+                      out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Fused gate + scan of the coupled write-forget MOGT mixer.
+
+    ``gate_logits`` is ``[B, L, r]`` (the pre-sigmoid output of
+    ``phi_value_gate``), ``v_raw`` is ``[B, L, r*c]`` (``phi_val`` output,
+    feature ``d = i*c + j``).  Returns ``H`` flattened to ``[B, L, r*c]`` with
+    ``H_t = damping*(1-g_t) * H_{t-1} + g_t * v_t`` per rank
+    (model_mogt.py:166-203, identity connection, coupled gate).
+    """
+    require_cuda("coupled_rank_scan", gate_logits, v_raw)
+    if gate_logits.ndim != 3 or v_raw.ndim != 3:
+        raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
+    B, L, r = gate_logits.shape
+    if v_raw.shape[:2] != (B, L) or v_raw.shape[2] % r != 0:
+        raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
+    return torch.ops.mogt.coupled_rank_scan(gate_logits, v_raw, r, float(damping), out_dtype)

@@ -1,0 +1,89 @@
+"""The C-ABI library loads without a GPU, exports every function declared in
+include/*.h, and rejects bad arguments before touching the device."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mogt_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(mogt_\w+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert names, "no declarations found in include/*.h"
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_python_binding_covers_header(lib):
+    assert declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.mogt_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_queries_are_host_only(lib):
+    n = lib.mogt_diag_scan_workspace_bytes(1, 32768, 768, _lib.MOGT_F32)
+    assert 256 < n < 64 << 20
+    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 4, 8, 4) <= n
+    assert lib.mogt_coupled_rank_scan_workspace_bytes(1, 1024, 16, 48, _lib.MOGT_BF16) > 256
+
+
+def test_argument_errors_without_device(lib):
+    # Validation happens on the host before any HIP call.
+    rc = lib.mogt_diag_scan_fwd(None, None, None, None, 1, 8, 8, 7, 0, None, 0, None)
+    assert rc == -1 and b"dtype" in lib.mogt_last_error()
+    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 3, 8, 4, None, 0, None)
+    assert rc == -1 and b"not compiled" in lib.mogt_last_error()
+    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 4, 8, 4, None, 0, None)
+    assert rc == -2 and b"workspace" in lib.mogt_last_error()
+    rc = lib.mogt_coupled_rank_scan_fwd(1, 1, 1, 1, 8, 0, 48, 1.0, 0, 0, 0, None, 0, None)
+    assert rc == -1
+    # zero-size problems are a no-op success
+    assert lib.mogt_diag_scan_fwd(None, None, None, None, 0, 8, 8, 0, 0, None, 0, None) == 0
+
+
+def test_check_maps_codes_to_python_errors(lib):
+    lib.mogt_diag_scan_fwd(None, None, None, None, 1, 8, 8, 7, 0, None, 0, None)
+    with pytest.raises(ValueError):
+        _lib.check(-1, "x")
+    with pytest.raises(_lib.MogtError):
+        _lib.check(-3, "x")
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+
+    import mogt_amd
+
+    a = torch.rand(1, 4, 8)
+    with pytest.raises(ValueError, match="CUDA"):
+        mogt_amd.diag_scan(a, a)
+    with pytest.raises(ValueError, match="CUDA"):
+        mogt_amd.coupled_rank_scan(torch.zeros(1, 4, 2), torch.zeros(1, 4, 8))
+
+
+def test_library_is_plain_c_abi():
+    """No torch symbols leak into the shared object's dynamic imports."""
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(_lib.library_path())],
+                         capture_output=True, text=True).stdout
+    assert "torch" not in out and "c10" not in out

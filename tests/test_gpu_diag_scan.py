@@ -1,0 +1,198 @@
+"""GPU parity of the single-pass diagonal scan and the coupled mixer scan
+against the CPU oracle on identical seeded inputs.
+
+Bars (normwise max relative error, float64): fp32 I/O <= 1e-4; bf16 I/O with
+fp32 state <= 2e-2.  Full-size (L = 32768) runs are checked against the oracle
+too (it takes < 1 s per case at D = 768) plus size-independent properties.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, rel_err, to_np
+from mogt_amd import synthetic
+from oracle import scan_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+# every compiled tile (vec, steps per thread, waves)
+TILES = [(1, 32, 4), (1, 16, 4), (2, 16, 4), (2, 8, 4), (4, 8, 4), (4, 16, 4), (4, 4, 4),
+         (1, 32, 8), (2, 16, 8), (4, 8, 8)]
+
+
+def _run_cfg(a, b, out_dtype, cfg, prefix=False):
+    from mogt_amd import ops
+
+    h = torch.empty(a.shape, dtype=out_dtype, device=a.device)
+    p = torch.empty(a.shape, dtype=out_dtype, device=a.device) if prefix else None
+    ops._diag_scan_launch(a.contiguous(), b.contiguous(), h, p, cfg)
+    return (p, h) if prefix else h
+
+
+def test_cfg1_fp32(gpu):
+    announce("diag cfg1 B=2 L=512 D=128 fp32")
+    import mogt_amd
+
+    a, b = synthetic.cfg1_inputs(seed=0)
+    ref = so.diag_scan(a, b)
+    h = mogt_amd.diag_scan(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    torch.cuda.synchronize()
+    assert h.dtype == torch.float32
+    assert rel_err(to_np(h), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_every_tile_fp32_ragged(gpu, tile):
+    """Ragged L (not a multiple of any chunk) and D a multiple of the vector."""
+    announce(f"diag tile {tile} B=3 L=1237 D=320")
+    a, b = synthetic.diag_inputs(3, 1237, 320, a_mean=2.0, b_std=1.0, seed=5)
+    ref = so.diag_scan(a, b)
+    P_ref = so.diag_scan(a, b, return_prefix=True)[0]
+    at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    p, h = _run_cfg(at, bt, torch.float32, tile, prefix=True)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(h), ref) <= FP32_TOL
+    assert rel_err(to_np(p), P_ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 4097])
+def test_edge_lengths(gpu, L):
+    announce(f"diag edge L={L}")
+    import mogt_amd
+
+    a, b = synthetic.diag_inputs(2, L, 40, a_mean=1.0, b_std=1.0, seed=L)
+    h = mogt_amd.diag_scan(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(h), so.diag_scan(a, b)) <= FP32_TOL
+
+
+def test_odd_feature_count_uses_scalar_tile(gpu):
+    announce("diag D=131 (odd)")
+    import mogt_amd
+
+    a, b = synthetic.diag_inputs(1, 777, 131, seed=2)
+    h = mogt_amd.diag_scan(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(h), so.diag_scan(a, b)) <= FP32_TOL
+
+
+def test_empty_input(gpu):
+    import mogt_amd
+
+    a = torch.empty(1, 0, 8, device=gpu)
+    assert mogt_amd.diag_scan(a, a).shape == (1, 0, 8)
+
+
+def test_special_cases_cumsum_and_identity(gpu):
+    """a = 1 -> cumsum(b) (long chains of unit decay through every chunk);
+    a = 0 -> h = b."""
+    announce("diag a=1 / a=0 L=20000 D=64")
+    import mogt_amd
+
+    g = synthetic.rng(3)
+    b = g.standard_normal((1, 20000, 64)).astype(np.float32)
+    bt = torch.from_numpy(b).to(gpu)
+    h1 = mogt_amd.diag_scan(torch.ones_like(bt), bt)
+    h0 = mogt_amd.diag_scan(torch.zeros_like(bt), bt)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(h1), np.cumsum(b.astype(np.float64), axis=1)) <= FP32_TOL
+    assert np.array_equal(to_np(h0), b)
+
+
+@pytest.mark.parametrize("L", [8192, 16384, 32768])
+def test_cfg2_fp32_full_size(gpu, L):
+    announce(f"diag cfg2 fp32 L={L}")
+    import mogt_amd
+
+    a, b = synthetic.cfg2_inputs(L, seed=1)
+    ref = so.diag_scan(a, b)
+    h = mogt_amd.diag_scan(torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(h), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("L", [8192, 32768])
+def test_cfg2_bf16_io_full_size(gpu, L):
+    announce(f"diag cfg2 bf16 L={L}")
+    import mogt_amd
+
+    a, b = synthetic.cfg2_inputs(L, seed=2)
+    at = torch.from_numpy(a).to(gpu).bfloat16()
+    bt = torch.from_numpy(b).to(gpu).bfloat16()
+    ref = so.diag_scan(to_np(at), to_np(bt))   # oracle sees the same bf16-rounded inputs
+    h = mogt_amd.diag_scan(at, bt)
+    torch.cuda.synchronize()
+    assert h.dtype == torch.bfloat16
+    assert rel_err(to_np(h), ref) <= BF16_TOL
+    hf = mogt_amd.diag_scan(at, bt, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(hf), ref) <= FP32_TOL   # fp32 state: only input rounding differs
+
+
+def test_repeated_launches_reuse_workspace(gpu):
+    """The workspace is only zeroed once; 50 back-to-back launches of different
+    shapes must all stay exact (epoch/ticket reset at the end of every launch)."""
+    announce("diag workspace reuse x50")
+    import mogt_amd
+
+    cases = []
+    for i, (L, D) in enumerate([(3000, 768), (515, 64), (8192, 256), (77, 1024)]):
+        a, b = synthetic.diag_inputs(1, L, D, seed=10 + i)
+        cases.append((torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu),
+                      so.diag_scan(a, b)))
+    outs = []
+    for it in range(50):
+        at, bt, ref = cases[it % len(cases)]
+        outs.append((mogt_amd.diag_scan(at, bt), ref))
+    torch.cuda.synchronize()
+    for h, ref in outs:
+        assert rel_err(to_np(h), ref) <= FP32_TOL
+
+
+def test_linearity_at_full_size(gpu):
+    """Size-independent property at L = 32768: scan(a, 2b1 - 3b2) = 2scan(a,b1) - 3scan(a,b2)."""
+    announce("diag linearity L=32768")
+    import mogt_amd
+
+    a, b1 = synthetic.cfg2_inputs(32768, seed=7)
+    _, b2 = synthetic.cfg2_inputs(32768, seed=8)
+    at = torch.from_numpy(a).to(gpu)
+    t1, t2 = torch.from_numpy(b1).to(gpu), torch.from_numpy(b2).to(gpu)
+    lhs = mogt_amd.diag_scan(at, 2 * t1 - 3 * t2)
+    rhs = 2 * mogt_amd.diag_scan(at, t1) - 3 * mogt_amd.diag_scan(at, t2)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(lhs), to_np(rhs).astype(np.float64)) <= FP32_TOL
+
+
+# --------------------------------------------------------------------------- coupled mixer scan
+@pytest.mark.parametrize("L,r,c", [(300, 4, 6), (4096, 16, 48), (32768, 16, 48)])
+@pytest.mark.parametrize("vdt", ["fp32", "bf16"])
+def test_coupled_rank_scan(gpu, L, r, c, vdt):
+    announce(f"coupled L={L} r={r} c={c} v={vdt}")
+    import mogt_amd
+
+    z, v = synthetic.coupled_inputs(1, L, r, c, seed=L + r)
+    zt = torch.from_numpy(z).to(gpu)
+    vt = torch.from_numpy(v).to(gpu)
+    if vdt == "bf16":
+        vt = vt.bfloat16()
+    ref = so.coupled_rank_scan(z, to_np(vt), r, damping=0.999, v_is_bf16=(vdt == "bf16"))
+    h = mogt_amd.coupled_rank_scan(zt, vt, damping=0.999)
+    torch.cuda.synchronize()
+    assert h.shape == (1, L, r * c) and h.dtype == torch.float32
+    # bf16 V: the product V*g is rounded to bf16 (model_mogt.py:180), so a
+    # last-bit difference of the fp32 sigmoid can flip one rounding -> bf16 bar.
+    tol = FP32_TOL if vdt == "fp32" else BF16_TOL
+    err = np.abs(to_np(h).astype(np.float64) - ref) / np.max(np.abs(ref))
+    assert float(err.max()) <= tol
+    assert float(np.median(err)) <= 1e-6   # the bulk is exact to fp32 accumulation
+
+
+def test_zz_no_lookback_wait_gave_up(gpu):
+    """Every bounded wait of every launch above completed normally."""
+    from mogt_amd import ops
+
+    assert ops.workspace_faults() == 0
