@@ -252,13 +252,16 @@ def main():
         log(f"calibration copy of {n} bytes done (x5)")
 
     if args.sweep:
-        tiles = [(1, 32, 4), (1, 16, 4), (2, 16, 4), (2, 8, 4), (4, 8, 4), (4, 16, 4), (4, 4, 4),
-                 (1, 32, 8), (2, 16, 8), (4, 8, 8)]
-        for dt in (torch.float32, torch.bfloat16):
-            for t in tiles:
-                r = measure_diag(torch, lib, ops, 32768, dt, dt, args.steps, args.warmup, tile=t)
-                log(f"sweep {dt} tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
-                    f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+        tiles = [(1, 32, 16), (1, 64, 16), (1, 48, 16), (1, 40, 8), (1, 32, 8), (1, 16, 8),
+                 (2, 32, 16), (2, 16, 8), (4, 16, 8), (4, 8, 8)]
+        for L in (8192, 16384, 32768):
+            for dt in (torch.float32, torch.bfloat16):
+                for t in tiles:
+                    if dt == torch.float32 and t[1] > 40:
+                        continue   # fp32 tiles beyond 40 steps spill registers
+                    r = measure_diag(torch, lib, ops, L, dt, dt, args.steps, args.warmup, tile=t)
+                    log(f"sweep L={L} {dt} tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
+                        f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
 
     log("headline: diag scan fp32 B=1 D=768 L=32768")
     head = measure_diag(torch, lib, ops, 32768, torch.float32, torch.float32, args.steps,

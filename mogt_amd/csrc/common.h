@@ -74,20 +74,28 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 // ---------------------------------------------------------------------------
 // Decoupled look-back workspace protocol (shared by every single-pass scan).
 //
-//   hdr[0]  ticket counter: work-groups take chunk ids in the order they start,
-//           so a chunk only ever waits on chunks that are already resident.
-//   hdr[1]  done counter: the last work-group to finish resets hdr[0..1] and
-//           advances the epoch, so the buffer is reusable by the next launch
-//           without a memset (also inside a captured HIP graph).
-//   hdr[2]  epoch (30 bits).
+// Chunk ids are blockIdx.x: work-groups are dispatched in increasing id order,
+// so the lowest unfinished chunk is always resident and never waits on an
+// unstarted one.  (A global atomic ticket would make this independent of the
+// dispatcher, but one same-address atomic per work-group costs more than the
+// whole scan on an 8-XCD part; every wait below is bounded instead.)
+//
+//   hdr[2]  epoch (30 bits), read once by every work-group.
 //   hdr[3]  count of bounded waits that gave up (must stay 0; a non-zero value
 //           means the protocol was violated and the output is not valid).
 //
 // Every published value is a 64-bit word {tag:32 | f32 bits:32} written with a
 // single agent-scope atomic store, tag = epoch << 2 | status.  A reader accepts
 // a word only if its tag matches, so payloads need no release/acquire fences
-// (an agent-scope release fence on gfx950 writes back the whole L2).  Per-chunk
-// status flags are hints that tell the look-back how far back to read.
+// (an agent-scope release fence on gfx950 writes back the whole L2).  Each
+// chunk also publishes one status flag word (same tag) that tells the
+// look-back how far back to read.
+//
+// Reuse without clearing: the last work-group waits until every chunk flag
+// carries the current epoch (each work-group writes its flag right after it
+// read the epoch), then advances the epoch.  Stale words of older launches can
+// never match a newer tag, so the buffer needs zero-filling only once, and the
+// scheme holds inside a captured HIP graph.
 // ---------------------------------------------------------------------------
 constexpr uint32_t ST_AGG = 1u;   // chunk aggregate published
 constexpr uint32_t ST_INC = 2u;   // inclusive prefix published
@@ -141,26 +149,79 @@ __device__ __forceinline__ float wait_word(const uint64_t* p, uint32_t tag, uint
     return word_val(w);
 }
 
-// Work-group start: take a ticket and read the epoch (thread 0, broadcast).
-__device__ __forceinline__ void ws_begin(uint32_t* hdr, int* s_ticket, uint32_t* s_epoch) {
-    if (threadIdx.x == 0) {
-        *s_ticket = static_cast<int>(fetch_add_relaxed(&hdr[0], 1u));
-        *s_epoch = ld_relaxed(&hdr[2]);
-    }
+// Work-group start: read the launch's epoch (thread 0, broadcast via LDS).
+__device__ __forceinline__ uint32_t ws_epoch(uint32_t* hdr, uint32_t* s_epoch) {
+    if (threadIdx.x == 0) *s_epoch = ld_relaxed(&hdr[2]);
     __syncthreads();
+    return *s_epoch;
 }
 
-// Work-group end: the last one resets the ticket/done counters and advances
-// the epoch for the next launch.
-__device__ __forceinline__ void ws_end(uint32_t* hdr, uint32_t epoch) {
-    if (threadIdx.x == 0) {
-        uint32_t total = gridDim.x * gridDim.y * gridDim.z;
-        uint32_t old = fetch_add_relaxed(&hdr[1], 1u);
-        if (old == total - 1) {
-            st_relaxed(&hdr[0], 0u);
-            st_relaxed(&hdr[1], 0u);
-            st_relaxed(&hdr[2], (epoch + 1u) & 0x3fffffffu);
+// Last work-group of the grid: once all n_flags chunk flags carry `epoch`,
+// advance the epoch for the next launch.
+__device__ __forceinline__ void ws_finish(uint32_t* hdr, const uint32_t* flags, int64_t n_flags,
+                                          uint32_t epoch) {
+    if (blockIdx.x != gridDim.x - 1) return;
+    for (int64_t i = threadIdx.x; i < n_flags; i += blockDim.x) {
+        uint32_t n = 0;
+        while ((ld_relaxed(&flags[i]) >> 2) != epoch) {
+            if (++n > MAX_SPIN) {
+                note_timeout(hdr);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) st_relaxed(&hdr[2], (epoch + 1u) & 0x3fffffffu);
+}
+
+// Streaming (non-temporal) vector loads/stores of N consecutive elements: the
+// scan touches every byte exactly once, so keep it out of the caches.
+template <int BYTES> struct WordVec;
+template <> struct WordVec<4> { typedef uint32_t type; };
+template <> struct WordVec<8> { typedef uint32_t type __attribute__((ext_vector_type(2))); };
+template <> struct WordVec<16> { typedef uint32_t type __attribute__((ext_vector_type(4))); };
+
+template <typename T, int N>
+__device__ __forceinline__ void load_stream(const T* __restrict__ p, float (&out)[N]) {
+    constexpr int BYTES = static_cast<int>(sizeof(T)) * N;
+    if constexpr (BYTES == 2) {
+        out[0] = IO<T>::ld(__builtin_nontemporal_load(p));
+    } else {
+        typedef typename WordVec<BYTES>::type W;
+        union { W w; T v[N]; } u;
+        u.w = __builtin_nontemporal_load(reinterpret_cast<const W*>(p));
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = IO<T>::ld(u.v[i]);
+    }
+}
+
+// Raw 16-bit patterns of N consecutive bf16 values (zero-extended).
+template <int N>
+__device__ __forceinline__ void load_bits16(const bf16_t* __restrict__ p, uint32_t (&out)[N]) {
+    constexpr int BYTES = 2 * N;
+    if constexpr (BYTES == 2) {
+        out[0] = __builtin_nontemporal_load(p);
+    } else {
+        typedef typename WordVec<BYTES>::type W;
+        union { W w; bf16_t v[N]; } u;
+        u.w = __builtin_nontemporal_load(reinterpret_cast<const W*>(p));
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = u.v[i];
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_stream(T* __restrict__ p, const float (&in)[N]) {
+    constexpr int BYTES = static_cast<int>(sizeof(T)) * N;
+    if constexpr (BYTES == 2) {
+        __builtin_nontemporal_store(IO<T>::st(in[0]), p);
+    } else {
+        typedef typename WordVec<BYTES>::type W;
+        union { W w; T v[N]; } u;
+#pragma unroll
+        for (int i = 0; i < N; ++i) u.v[i] = IO<T>::st(in[i]);
+        __builtin_nontemporal_store(u.w, reinterpret_cast<W*>(p));
     }
 }
 

@@ -14,10 +14,13 @@
 //   level 2  wave summaries (prod a, h_end) go through LDS; each wave folds the
 //            summaries of the waves before it to get its in-chunk carry.
 //   level 3  chunks of one feature group are chained with a decoupled look-back
-//            (tagged 64-bit words, see common.h): publish the chunk aggregate,
+//            (tagged 64-bit words, see common.h; chunk id = blockIdx.x, chunk-
+//            major over the feature groups): publish the chunk aggregate,
 //            fold predecessors' aggregates until an inclusive prefix is found,
 //            publish the inclusive prefix, then apply the carry in registers and
 //            write h once.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mogt {
@@ -47,19 +50,19 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int T = WT * S;
     static_assert(FW <= NT, "look-back needs one thread per feature of the group");
 
-    __shared__ int s_ticket;
     __shared__ uint32_t s_epoch;
     __shared__ float s_sumA[WT][FW];
     __shared__ float s_sumH[WT][FW];
     __shared__ float s_inA[FW];
     __shared__ float s_inH[FW];
+    __shared__ float s_partA[NT];
+    __shared__ float s_partH[NT];
     __shared__ int s_nfold, s_found;
 
-    ws_begin(p.hdr, &s_ticket, &s_epoch);
-    const int ticket = s_ticket;
-    const uint32_t epoch = s_epoch;
-    const int chunk = ticket / p.G;
-    const int g = ticket - chunk * p.G;
+    const uint32_t epoch = ws_epoch(p.hdr, &s_epoch);
+    const int blk = blockIdx.x;
+    const int chunk = blk / p.G;
+    const int g = blk - chunk * p.G;
     const int bi = g / p.n_fg;
     const int fg = g - bi * p.n_fg;
 
@@ -75,7 +78,13 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     const int64_t rowoff0 = (row0 + t0) * p.D + fbase;
 
     // ---- load (all loads issued before any use) -------------------------
-    float ra[S][VEC], rb[S][VEC];
+    // The raw per-step inputs stay in registers until the carry is known; the
+    // outputs are then produced by re-running the recurrence from the carry
+    // (same arithmetic order as the sequential reference).  bf16 inputs are
+    // kept as packed bit pairs (one VGPR per step), halving register use.
+    constexpr bool PACKED = !COUPLED && std::is_same<TIn, bf16_t>::value;
+    float ra[PACKED ? 1 : S][VEC], rb[PACKED ? 1 : S][VEC];
+    uint32_t pk[PACKED ? S : 1][VEC];
     {
         const TIn* pa = static_cast<const TIn*>(COUPLED ? p.b : p.a) + rowoff0;
         const TIn* pb = static_cast<const TIn*>(p.b) + rowoff0;
@@ -88,7 +97,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 if constexpr (COUPLED) {
                     const float zz = IO<TZ>::ld(pz[gi]);
                     float vv[VEC];
-                    load_vec<TIn, VEC>(pb + flane, vv);
+                    load_stream<TIn, VEC>(pb + flane, vv);
                     const float gate = sigmoidf_(zz);
                     // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)
                     const float gate_io = IO<TIn>::ld(IO<TIn>::st(gate));
@@ -97,33 +106,58 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                         ra[s][v] = p.damping * (1.0f - gate);
                         rb[s][v] = IO<TIn>::ld(IO<TIn>::st(vv[v] * gate_io));
                     }
+                } else if constexpr (PACKED) {
+                    uint32_t ab[VEC], bb[VEC];
+                    load_bits16<VEC>(pa + flane, ab);
+                    load_bits16<VEC>(pb + flane, bb);
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) pk[s][v] = ab[v] | (bb[v] << 16);
                 } else {
-                    load_vec<TIn, VEC>(pa + flane, ra[s]);
-                    load_vec<TIn, VEC>(pb + flane, rb[s]);
+                    load_stream<TIn, VEC>(pa + flane, ra[s]);
+                    load_stream<TIn, VEC>(pb + flane, rb[s]);
                 }
             } else {
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) { ra[s][v] = 1.0f; rb[s][v] = 0.0f; }
+                for (int v = 0; v < VEC; ++v) {
+                    if constexpr (PACKED) pk[s][v] = 0x3f80u;   // a = 1.0, b = 0.0
+                    else { ra[s][v] = 1.0f; rb[s][v] = 0.0f; }
+                }
             }
             pa += p.D;
             pb += p.D;
             if constexpr (COUPLED) pz += p.R;
         }
     }
+    auto step_a = [&](int s, int v) -> float {
+        if constexpr (PACKED) return __uint_as_float(pk[s][v] << 16);
+        else return ra[s][v];
+    };
+    auto step_b = [&](int s, int v) -> float {
+        if constexpr (PACKED) return __uint_as_float(pk[s][v] & 0xffff0000u);
+        else return rb[s][v];
+    };
 
-    // ---- level 1: serial in-lane scan; ra <- prod a, rb <- h -------------
+    // ---- level 1: in-lane summary (prod a, h_end) of the S steps ---------
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
         float A = 1.0f, hh = 0.0f;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            hh = fmaf(ra[s][v], hh, rb[s][v]);
-            A *= ra[s][v];
-            ra[s][v] = A;
-            rb[s][v] = hh;
+            const float av = step_a(s, v);
+            hh = fmaf(av, hh, step_b(s, v));
+            A *= av;
         }
         s_sumA[wave][lane * VEC + v] = A;
         s_sumH[wave][lane * VEC + v] = hh;
+    }
+    if constexpr (PACKED) {
+        // Keep only the packed words live across the look-back: an empty asm
+        // that "rewrites" them stops the compiler from holding the unpacked
+        // floats of the first pass until the second.
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) asm volatile("" : "+v"(pk[s][v]));
     }
     __syncthreads();
 
@@ -175,7 +209,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     if (tid == 0) st_relaxed(&p.flags[gbase + chunk], make_tag(epoch, chunk == 0 ? ST_INC : ST_AGG));
 
     if (chunk > 0) {
-        float cA = 1.0f, cH = 0.0f;   // composite of folded aggregates (feature tid)
+        float cA = 1.0f, cH = 0.0f;   // composite of folded aggregates (threads tid < FW)
         int p_hi = chunk - 1;
         while (true) {
             if (wave == 0) {
@@ -220,38 +254,78 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
             __syncthreads();
             const int nf = s_nfold;
             const int found = s_found;
-            if (tid < FW) {
-                // Fold aggregates of chunks p_hi, p_hi-1, ..., p_hi-nf+1 (newest first).
-                constexpr int BATCH = 8;
-                for (int q0 = 0; q0 < nf; q0 += BATCH) {
-                    float bA[BATCH], bH[BATCH];
+            {
+                // Fold the aggregates of chunks p_hi, ..., p_hi-nf+1 (newest first) and,
+                // if found, the inclusive prefix of chunk p_hi-nf.  The window is split
+                // into NR contiguous slices folded concurrently (feature f = tid % FW,
+                // slice r = tid / FW), each issuing all its loads before the first use,
+                // so one window costs about one memory round trip.
+                constexpr int NR = NT / FW;
+                constexpr int BATCH = 4;
+                const int f = tid % FW;
+                const int r = tid / FW;
+                const int per = (nf + NR - 1) / NR;
+                const int q_lo = r * per;
+                const int q_hi = min(nf, q_lo + per);
+                const int64_t iidx = (gbase + p_hi - nf) * FW + f;
+                uint64_t iwA = 0, iwH = 0;
+                if (found && r == 0) {
+                    iwA = ld_relaxed(&incA[iidx]);
+                    iwH = ld_relaxed(&incH[iidx]);
+                }
+                float rA = 1.0f, rH = 0.0f;
+                for (int q0 = q_lo; q0 < q_hi; q0 += BATCH) {
+                    uint64_t wA[BATCH], wH[BATCH];
 #pragma unroll
                     for (int q = 0; q < BATCH; ++q) {
-                        if (q0 + q < nf) {
-                            const int64_t idx = (gbase + p_hi - q0 - q) * FW + tid;
-                            bA[q] = wait_word(&aggA[idx], tagA, p.hdr);
-                            bH[q] = wait_word(&aggH[idx], tagA, p.hdr);
+                        if (q0 + q < q_hi) {
+                            const int64_t idx = (gbase + p_hi - q0 - q) * FW + f;
+                            wA[q] = ld_relaxed(&aggA[idx]);
+                            wH[q] = ld_relaxed(&aggH[idx]);
                         }
                     }
 #pragma unroll
                     for (int q = 0; q < BATCH; ++q) {
-                        if (q0 + q < nf) {
-                            cH = fmaf(cA, bH[q], cH);
-                            cA *= bA[q];
+                        if (q0 + q < q_hi) {
+                            const int64_t idx = (gbase + p_hi - q0 - q) * FW + f;
+                            const float A = word_tag(wA[q]) == tagA ? word_val(wA[q])
+                                                                    : wait_word(&aggA[idx], tagA, p.hdr);
+                            const float H = word_tag(wH[q]) == tagA ? word_val(wH[q])
+                                                                    : wait_word(&aggH[idx], tagA, p.hdr);
+                            rH = fmaf(rA, H, rH);
+                            rA *= A;
                         }
                     }
                 }
-                if (found) {
-                    const int64_t idx = (gbase + p_hi - nf) * FW + tid;
-                    const float iA = wait_word(&incA[idx], tagI, p.hdr);
-                    const float iH = wait_word(&incH[idx], tagI, p.hdr);
-                    const float inH = fmaf(cA, iH, cH);
-                    const float inA = cA * iA;
-                    s_inA[tid] = inA;
-                    s_inH[tid] = inH;
-                    const int64_t me = (gbase + chunk) * FW + tid;
-                    st_relaxed(&incA[me], pack_word(gA * inA, tagI));
-                    st_relaxed(&incH[me], pack_word(fmaf(gA, inH, gH), tagI));
+                if constexpr (NR > 1) {
+                    s_partA[tid] = rA;
+                    s_partH[tid] = rH;
+                    __syncthreads();
+                }
+                if (r == 0) {
+                    if constexpr (NR > 1) {
+#pragma unroll
+                        for (int rr = 0; rr < NR; ++rr) {
+                            cH = fmaf(cA, s_partH[rr * FW + f], cH);
+                            cA *= s_partA[rr * FW + f];
+                        }
+                    } else {
+                        cH = fmaf(cA, rH, cH);
+                        cA *= rA;
+                    }
+                    if (found) {
+                        const float iA = word_tag(iwA) == tagI ? word_val(iwA)
+                                                               : wait_word(&incA[iidx], tagI, p.hdr);
+                        const float iH = word_tag(iwH) == tagI ? word_val(iwH)
+                                                               : wait_word(&incH[iidx], tagI, p.hdr);
+                        const float inH = fmaf(cA, iH, cH);
+                        const float inA = cA * iA;
+                        s_inA[f] = inA;
+                        s_inH[f] = inH;
+                        const int64_t me = (gbase + chunk) * FW + f;
+                        st_relaxed(&incA[me], pack_word(gA * inA, tagI));
+                        st_relaxed(&incH[me], pack_word(fmaf(gA, inH, gH), tagI));
+                    }
                 }
             }
             if (found) break;
@@ -276,17 +350,25 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     {
         TOut* ph = static_cast<TOut*>(p.h) + rowoff0;
         TOut* pp = PREFIX ? static_cast<TOut*>(p.aprefix) + rowoff0 : nullptr;
+        float hh[VEC], Ap[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) { hh[v] = stH[v]; Ap[v] = stA[v]; }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            if (fvalid && t0 + s < p.L) {
-                float o[VEC];
+            float o[VEC];
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) o[v] = fmaf(ra[s][v], stH[v], rb[s][v]);
-                store_vec<TOut, VEC>(ph + flane, o);
+            for (int v = 0; v < VEC; ++v) {
+                const float av = step_a(s, v);
+                hh[v] = fmaf(av, hh[v], step_b(s, v));
+                if constexpr (PREFIX) Ap[v] *= av;
+                o[v] = hh[v];
+            }
+            if (fvalid && t0 + s < p.L) {
+                store_stream<TOut, VEC>(ph + flane, o);
                 if constexpr (PREFIX) {
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v) o[v] = ra[s][v] * stA[v];
-                    store_vec<TOut, VEC>(pp + flane, o);
+                    for (int v = 0; v < VEC; ++v) o[v] = Ap[v];
+                    store_stream<TOut, VEC>(pp + flane, o);
                 }
             }
             ph += p.D;
@@ -294,7 +376,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         }
     }
 
-    ws_end(p.hdr, epoch);
+    ws_finish(p.hdr, p.flags, static_cast<int64_t>(p.G) * p.n_ch, epoch);
 }
 
 // ---------------------------------------------------------------------------
@@ -304,10 +386,10 @@ namespace {
 
 struct TileCfg { int vec, steps, waves; };
 
-// Tile configurations compiled into the library.
+// Tile configurations compiled into the library (vec, steps, waves).
 constexpr TileCfg kCfgs[] = {
-    {1, 32, 4}, {1, 16, 4}, {2, 16, 4}, {2, 8, 4}, {4, 8, 4}, {4, 16, 4}, {4, 4, 4},
-    {1, 32, 8}, {2, 16, 8}, {4, 8, 8},
+    {1, 32, 16}, {1, 64, 16}, {1, 48, 16}, {1, 40, 8}, {1, 32, 8}, {1, 16, 8},
+    {2, 32, 16}, {2, 16, 8}, {4, 16, 8}, {4, 8, 8},
 };
 
 bool cfg_known(int vec, int steps, int waves) {
@@ -347,37 +429,44 @@ int launch_cfg(const DiagParams& prm, int grid, int vec, int steps, int waves, h
 #define MOGT_DIAG_CASE(V_, S_, W_)                                                     \
     if (vec == V_ && steps == S_ && waves == W_)                                        \
         return launch_one<TIn, TZ, TOut, V_, S_, W_, PREFIX, COUPLED>(prm, grid, st);
-    MOGT_DIAG_CASE(1, 32, 4)
-    MOGT_DIAG_CASE(1, 16, 4)
-    MOGT_DIAG_CASE(2, 16, 4)
-    MOGT_DIAG_CASE(2, 8, 4)
-    MOGT_DIAG_CASE(4, 8, 4)
-    MOGT_DIAG_CASE(4, 16, 4)
-    MOGT_DIAG_CASE(4, 4, 4)
+    MOGT_DIAG_CASE(1, 32, 16)
+    MOGT_DIAG_CASE(1, 64, 16)
+    MOGT_DIAG_CASE(1, 48, 16)
+    MOGT_DIAG_CASE(1, 40, 8)
     MOGT_DIAG_CASE(1, 32, 8)
+    MOGT_DIAG_CASE(1, 16, 8)
+    MOGT_DIAG_CASE(2, 32, 16)
     MOGT_DIAG_CASE(2, 16, 8)
+    MOGT_DIAG_CASE(4, 16, 8)
     MOGT_DIAG_CASE(4, 8, 8)
 #undef MOGT_DIAG_CASE
     return set_error(MOGT_E_INVALID, "diag scan: tile (vec=%d, steps=%d, waves=%d) not compiled", vec,
                      steps, waves);
 }
 
-// Default tile choice: the widest vector the feature count and dtype allow.
-TileCfg default_cfg(int64_t D, int in_dtype, int64_t align_elems) {
-    (void)in_dtype;
-    if (D % 4 == 0 && align_elems % 4 == 0) return {4, 8, 4};
-    if (D % 2 == 0 && align_elems % 2 == 0) return {2, 16, 4};
-    return {1, 32, 4};
+// Default tile (measured on MI355X, D = 768, L = 8k..32k): fp32 I/O runs best
+// with one feature per lane (256 B coalesced rows per wave) and 512-step chunks
+// (16 waves x 32 steps), which keeps look-back chains at L/512 links; bf16
+// I/O with two features per lane (4-byte loads, 256 B rows).  Small problems
+// fall back to 128-step chunks so the grid still fills the GPU.
+int64_t n_groups(int64_t B, int64_t L, int64_t D, const TileCfg& c) {
+    const int64_t FW = 64 * c.vec;
+    const int64_t T = static_cast<int64_t>(c.steps) * c.waves;
+    return B * ((D + FW - 1) / FW) * ((L + T - 1) / T);
+}
+
+TileCfg default_cfg(int64_t B, int64_t L, int64_t D, bool bf16_in, bool vec2_aligned) {
+    if (bf16_in && D % 2 == 0 && vec2_aligned) {
+        const TileCfg big{2, 32, 16};
+        if (n_groups(B, L, D, big) >= 192) return big;
+        return {2, 16, 8};
+    }
+    const TileCfg big{1, 32, 16};
+    if (n_groups(B, L, D, big) >= 128) return big;
+    return {1, 16, 8};
 }
 
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
-
-int64_t ptr_align_elems(const void* p, size_t esize) {
-    const uintptr_t u = reinterpret_cast<uintptr_t>(p);
-    int64_t e = 1;
-    while (e < 4 && (u % (esize * e * 2)) == 0) e *= 2;
-    return e;
-}
 
 int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, int64_t L,
              int64_t D, int R, int C, float damping, int in_dtype, int z_dtype, int out_dtype,
@@ -440,8 +529,6 @@ int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, in
     return set_error(MOGT_E_INVALID, "unsupported dtype combination");
 }
 
-size_t esize(int dt) { return dt == MOGT_BF16 ? 2 : 4; }
-
 }  // namespace
 }  // namespace mogt
 
@@ -457,15 +544,12 @@ extern "C" size_t mogt_diag_scan_workspace_bytes_cfg(int64_t batch, int64_t leng
 
 extern "C" size_t mogt_diag_scan_workspace_bytes(int64_t batch, int64_t length, int64_t features,
                                                  int in_dtype) {
-    // Sized for the widest default tile any pointer alignment can select.
-    size_t best = 0;
-    for (int v : {1, 2, 4}) {
-        TileCfg c = default_cfg(features, in_dtype, v);
-        size_t s = mogt_diag_scan_workspace_bytes_cfg(batch, length, features, c.vec, c.steps,
-                                                      c.waves);
-        if (s > best) best = s;
-    }
-    return best;
+    // Largest requirement over the tiles the entry point may pick.
+    const TileCfg a = default_cfg(batch, length, features, in_dtype == MOGT_BF16, true);
+    const TileCfg b = default_cfg(batch, length, features, in_dtype == MOGT_BF16, false);
+    const size_t sa = mogt_diag_scan_workspace_bytes_cfg(batch, length, features, a.vec, a.steps, a.waves);
+    const size_t sb = mogt_diag_scan_workspace_bytes_cfg(batch, length, features, b.vec, b.steps, b.waves);
+    return sa > sb ? sa : sb;
 }
 
 extern "C" int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix,
@@ -484,14 +568,14 @@ extern "C" int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a
         clear_error();
         return set_error(MOGT_E_INVALID, "unsupported dtype code");
     }
-    int64_t al = 4;
-    for (const void* ptr : {a, b, static_cast<const void*>(h), static_cast<const void*>(a_prefix)}) {
-        if (!ptr) continue;
-        const size_t es = (ptr == a || ptr == b) ? esize(in_dtype) : esize(out_dtype);
-        const int64_t e = ptr_align_elems(ptr, es);
-        if (e < al) al = e;
-    }
-    const TileCfg c = default_cfg(features, in_dtype, al);
+    // Two-feature vectors need every pointer aligned to two elements.
+    auto aligned = [](const void* ptr, uintptr_t n) {
+        return ptr == nullptr || reinterpret_cast<uintptr_t>(ptr) % n == 0;
+    };
+    const uintptr_t in2 = in_dtype == MOGT_BF16 ? 4 : 8;
+    const uintptr_t out2 = out_dtype == MOGT_BF16 ? 4 : 8;
+    const bool al2 = aligned(a, in2) && aligned(b, in2) && aligned(h, out2) && aligned(a_prefix, out2);
+    const TileCfg c = default_cfg(batch, length, features, in_dtype == MOGT_BF16, al2);
     return run_scan(a, b, h, a_prefix, batch, length, features, 1, 1, 1.0f, in_dtype, MOGT_F32,
                     out_dtype, false, c.vec, c.steps, c.waves, workspace, workspace_bytes, stream);
 }
@@ -499,7 +583,11 @@ extern "C" int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a
 extern "C" size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t length,
                                                          int64_t rank, int64_t channels,
                                                          int v_dtype) {
-    return mogt_diag_scan_workspace_bytes(batch, length, rank * channels, v_dtype);
+    (void)v_dtype;
+    if (batch <= 0 || length <= 0 || rank <= 0 || channels <= 0) return WS_HDR_BYTES;
+    const TileCfg c = default_cfg(batch, length, rank * channels, false, false);
+    return mogt_diag_scan_workspace_bytes_cfg(batch, length, rank * channels, c.vec, c.steps,
+                                              c.waves);
 }
 
 extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h, int64_t batch,
@@ -512,16 +600,7 @@ extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
     if (!dtype_ok(z_dtype) || !dtype_ok(v_dtype) || !dtype_ok(out_dtype))
         return set_error(MOGT_E_INVALID, "unsupported dtype code");
     const int64_t D = rank * channels;
-    int64_t al = 4;
-    for (const void* ptr : {v, static_cast<const void*>(h)}) {
-        if (!ptr) continue;
-        const size_t es = (ptr == v) ? esize(v_dtype) : esize(out_dtype);
-        const int64_t e = ptr_align_elems(ptr, es);
-        if (e < al) al = e;
-    }
-    if (channels % 4 != 0) al = al < 2 ? al : 2;
-    if (channels % 2 != 0) al = 1;
-    const TileCfg c = default_cfg(D, v_dtype, al);
+    const TileCfg c = default_cfg(batch, length, D, false, false);
     return run_scan(z, v, h, nullptr, batch, length, D, static_cast<int>(rank),
                     static_cast<int>(channels), damping, v_dtype, z_dtype, out_dtype, true, c.vec,
                     c.steps, c.waves, workspace, workspace_bytes, stream);

@@ -42,7 +42,7 @@ def test_abi_version(lib):
 def test_workspace_queries_are_host_only(lib):
     n = lib.mogt_diag_scan_workspace_bytes(1, 32768, 768, _lib.MOGT_F32)
     assert 256 < n < 64 << 20
-    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 4, 8, 4) <= n
+    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 1, 32, 16) == n
     assert lib.mogt_coupled_rank_scan_workspace_bytes(1, 1024, 16, 48, _lib.MOGT_BF16) > 256
 
 
@@ -52,7 +52,7 @@ def test_argument_errors_without_device(lib):
     assert rc == -1 and b"dtype" in lib.mogt_last_error()
     rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 3, 8, 4, None, 0, None)
     assert rc == -1 and b"not compiled" in lib.mogt_last_error()
-    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 4, 8, 4, None, 0, None)
+    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 4, 8, 8, None, 0, None)
     assert rc == -2 and b"workspace" in lib.mogt_last_error()
     rc = lib.mogt_coupled_rank_scan_fwd(1, 1, 1, 1, 8, 0, 48, 1.0, 0, 0, 0, None, 0, None)
     assert rc == -1

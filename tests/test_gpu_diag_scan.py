@@ -19,8 +19,8 @@ FP32_TOL = 1e-4
 BF16_TOL = 2e-2
 
 # every compiled tile (vec, steps per thread, waves)
-TILES = [(1, 32, 4), (1, 16, 4), (2, 16, 4), (2, 8, 4), (4, 8, 4), (4, 16, 4), (4, 4, 4),
-         (1, 32, 8), (2, 16, 8), (4, 8, 8)]
+TILES = [(1, 32, 16), (1, 64, 16), (1, 48, 16), (1, 40, 8), (1, 32, 8), (1, 16, 8),
+         (2, 32, 16), (2, 16, 8), (4, 16, 8), (4, 8, 8)]
 
 
 def _run_cfg(a, b, out_dtype, cfg, prefix=False):
@@ -45,13 +45,17 @@ def test_cfg1_fp32(gpu):
 
 
 @pytest.mark.parametrize("tile", TILES)
-def test_every_tile_fp32_ragged(gpu, tile):
-    """Ragged L (not a multiple of any chunk) and D a multiple of the vector."""
-    announce(f"diag tile {tile} B=3 L=1237 D=320")
-    a, b = synthetic.diag_inputs(3, 1237, 320, a_mean=2.0, b_std=1.0, seed=5)
-    ref = so.diag_scan(a, b)
-    P_ref = so.diag_scan(a, b, return_prefix=True)[0]
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_every_tile_ragged(gpu, tile, dt):
+    """Ragged L (not a multiple of any chunk), several chunks per chain, D a
+    multiple of the vector but not of the feature-group width; with prefix."""
+    announce(f"diag tile {tile} {dt} B=3 L=4237 D=320")
+    a, b = synthetic.diag_inputs(3, 4237, 320, a_mean=2.0, b_std=1.0, seed=5)
     at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    if dt == "bf16":
+        at, bt = at.bfloat16(), bt.bfloat16()
+        a, b = to_np(at), to_np(bt)
+    P_ref, ref = so.diag_scan(a, b, return_prefix=True)
     p, h = _run_cfg(at, bt, torch.float32, tile, prefix=True)
     torch.cuda.synchronize()
     assert rel_err(to_np(h), ref) <= FP32_TOL
