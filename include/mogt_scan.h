@@ -85,6 +85,41 @@ int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                float damping, int z_dtype, int v_dtype, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Dense affine scan  H_t = U_t H_{t-1} + V_t,  H_0 = 0  (R <= 32, any C).
+ *
+ * Replaces the forward of triton_affine_scan_hybrid / its
+ * _triton_affine_scan_hybrid_forward (triton_scan.py:232-311, :429-477) and
+ * the reference scans affine_scan_sequential / _doubling / _block_reference
+ * (affine_scan.py:14-278), without the R == 16 restriction (triton_scan.py:200).
+ * U: [B, L, R, R] fp32 (the reference up-casts U to fp32, triton_scan.py:203);
+ * V: [B, L, R, C] fp32 or bf16; H: [B, L, R, C] in out_dtype.  U_prefix
+ * (nullable) receives U_t ... U_1 in out_dtype (return_prefix=True).
+ * Three launches on `stream` (chunk summaries, carries, output).            */
+size_t mogt_affine_scan_workspace_bytes(int64_t batch, int64_t length, int64_t rank,
+                                        int64_t channels);
+int mogt_affine_scan_fwd(const void* U, const void* V, void* H, void* U_prefix,
+                         int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                         int v_dtype, int out_dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Transport-only prefix product Y_t = U_t Y_{t-1}, Y_0 = I.
+ * Replaces triton_fused_scan / _fused_scan_kernel (triton_scan.py:13-51,
+ * :151-175), which hard-codes R = 16; here any R <= 32.  U fp32, Y out_dtype. */
+size_t mogt_fused_scan_workspace_bytes(int64_t batch, int64_t length, int64_t rank);
+int mogt_fused_scan_fwd(const void* U, void* Y, int64_t batch, int64_t length, int64_t rank,
+                        int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Block-local affine scan: per block of `block_size` steps, the local prefixes
+ * U_prefix/H_prefix [B, L, ...] and the per-block summaries U_summary
+ * [B, nb, R, R] / H_summary [B, nb, R, C], nb = ceil(L / block_size); all
+ * outputs fp32.  Replaces triton_affine_local_scan / _affine_local_scan_kernel
+ * (triton_scan.py:54-148, :178-229).  No workspace; one launch.             */
+int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H_prefix,
+                           void* U_summary, void* H_summary, int64_t batch, int64_t length,
+                           int64_t rank, int64_t channels, int64_t block_size, int v_dtype,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -160,7 +160,9 @@ __device__ __forceinline__ uint32_t ws_epoch(uint32_t* hdr, uint32_t* s_epoch) {
 // advance the epoch for the next launch.
 __device__ __forceinline__ void ws_finish(uint32_t* hdr, const uint32_t* flags, int64_t n_flags,
                                           uint32_t epoch) {
-    if (blockIdx.x != gridDim.x - 1) return;
+    const uint64_t lin = blockIdx.x + static_cast<uint64_t>(gridDim.x) *
+                                          (blockIdx.y + static_cast<uint64_t>(gridDim.y) * blockIdx.z);
+    if (lin != static_cast<uint64_t>(gridDim.x) * gridDim.y * gridDim.z - 1) return;
     for (int64_t i = threadIdx.x; i < n_flags; i += blockDim.x) {
         uint32_t n = 0;
         while ((ld_relaxed(&flags[i]) >> 2) != epoch) {

@@ -199,3 +199,161 @@ def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping
     if v_raw.shape[:2] != (B, L) or v_raw.shape[2] % r != 0:
         raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
     return torch.ops.mogt.coupled_rank_scan(gate_logits, v_raw, r, float(damping), out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# dense affine scan: H_t = U_t H_{t-1} + V_t (U [B,L,R,R], V/H [B,L,R,C])
+# ---------------------------------------------------------------------------
+def check_affine_shapes(U: torch.Tensor, V: torch.Tensor) -> tuple[int, int, int, int]:
+    """The reference's shape checks (affine_scan.py:26-32, triton_scan.py:193-199)."""
+    if U.ndim != 4 or V.ndim != 4:
+        raise ValueError("U and V must be rank-4 tensors")
+    B, L, R, R2 = U.shape
+    Bv, Lv, Rv, C = V.shape
+    if (B, L, R) != (Bv, Lv, Rv) or R != R2:
+        raise ValueError("U must be [B, L, R, R] and V must be [B, L, R, C]")
+    if R > 32:
+        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= 32)")
+    return B, L, R, C
+
+
+def _affine_launch(U: torch.Tensor, V: torch.Tensor | None, H: torch.Tensor | None,
+                   P: torch.Tensor | None) -> None:
+    lib = _lib.load()
+    B, L, R, _ = U.shape
+    C = V.shape[-1] if V is not None else 0
+    vc = dtype_code(V.dtype, "affine_scan") if V is not None else _lib.MOGT_F32
+    out = H if H is not None else P
+    oc = dtype_code(out.dtype, "affine_scan")
+    stream = _stream_handle(U.device)
+    if V is None:
+        nbytes = lib.mogt_fused_scan_workspace_bytes(B, L, R)
+        ws = workspace(nbytes, U.device)
+        rc = lib.mogt_fused_scan_fwd(U.data_ptr(), P.data_ptr(), B, L, R, oc, ws.data_ptr(),
+                                     ws.numel(), stream)
+        _lib.check(rc, "mogt_fused_scan_fwd")
+        return
+    nbytes = lib.mogt_affine_scan_workspace_bytes(B, L, R, C)
+    ws = workspace(nbytes, U.device)
+    rc = lib.mogt_affine_scan_fwd(U.data_ptr(), V.data_ptr(), H.data_ptr(),
+                                  P.data_ptr() if P is not None else None, B, L, R, C, vc, oc,
+                                  ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "mogt_affine_scan_fwd")
+
+
+def _prep_uv(U: torch.Tensor, V: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    U = U.contiguous()
+    if U.dtype != torch.float32:
+        U = U.to(torch.float32)   # the reference up-casts U (triton_scan.py:203)
+    V = V.contiguous()
+    if V.dtype not in _DTYPE_CODE:
+        V = V.to(torch.float32)
+    return U, V
+
+
+@torch.library.custom_op("mogt::affine_scan", mutates_args=())
+def _affine_scan_op(U: torch.Tensor, V: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    U, V = _prep_uv(U, V)
+    H = torch.empty(V.shape, dtype=out_dtype, device=V.device)
+    _affine_launch(U, V, H, None)
+    return H
+
+
+@_affine_scan_op.register_fake
+def _(U, V, out_dtype):
+    return V.new_empty(V.shape, dtype=out_dtype)
+
+
+@torch.library.custom_op("mogt::affine_scan_prefix", mutates_args=())
+def _affine_scan_prefix_op(U: torch.Tensor, V: torch.Tensor,
+                           out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    U, V = _prep_uv(U, V)
+    H = torch.empty(V.shape, dtype=out_dtype, device=V.device)
+    P = torch.empty(U.shape, dtype=out_dtype, device=U.device)
+    _affine_launch(U, V, H, P)
+    return P, H
+
+
+@_affine_scan_prefix_op.register_fake
+def _(U, V, out_dtype):
+    return U.new_empty(U.shape, dtype=out_dtype), V.new_empty(V.shape, dtype=out_dtype)
+
+
+def affine_scan(U: torch.Tensor, V: torch.Tensor, *, output_dtype: torch.dtype | None = None,
+                return_prefix: bool = False):
+    """H_t = U_t H_{t-1} + V_t on the GPU (fp32 state), ``output_dtype``
+    defaulting to ``V.dtype``; with ``return_prefix`` returns ``(U_prefix, H)``
+    (affine_scan.py:14-62 semantics)."""
+    require_cuda("affine_scan", U, V)
+    check_affine_shapes(U, V)
+    output_dtype = output_dtype or V.dtype
+    if output_dtype not in _DTYPE_CODE:
+        raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
+    if return_prefix:
+        return torch.ops.mogt.affine_scan_prefix(U, V, output_dtype)
+    return torch.ops.mogt.affine_scan(U, V, output_dtype)
+
+
+@torch.library.custom_op("mogt::fused_scan", mutates_args=())
+def _fused_scan_op(U: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    Uf = U.contiguous().to(torch.float32)
+    Y = torch.empty(U.shape, dtype=out_dtype, device=U.device)
+    _affine_launch(Uf, None, None, Y)
+    return Y
+
+
+@_fused_scan_op.register_fake
+def _(U, out_dtype):
+    return U.new_empty(U.shape, dtype=out_dtype)
+
+
+def fused_scan(U: torch.Tensor, *, output_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Transport-only prefix product Y_t = U_t Y_{t-1}, Y_0 = I (triton_scan.py:13-51)."""
+    require_cuda("fused_scan", U)
+    if U.ndim != 4 or U.shape[2] != U.shape[3]:
+        raise ValueError("U must be [B, L, R, R]")
+    if U.shape[2] > 32:
+        raise ValueError(f"R = {U.shape[2]} not supported by the MI355X scan (R <= 32)")
+    output_dtype = output_dtype or U.dtype
+    if output_dtype not in _DTYPE_CODE:
+        raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
+    return torch.ops.mogt.fused_scan(U, output_dtype)
+
+
+@torch.library.custom_op("mogt::affine_local_scan", mutates_args=())
+def _affine_local_scan_op(U: torch.Tensor, V: torch.Tensor, block_size: int
+                          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    U, V = _prep_uv(U, V)
+    B, L, R, _ = U.shape
+    C = V.shape[-1]
+    nb = (L + block_size - 1) // block_size
+    f32 = dict(dtype=torch.float32, device=U.device)
+    Up = torch.empty(U.shape, **f32)
+    Hp = torch.empty(V.shape, **f32)
+    Us = torch.empty((B, nb, R, R), **f32)
+    Hs = torch.empty((B, nb, R, C), **f32)
+    rc = lib.mogt_affine_local_scan(U.data_ptr(), V.data_ptr(), Up.data_ptr(), Hp.data_ptr(),
+                                    Us.data_ptr(), Hs.data_ptr(), B, L, R, C, block_size,
+                                    dtype_code(V.dtype, "affine_local_scan"),
+                                    _stream_handle(U.device))
+    _lib.check(rc, "mogt_affine_local_scan")
+    return Up, Hp, Us, Hs
+
+
+@_affine_local_scan_op.register_fake
+def _(U, V, block_size):
+    B, L, R, _ = U.shape
+    C = V.shape[-1]
+    nb = (L + block_size - 1) // block_size
+    f = dict(dtype=torch.float32)
+    return (U.new_empty(U.shape, **f), V.new_empty(V.shape, **f),
+            U.new_empty((B, nb, R, R), **f), V.new_empty((B, nb, R, C), **f))
+
+
+def affine_local_scan(U: torch.Tensor, V: torch.Tensor, *, block_size: int = 256):
+    require_cuda("affine_local_scan", U, V)
+    check_affine_shapes(U, V)
+    if block_size <= 0:
+        raise ValueError("block_size must be positive")
+    return torch.ops.mogt.affine_local_scan(U, V, int(block_size))

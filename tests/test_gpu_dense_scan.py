@@ -1,0 +1,193 @@
+"""GPU parity of the dense affine scan pipeline (drop-in triton_scan / affine_scan
+API) against the CPU oracle on identical seeded inputs.  fp32 bar: normwise
+max relative error <= 1e-4; bf16 V I/O: <= 2e-2."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, rel_err, to_np
+from mogt_amd import synthetic
+from oracle import scan_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _stable_affine(B, L, R, C, seed, scale=0.05):
+    """U = I + scale*N(0,1) (the reference's sanity distribution) rescaled so the
+    spectral norm stays <= 1 over long sequences; V ~ N(0,1)."""
+    g = synthetic.rng(seed)
+    U = np.eye(R, dtype=np.float32) + np.float32(scale) * g.standard_normal((B, L, R, R), dtype=np.float32)
+    U /= np.maximum(1.0, np.linalg.norm(U, ord=2, axis=(-2, -1)))[..., None, None].astype(np.float32)
+    V = g.standard_normal((B, L, R, C), dtype=np.float32)
+    return U, V
+
+
+def test_reference_sanity_case_fp32(gpu):
+    """sanity_affine_scan.py:11-16 inputs (seed 42, B2 L17 R4 C3), prefix included."""
+    announce("dense reference sanity case")
+    from mogt_amd import triton_scan
+
+    Ut, Vt = synthetic.reference_test_case()
+    U, V = Ut.float().numpy(), Vt.float().numpy()
+    P_ref, H_ref = so.affine_scan_sequential(U, V, return_prefix=True)
+    P, H = triton_scan.triton_affine_scan_hybrid(
+        torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu), block_size=5,
+        carry_scan="doubling", output_dtype=torch.float32, return_prefix=True)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(H), H_ref) <= FP32_TOL
+    assert rel_err(to_np(P), P_ref) <= FP32_TOL
+
+
+def test_reference_triton_sanity_case(gpu):
+    """sanity_affine_scan.py:64-99: B1 L64 R16 C8, block 32, block_c 8; the
+    reference asserts 5e-5 max abs against the sequential scan."""
+    announce("dense triton sanity case")
+    from mogt_amd import triton_scan
+
+    Ut, Vt = synthetic.reference_test_case(batch_size=1, seq_len=64, rank=16, channels=8)
+    U, V = Ut.float().numpy(), Vt.float().numpy()
+    P_ref, H_ref = so.affine_scan_sequential(U, V, return_prefix=True)
+    P, H = triton_scan.triton_affine_scan_hybrid(
+        torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu), block_size=32, block_c=8,
+        carry_scan="sequential", output_dtype=torch.float32, return_prefix=True)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(to_np(H) - H_ref)) <= 5e-5
+    assert np.max(np.abs(to_np(P) - P_ref)) <= 5e-5
+
+
+@pytest.mark.parametrize("B,L,R,C", [
+    (1, 1, 4, 3), (2, 31, 3, 5), (1, 1000, 16, 48), (3, 777, 7, 11), (1, 2049, 32, 32),
+    (2, 600, 16, 70), (1, 500, 5, 130), (1, 4100, 1, 1), (1, 3000, 2, 9),
+])
+def test_random_shapes(gpu, B, L, R, C):
+    announce(f"dense B={B} L={L} R={R} C={C}")
+    import mogt_amd.affine_scan as gas
+
+    U, V = _stable_affine(B, L, R, C, seed=B * 1000 + L + R)
+    P_ref, H_ref = so.affine_scan_sequential(U, V, return_prefix=True)
+    P, H = gas.affine_scan_sequential(torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu),
+                                      return_prefix=True)
+    torch.cuda.synchronize()
+    assert H.dtype == torch.float32 and P.shape == (B, L, R, R)
+    assert rel_err(to_np(H), H_ref) <= FP32_TOL
+    assert rel_err(to_np(P), P_ref) <= FP32_TOL
+
+
+def test_bf16_values_and_output(gpu):
+    announce("dense bf16 V / bf16 out")
+    import mogt_amd
+
+    U, V = _stable_affine(1, 3000, 16, 48, seed=9)
+    Vt = torch.from_numpy(V).to(gpu).bfloat16()
+    H_ref = so.affine_scan_sequential(U, to_np(Vt).astype(np.float64))
+    H = mogt_amd.ops.affine_scan(torch.from_numpy(U).to(gpu), Vt)
+    torch.cuda.synchronize()
+    assert H.dtype == torch.bfloat16
+    assert rel_err(to_np(H), H_ref) <= BF16_TOL
+    H32 = mogt_amd.ops.affine_scan(torch.from_numpy(U).to(gpu), Vt, output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(H32), H_ref) <= FP32_TOL
+
+
+def test_identity_transport_is_cumsum_and_scalar_decay_is_diag(gpu):
+    announce("dense U=I cumsum / U=f I")
+    import mogt_amd
+
+    g = synthetic.rng(4)
+    L, R, C = 5000, 16, 48
+    V = g.standard_normal((1, L, R, C), dtype=np.float32)
+    U = np.broadcast_to(np.eye(R, dtype=np.float32), (1, L, R, R)).copy()
+    H = mogt_amd.ops.affine_scan(torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu))
+    f = (1.0 / (1.0 + np.exp(-g.standard_normal((1, L), dtype=np.float32) - 3.0))).astype(np.float32)
+    Uf = (f[..., None, None] * np.eye(R, dtype=np.float32)).astype(np.float32)
+    Hf = mogt_amd.ops.affine_scan(torch.from_numpy(Uf).to(gpu), torch.from_numpy(V).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(H), np.cumsum(V.astype(np.float64), axis=1)) <= FP32_TOL
+    a = np.broadcast_to(f[..., None], (1, L, R * C))
+    ref = so.diag_scan(a, V.reshape(1, L, R * C)).reshape(1, L, R, C)
+    assert rel_err(to_np(Hf), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("R,L", [(16, 2048), (4, 300), (32, 1500)])
+def test_fused_scan(gpu, R, L):
+    """triton_scan.py:480-494 demo: U = I + 0.01 N(0,1), prefix product."""
+    announce(f"fused scan R={R} L={L}")
+    from mogt_amd import triton_scan
+
+    g = synthetic.rng(R + L)
+    U = (np.eye(R, dtype=np.float32) + np.float32(0.01) * g.standard_normal((2, L, R, R), dtype=np.float32))
+    Y = triton_scan.triton_fused_scan(torch.from_numpy(U).to(gpu))
+    torch.cuda.synchronize()
+    assert Y.dtype == torch.float32
+    assert rel_err(to_np(Y), so.fused_scan(U)) <= FP32_TOL
+
+
+@pytest.mark.parametrize("block", [1, 16, 32, 256, 1000])
+def test_local_scan(gpu, block):
+    announce(f"local scan block={block}")
+    from mogt_amd import triton_scan
+
+    U, V = _stable_affine(2, 777, 16, 24, seed=block)
+    ref = so.local_scan(U, V, block_size=block)
+    out = triton_scan.triton_affine_local_scan(torch.from_numpy(U).to(gpu),
+                                               torch.from_numpy(V).to(gpu), block_size=block)
+    torch.cuda.synchronize()
+    for got, want in zip(out, ref):
+        assert got.dtype == torch.float32 and tuple(got.shape) == want.shape
+        assert rel_err(to_np(got), want) <= FP32_TOL
+
+
+def test_validation_matches_reference(gpu):
+    from mogt_amd import triton_scan
+
+    U = torch.zeros(1, 4, 4, 4, device=gpu)
+    V = torch.zeros(1, 4, 4, 3, device=gpu)
+    with pytest.raises(ValueError):
+        triton_scan.triton_affine_scan_hybrid(U, V, carry_scan="tree")
+    with pytest.raises(ValueError):
+        triton_scan.triton_affine_local_scan(U, V[:, :, :3])
+    with pytest.raises(ValueError):
+        triton_scan.triton_affine_local_scan(U.cpu(), V.cpu())
+    with pytest.raises(ValueError):
+        triton_scan.triton_affine_scan_hybrid(U[0], V)
+
+
+@pytest.mark.parametrize("R,C", [(4, 3), (16, 8)])
+def test_backward_matches_oracle(gpu, R, C):
+    """sanity_affine_scan.py:102-135 (hand backward vs autograd): here the GPU
+    autograd Function against the oracle's reverse scan."""
+    announce(f"dense backward R={R} C={C}")
+    from mogt_amd import triton_scan
+
+    U, V = _stable_affine(2, 53, R, C, seed=R)
+    G = synthetic.rng(7).standard_normal(V.shape, dtype=np.float32)
+    gU_ref, gV_ref = so.affine_scan_sequential_backward(U.astype(np.float64), V.astype(np.float64), G)
+    Ut = torch.from_numpy(U).to(gpu).requires_grad_(True)
+    Vt = torch.from_numpy(V).to(gpu).requires_grad_(True)
+    H = triton_scan.triton_affine_scan_hybrid(Ut, Vt, block_size=16)
+    H.backward(torch.from_numpy(G).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(Vt.grad), gV_ref) <= FP32_TOL
+    assert rel_err(to_np(Ut.grad), gU_ref) <= FP32_TOL
+
+
+def test_cfg4_dense_cayley_full_size(gpu):
+    """H=8, d_h=32, B=1, L=16384, fp32, A_t = gate * Cayley(W_t),
+    B_t = v k^T; output S_t for every step."""
+    announce("cfg4 dense cayley full size")
+    import mogt_amd
+
+    U, V = synthetic.dense_cayley_inputs(1, 16384, 8, 32, seed=0)
+    ref = so.affine_scan_sequential(U, V)
+    S = mogt_amd.ops.affine_scan(torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(S), ref) <= FP32_TOL
+
+
+def test_zz_dense_no_lookback_wait_gave_up(gpu):
+    from mogt_amd import ops
+
+    assert ops.workspace_faults() == 0
