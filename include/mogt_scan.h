@@ -120,6 +120,26 @@ int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H
                            int64_t rank, int64_t channels, int64_t block_size, int v_dtype,
                            void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Row-wise kernels of the MOGT block (one wave per row, rows of `dim`
+ * contiguous elements, dim a multiple of 4 and <= 4096; weight fp32 [dim]).
+ *
+ * mogt_rmsnorm_fwd: out = (x * rsqrt(mean(x^2) + eps)).type_as(x) * weight
+ *   -- RMSNorm.forward, model_mogt.py:9-20 (statistics in fp32).
+ * mogt_add_rmsnorm_fwd: x_out = x + (scale * z) [the product rounded to z's
+ *   dtype], out = rmsnorm(x_out) -- the residual update followed by the next
+ *   RMSNorm (model_mogt.py:243-256), x and x_out fp32.
+ * mogt_silu_mul_fwd: y = [rows, 2*hidden] (w1 | w2 outputs), out = silu(y1) *
+ *   y2 [rows, hidden] -- SwiGLU.forward, model_mogt.py:29-30 (silu result
+ *   rounded to the tensor dtype before the product, as torch does).          */
+int mogt_rmsnorm_fwd(const void* x, const float* weight, void* out, int64_t rows, int64_t dim,
+                     float eps, int x_dtype, int out_dtype, void* stream);
+int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float* weight,
+                         float* x_out, void* out, int64_t rows, int64_t dim, float eps,
+                         int z_dtype, int out_dtype, void* stream);
+int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,13 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
          _c_i64, _c_i64, _c_int, _c_void_p],
     ),
+    "mogt_rmsnorm_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_int, _c_int, _c_void_p]),
+    "mogt_add_rmsnorm_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
+         _c_int, _c_int, _c_void_p]),
+    "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
 }
 
 _lock = threading.Lock()

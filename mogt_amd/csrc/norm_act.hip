@@ -1,0 +1,192 @@
+// Fused row-wise kernels of the MOGT block (model_mogt.py:9-30, 238-256):
+//   rmsnorm       out = (x * rsqrt(mean(x^2) + eps)).type_as(x) * w
+//   add_rmsnorm   x' = x + round(s * z);  out = rmsnorm(x') * w   (residual + norm)
+//   silu_mul      out = silu(y[:, :H]) * y[:, H:]                   (SwiGLU gate)
+// Each rounds to bf16 at the points where the reference's bf16 tensors do, so
+// results track the reference's autocast dtype flow; statistics are fp32.
+// One wave per row: lanes hold 4-element vectors of the row (coalesced 16 B
+// loads), the sum of squares is reduced across the wave with cross-lane
+// shuffles, and the row is written once.
+#include "common.h"
+
+namespace mogt {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <typename T> __device__ __forceinline__ float rnd(float v) { return IO<T>::ld(IO<T>::st(v)); }
+
+constexpr int NA_WAVES = 4;   // rows per work-group
+
+// VPL = 4-element vectors per lane (row length <= 256 * VPL).
+template <typename TX, typename TZ, typename TO, int VPL, bool ADD>
+__global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
+    const TX* __restrict__ x, const TZ* __restrict__ z, float scale, const float* __restrict__ w,
+    float* __restrict__ x_out, TO* __restrict__ out, int64_t rows, int D, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * NA_WAVES + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const TX* xr = x + row * D;
+    float v[VPL][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int c = (k * 64 + lane) * 4;
+        if (c < D) {
+            load_vec<TX, 4>(xr + c, v[k]);
+            if constexpr (ADD) {
+                float zz[4];
+                load_vec<TZ, 4>(z + row * D + c, zz);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[k][e] += rnd<TZ>(scale * zz[e]);
+                store_vec<float, 4>(x_out + row * D + c, v[k]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[k][e] = 0.0f;
+        }
+    }
+    const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+    TO* orow = out + row * D;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int c = (k * 64 + lane) * 4;
+        if (c < D) {
+            float ww[4], o[4];
+            load_vec<float, 4>(w + c, ww);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // .type_as(x): the normalised value takes the input's dtype first
+                const float nrm = ADD ? v[k][e] * inv : rnd<TX>(v[k][e] * inv);
+                o[e] = nrm * ww[e];
+            }
+            store_vec<TO, 4>(orow + c, o);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ y, T* __restrict__ out,
+                                                       int64_t rows, int64_t H) {
+    const int64_t nvec = rows * H / 4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t e = i * 4;
+        const int64_t r = e / H;
+        const int64_t c = e - r * H;
+        float a[4], b[4], o[4];
+        load_vec<T, 4>(y + r * 2 * H + c, a);
+        load_vec<T, 4>(y + r * 2 * H + H + c, b);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float s = rnd<T>(a[k] / (1.0f + expf(-a[k])));   // F.silu on the bf16 tensor
+            o[k] = s * b[k];
+        }
+        store_vec<T, 4>(out + r * H + c, o);
+    }
+}
+
+namespace {
+
+bool dt_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
+
+template <typename TX, typename TZ, typename TO, bool ADD>
+int launch_norm(const void* x, const void* z, float scale, const float* w, float* x_out, void* out,
+                int64_t rows, int D, float eps, hipStream_t st) {
+    const int vpl = (D + 255) / 256;
+    const dim3 grid(static_cast<unsigned>((rows + NA_WAVES - 1) / NA_WAVES));
+    const dim3 block(64 * NA_WAVES);
+    const TX* xp = static_cast<const TX*>(x);
+    const TZ* zp = static_cast<const TZ*>(z);
+    TO* op = static_cast<TO*>(out);
+#define MOGT_NORM_CASE(V)                                                                      \
+    if (vpl <= V) {                                                                             \
+        hipLaunchKernelGGL((rmsnorm_kernel<TX, TZ, TO, V, ADD>), grid, block, 0, st, xp, zp,    \
+                           scale, w, x_out, op, rows, D, eps);                                  \
+        return check_launch("rmsnorm_kernel");                                                  \
+    }
+    MOGT_NORM_CASE(1)
+    MOGT_NORM_CASE(2)
+    MOGT_NORM_CASE(3)
+    MOGT_NORM_CASE(4)
+    MOGT_NORM_CASE(8)
+    MOGT_NORM_CASE(16)
+#undef MOGT_NORM_CASE
+    return set_error(MOGT_E_INVALID, "rmsnorm: row length %d > 4096", D);
+}
+
+int check_norm_args(int64_t rows, int64_t dim) {
+    if (rows < 0 || dim <= 0) return set_error(MOGT_E_INVALID, "rmsnorm: bad shape");
+    if (dim % 4 != 0) return set_error(MOGT_E_INVALID, "rmsnorm: row length must be a multiple of 4");
+    if (dim > 4096) return set_error(MOGT_E_INVALID, "rmsnorm: row length %lld > 4096", (long long)dim);
+    return MOGT_OK;
+}
+
+}  // namespace
+}  // namespace mogt
+
+using namespace mogt;
+
+extern "C" int mogt_rmsnorm_fwd(const void* x, const float* weight, void* out, int64_t rows, int64_t dim,
+                                float eps, int x_dtype, int out_dtype, void* stream) {
+    clear_error();
+    int rc = check_norm_args(rows, dim);
+    if (rc) return rc;
+    if (!dt_ok(x_dtype) || !dt_ok(out_dtype)) return set_error(MOGT_E_INVALID, "rmsnorm: dtype");
+    if (rows == 0) return MOGT_OK;
+    if (!x || !weight || !out) return set_error(MOGT_E_INVALID, "rmsnorm: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int D = static_cast<int>(dim);
+    if (x_dtype == MOGT_F32 && out_dtype == MOGT_F32)
+        return launch_norm<float, float, float, false>(x, nullptr, 0.f, weight, nullptr, out, rows, D, eps, st);
+    if (x_dtype == MOGT_F32 && out_dtype == MOGT_BF16)
+        return launch_norm<float, float, bf16_t, false>(x, nullptr, 0.f, weight, nullptr, out, rows, D, eps, st);
+    if (x_dtype == MOGT_BF16 && out_dtype == MOGT_F32)
+        return launch_norm<bf16_t, float, float, false>(x, nullptr, 0.f, weight, nullptr, out, rows, D, eps, st);
+    return launch_norm<bf16_t, float, bf16_t, false>(x, nullptr, 0.f, weight, nullptr, out, rows, D, eps, st);
+}
+
+extern "C" int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float* weight,
+                                    float* x_out, void* out, int64_t rows, int64_t dim, float eps,
+                                    int z_dtype, int out_dtype, void* stream) {
+    clear_error();
+    int rc = check_norm_args(rows, dim);
+    if (rc) return rc;
+    if (!dt_ok(z_dtype) || !dt_ok(out_dtype)) return set_error(MOGT_E_INVALID, "add_rmsnorm: dtype");
+    if (rows == 0) return MOGT_OK;
+    if (!x || !z || !weight || !x_out || !out) return set_error(MOGT_E_INVALID, "add_rmsnorm: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int D = static_cast<int>(dim);
+    if (z_dtype == MOGT_F32 && out_dtype == MOGT_F32)
+        return launch_norm<float, float, float, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
+    if (z_dtype == MOGT_F32 && out_dtype == MOGT_BF16)
+        return launch_norm<float, float, bf16_t, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
+    if (z_dtype == MOGT_BF16 && out_dtype == MOGT_F32)
+        return launch_norm<float, bf16_t, float, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
+    return launch_norm<float, bf16_t, bf16_t, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
+}
+
+extern "C" int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
+                                 void* stream) {
+    clear_error();
+    if (rows < 0 || hidden <= 0 || hidden % 4 != 0)
+        return set_error(MOGT_E_INVALID, "silu_mul: hidden must be a positive multiple of 4");
+    if (!dt_ok(dtype)) return set_error(MOGT_E_INVALID, "silu_mul: dtype");
+    if (rows == 0) return MOGT_OK;
+    if (!y || !out) return set_error(MOGT_E_INVALID, "silu_mul: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t nvec = rows * hidden / 4;
+    const unsigned grid = static_cast<unsigned>(nvec / 256 + 1 < 8192 ? nvec / 256 + 1 : 8192);
+    if (dtype == MOGT_F32)
+        hipLaunchKernelGGL((silu_mul_kernel<float>), dim3(grid), dim3(256), 0, st,
+                           static_cast<const float*>(y), static_cast<float*>(out), rows, hidden);
+    else
+        hipLaunchKernelGGL((silu_mul_kernel<bf16_t>), dim3(grid), dim3(256), 0, st,
+                           static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), rows, hidden);
+    return check_launch("silu_mul_kernel");
+}

@@ -357,3 +357,93 @@ def affine_local_scan(U: torch.Tensor, V: torch.Tensor, *, block_size: int = 256
     if block_size <= 0:
         raise ValueError("block_size must be positive")
     return torch.ops.mogt.affine_local_scan(U, V, int(block_size))
+
+
+# ---------------------------------------------------------------------------
+# row-wise block kernels: rmsnorm, residual-add + rmsnorm, silu-mul
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("mogt::rmsnorm", mutates_args=())
+def _rmsnorm_op(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                out_dtype: torch.dtype) -> torch.Tensor:
+    lib = _lib.load()
+    x = x.contiguous()
+    w = weight.contiguous().to(torch.float32)
+    D = x.shape[-1]
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    rc = lib.mogt_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), out.data_ptr(), x.numel() // D, D,
+                              float(eps), dtype_code(x.dtype, "rmsnorm"),
+                              dtype_code(out_dtype, "rmsnorm"), _stream_handle(x.device))
+    _lib.check(rc, "mogt_rmsnorm_fwd")
+    return out
+
+
+@_rmsnorm_op.register_fake
+def _(x, weight, eps, out_dtype):
+    return x.new_empty(x.shape, dtype=out_dtype)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+            out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """RMSNorm.forward (model_mogt.py:15-20) in one pass; ``out_dtype`` defaults
+    to float32 (the dtype of ``normalised.type_as(x) * fp32 weight``)."""
+    require_cuda("rmsnorm", x, weight)
+    return torch.ops.mogt.rmsnorm(x, weight, float(eps), out_dtype or torch.float32)
+
+
+@torch.library.custom_op("mogt::add_rmsnorm", mutates_args=())
+def _add_rmsnorm_op(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Tensor, eps: float,
+                    out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    x = x.contiguous()
+    z = z.contiguous()
+    w = weight.contiguous().to(torch.float32)
+    D = x.shape[-1]
+    x_out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    rc = lib.mogt_add_rmsnorm_fwd(x.data_ptr(), z.data_ptr(), float(scale), w.data_ptr(),
+                                  x_out.data_ptr(), out.data_ptr(), x.numel() // D, D, float(eps),
+                                  dtype_code(z.dtype, "add_rmsnorm"),
+                                  dtype_code(out_dtype, "add_rmsnorm"), _stream_handle(x.device))
+    _lib.check(rc, "mogt_add_rmsnorm_fwd")
+    return x_out, out
+
+
+@_add_rmsnorm_op.register_fake
+def _(x, z, scale, weight, eps, out_dtype):
+    return x.new_empty(x.shape, dtype=torch.float32), x.new_empty(x.shape, dtype=out_dtype)
+
+
+def add_rmsnorm(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Tensor,
+                eps: float = 1e-6, out_dtype: torch.dtype = torch.float32):
+    """``x' = x + scale * z`` (fp32 residual stream) and ``rmsnorm(x') * weight``."""
+    require_cuda("add_rmsnorm", x, z, weight)
+    if x.dtype != torch.float32:
+        raise ValueError("add_rmsnorm keeps the residual stream in float32")
+    if x.shape != z.shape:
+        raise ValueError("x and z must have the same shape")
+    return torch.ops.mogt.add_rmsnorm(x, z, float(scale), weight, float(eps), out_dtype)
+
+
+@torch.library.custom_op("mogt::silu_mul", mutates_args=())
+def _silu_mul_op(y: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    y = y.contiguous()
+    H2 = y.shape[-1]
+    out = torch.empty((*y.shape[:-1], H2 // 2), dtype=y.dtype, device=y.device)
+    rc = lib.mogt_silu_mul_fwd(y.data_ptr(), out.data_ptr(), y.numel() // H2, H2 // 2,
+                               dtype_code(y.dtype, "silu_mul"), _stream_handle(y.device))
+    _lib.check(rc, "mogt_silu_mul_fwd")
+    return out
+
+
+@_silu_mul_op.register_fake
+def _(y):
+    return y.new_empty((*y.shape[:-1], y.shape[-1] // 2))
+
+
+def silu_mul(y: torch.Tensor) -> torch.Tensor:
+    """``silu(y[..., :H]) * y[..., H:]`` for the fused ``[w1; w2]`` projection."""
+    require_cuda("silu_mul", y)
+    if y.shape[-1] % 8 != 0:
+        raise ValueError("silu_mul needs an even hidden size that is a multiple of 4")
+    return torch.ops.mogt.silu_mul(y)
