@@ -212,6 +212,30 @@ def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets
             "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=3):
+    """rank-1 coupled write-forget scan with readout, bf16 I/O."""
+    from mogt_amd import synthetic
+
+    dev = torch.device("cuda:0")
+    f, k, v, q = (torch.from_numpy(x).to(dev).bfloat16() for x in synthetic.rank1_inputs(B, L, H, d, seed=0))
+    bufs = [(f.clone(), k.clone(), v.clone(), q.clone(), torch.empty_like(q)) for _ in range(sets)]
+    ws = ops.workspace(lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d), dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    fn = lib.mogt_rank1_coupled_scan_fwd
+
+    def launch(i):
+        ff, kk, vv, qq, yy = bufs[i % sets]
+        rc = fn(ff.data_ptr(), kk.data_ptr(), vv.data_ptr(), qq.data_ptr(), yy.data_ptr(), B, L, H, d,
+                1, 1, 1, ws.data_ptr(), ws.numel(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    total = B * L * H * (4 * d * 2 + 2)   # f, k, v, q in + y out (bf16)
+    return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
+
+
 def measure_backbone(torch, layers, ffn_hidden, vocab, L, iters, warmup):
     """MOGT backbone forward (embedding -> blocks -> norm_f) under bf16 autocast
     and inference_mode, identity-coupled slot-addressed blocks, random N(0,0.02)
@@ -378,6 +402,11 @@ def main():
             "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
+        r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
+        extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
+            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+            "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out)"}
         r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
         extras["dense_affine_r16_c48_L32768"] = {
             "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),

@@ -121,6 +121,21 @@ int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H
                            void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* Rank-1 coupled write-forget scan with readout:
+ *   S_t = f_t S_{t-1} + (1 - f_t) v_t k_t^T,  y_t = S_t q_t,  S_0 = 0
+ * i.e. affine_scan_sequential (affine_scan.py:14-62) with U_t = f_t I and
+ * V_t = (1 - f_t) v_t k_t^T, read out through q_t, without materialising S_t.
+ * f: [B, L, H]; k, v, q, y: [B, L, H, head_dim]; head_dim = 64.  Products run
+ * on bf16 MFMA with fp32 accumulation and fp32 carried state (inputs are
+ * rounded to bf16); three launches (chunk states, carries, outputs).        */
+size_t mogt_rank1_coupled_scan_workspace_bytes(int64_t batch, int64_t length, int64_t heads,
+                                               int64_t head_dim);
+int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, const void* q,
+                                void* y, int64_t batch, int64_t length, int64_t heads,
+                                int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* Row-wise kernels of the MOGT block (one wave per row, rows of `dim`
  * contiguous elements, dim a multiple of 4 and <= 4096; weight fp32 [dim]).
  *

@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
          _c_int, _c_int, _c_void_p]),
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_rank1_coupled_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "mogt_rank1_coupled_scan_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
 }
 
 _lock = threading.Lock()
