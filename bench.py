@@ -43,7 +43,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
     p.add_argument("--only", choices=["diag", "all"], default="all")
-    p.add_argument("--tile", default=None, help="vec,steps,waves override for the diag scan")
+    p.add_argument("--tile", default=None,
+                   help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC calibration)")
@@ -111,11 +112,11 @@ def diag_launcher(torch, lib, ops, B, L, D, dtype, out_dtype, sets, tile=None, s
                 raise RuntimeError(lib.mogt_last_error().decode())
     else:
         fn = lib.mogt_diag_scan_fwd_cfg
-        v, s, w = tile
+        v, fl, s, w = tile
 
         def launch(i):
             pa, pb, ph = args[i % sets]
-            rc = fn(pa, pb, ph, None, B, L, D, ic, oc, v, s, w, wsp, wsn, sh)
+            rc = fn(pa, pb, ph, None, B, L, D, ic, oc, v, fl, s, w, wsp, wsn, sh)
             if rc:
                 raise RuntimeError(lib.mogt_last_error().decode())
 
@@ -369,13 +370,9 @@ def main():
         log(f"calibration copy of {n} bytes done (x5)")
 
     if args.sweep:
-        tiles = [(1, 32, 16), (1, 64, 16), (1, 48, 16), (1, 40, 8), (1, 32, 8), (1, 16, 8),
-                 (2, 32, 16), (2, 16, 8), (4, 16, 8), (4, 8, 8)]
         for L in (8192, 16384, 32768):
             for dt in (torch.float32, torch.bfloat16):
-                for t in tiles:
-                    if dt == torch.float32 and t[1] > 40:
-                        continue   # fp32 tiles beyond 40 steps spill registers
+                for t in mogt_amd._lib.diag_tiles(0 if dt == torch.float32 else 1):
                     r = measure_diag(torch, lib, ops, L, dt, dt, args.steps, args.warmup, tile=t)
                     log(f"sweep L={L} {dt} tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
                         f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")

@@ -59,15 +59,20 @@ int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a_prefix,
                        int in_dtype, int out_dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* Same with an explicit tile configuration (features per lane, steps per
- * thread, waves per work-group); used for tuning.  The workspace query takes
- * the same triple.                                                          */
+/* Same with an explicit tile configuration, for tuning: `vec` features per
+ * lane, `lanes` lanes per row (64, 32 or 16; a row of the chunk is one vector
+ * load of `lanes` lanes, so a wave covers 64/lanes rows at once), `steps` steps
+ * per lane, `waves` waves per work-group.  A chunk covers lanes*vec features
+ * and steps*waves*64/lanes steps.  The workspace query takes the same tile.
+ * mogt_diag_scan_tiles lists the compiled tiles of a family (0: fp32 input,
+ * 1: bf16 input, 2: coupled scan) as 4 ints each and returns their count.   */
 size_t mogt_diag_scan_workspace_bytes_cfg(int64_t batch, int64_t length, int64_t features,
-                                          int vec, int steps, int waves);
+                                          int vec, int lanes, int steps, int waves);
 int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix,
                            int64_t batch, int64_t length, int64_t features,
-                           int in_dtype, int out_dtype, int vec, int steps, int waves,
+                           int in_dtype, int out_dtype, int vec, int lanes, int steps, int waves,
                            void* workspace, size_t workspace_bytes, void* stream);
+int mogt_diag_scan_tiles(int family, int* out, int max_tiles);
 
 /* ------------------------------------------------------------------------- */
 /* Coupled write-forget per-rank scan of the MOGT mixer with identity

@@ -65,7 +65,7 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objs = [objdir / (s.stem + ".o") for s in srcs]
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2))
+    jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 2))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_compile, srcs, objs))
     out = lib_path()

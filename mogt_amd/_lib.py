@@ -14,7 +14,7 @@ from . import _build
 
 MOGT_F32 = 0
 MOGT_BF16 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -32,12 +32,14 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
          _c_void_p, _c_size, _c_void_p],
     ),
-    "mogt_diag_scan_workspace_bytes_cfg": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
+    "mogt_diag_scan_workspace_bytes_cfg": (
+        _c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int]),
     "mogt_diag_scan_fwd_cfg": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
-         _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
+         _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_diag_scan_tiles": (_c_int, [_c_int, ctypes.POINTER(_c_int), _c_int]),
     "mogt_coupled_rank_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "mogt_coupled_rank_scan_fwd": (
         _c_int,
@@ -123,3 +125,13 @@ def check(rc: int, what: str) -> None:
 
 def exported_symbols() -> list[str]:
     return list(SIGNATURES)
+
+
+def diag_tiles(family: int) -> list[tuple[int, int, int, int]]:
+    """Compiled diag-scan tiles (vec, lanes, steps, waves) of a family:
+    0 fp32 input, 1 bf16 input, 2 coupled scan."""
+    lib = load()
+    n = lib.mogt_diag_scan_tiles(family, None, 0)
+    buf = (_c_int * (4 * n))()
+    lib.mogt_diag_scan_tiles(family, buf, n)
+    return [tuple(buf[4 * i:4 * i + 4]) for i in range(n)]

@@ -31,4 +31,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* mogt_last_error(void) { return mogt::g_last_error; }
 
-extern "C" int mogt_abi_version(void) { return 1; }
+extern "C" int mogt_abi_version(void) { return 2; }

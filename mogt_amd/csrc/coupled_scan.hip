@@ -1,0 +1,100 @@
+// Coupled write-forget per-rank scan of the MOGT mixer (identity connection):
+// the gate sigmoid, the coupling a = damping * (1 - g) and the gated write
+// b = v * g are computed in registers inside the single-pass diagonal scan
+// (diag_kernel.h), so the reference's [B, L, r, r] fp32 U, its [B, L, 3d] gate
+// input and its gated V (model_mogt.py:104-182) are never written to memory.
+#include "diag_kernel.h"
+
+namespace mogt {
+
+namespace {
+
+template <typename TZ, typename TV, typename TO>
+int coupled_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
+#define MOGT_CASE(V_, F_, S_, W_)                                          \
+    if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) \
+        return diag_launch<MODE_COUPLED, TV, TZ, TO, V_, F_, S_, W_, false>(prm, st);
+    MOGT_COUPLED_TILES(MOGT_CASE)
+#undef MOGT_CASE
+    return set_error(MOGT_E_INVALID, "coupled scan: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
+                     t.vec, t.lanes, t.steps, t.waves);
+}
+
+bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
+
+// Default tile (measured on MI355X at r = 16, c = 48, L = 8k..32k): two
+// channels per lane (the lanes of one vector must share a gate, so the vector
+// must divide the channel count), 32 lanes per row, 512-step chunks; short
+// problems fall back to shorter chunks.
+DiagTile coupled_tile(int64_t B, int64_t L, int64_t R, int64_t C, bool aligned2) {
+    static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
+    static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
+    if (C % 2 == 0 && aligned2) return pick_tile(B, L, R * C, v2, 3);
+    return pick_tile(B, L, R * C, v1, 3);
+}
+
+}  // namespace
+
+int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int64_t R, int64_t C,
+                float damping, int z_dtype, int v_dtype, int out_dtype, const DiagTile& t,
+                void* ws, size_t ws_bytes, void* stream) {
+    const int64_t D = R * C;
+    if (C % t.vec != 0)
+        return set_error(MOGT_E_INVALID, "channels %lld not a multiple of vec %d", (long long)C, t.vec);
+    DiagParams prm{};
+    int rc = diag_prepare(prm, B, L, D, t, ws, ws_bytes);
+    if (rc) return rc;
+    prm.a = z;
+    prm.b = v;
+    prm.h = h;
+    prm.aprefix = nullptr;
+    prm.R = static_cast<int>(R);
+    prm.C = static_cast<int>(C);
+    prm.damping = damping;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool zb = z_dtype == MOGT_BF16, vb = v_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
+    if (!zb && vb && !ob) return coupled_dispatch<float, bf16_t, float>(prm, t, st);
+    if (!zb && vb && ob) return coupled_dispatch<float, bf16_t, bf16_t>(prm, t, st);
+    if (zb && vb && !ob) return coupled_dispatch<bf16_t, bf16_t, float>(prm, t, st);
+    if (zb && vb && ob) return coupled_dispatch<bf16_t, bf16_t, bf16_t>(prm, t, st);
+    if (!zb && !vb && !ob) return coupled_dispatch<float, float, float>(prm, t, st);
+    if (!zb && !vb && ob) return coupled_dispatch<float, float, bf16_t>(prm, t, st);
+    if (zb && !vb && !ob) return coupled_dispatch<bf16_t, float, float>(prm, t, st);
+    return coupled_dispatch<bf16_t, float, bf16_t>(prm, t, st);
+}
+
+}  // namespace mogt
+
+using namespace mogt;
+
+extern "C" size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t length,
+                                                         int64_t rank, int64_t channels,
+                                                         int v_dtype) {
+    if (batch <= 0 || length <= 0 || rank <= 0 || channels <= 0) return WS_HDR_BYTES;
+    // Largest requirement over the tiles the entry point may pick.
+    const size_t a = diag_geometry(batch, length, rank * channels,
+                                   coupled_tile(batch, length, rank, channels, true)).bytes;
+    const size_t b = diag_geometry(batch, length, rank * channels,
+                                   coupled_tile(batch, length, rank, channels, false)).bytes;
+    (void)v_dtype;
+    return a > b ? a : b;
+}
+
+extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h, int64_t batch,
+                                          int64_t length, int64_t rank, int64_t channels,
+                                          float damping, int z_dtype, int v_dtype, int out_dtype,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "rank and channels must be positive");
+    if (!dtype_ok(z_dtype) || !dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+        return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!z || !v || !h) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    auto aligned = [](const void* ptr, uintptr_t n) { return reinterpret_cast<uintptr_t>(ptr) % n == 0; };
+    const bool al2 = aligned(v, v_dtype == MOGT_BF16 ? 4 : 8) && aligned(h, out_dtype == MOGT_BF16 ? 4 : 8);
+    const DiagTile t = coupled_tile(batch, length, rank, channels, al2);
+    return coupled_run(z, v, h, batch, length, rank, channels, damping, z_dtype, v_dtype, out_dtype,
+                       t, workspace, workspace_bytes, stream);
+}

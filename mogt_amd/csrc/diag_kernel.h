@@ -1,0 +1,469 @@
+// Single-pass diagonal affine scan h_t = a_t * h_{t-1} + b_t for gfx950, shared
+// by the plain per-feature scan (diag_scan.hip) and the coupled write-forget
+// mixer scan (coupled_scan.hip).
+//
+// Semantics follow the reference's sequential recurrence (affine_scan.py:48-55,
+// H_0 = 0, fp32 state, outputs cast at the end) in the per-feature R=C=1 case,
+// and the coupled write-forget gate of the MOGT mixer (model_mogt.py:166-182).
+//
+// Design (one launch, 3 HBM streams: read a, read b, write h):
+//   tile     one work-group = WT waves x 64 lanes.  A lane owns VEC consecutive
+//            features (one vector load/store per row, rows contiguous along D);
+//            a wave owns S consecutive steps of them; the WT waves of a group
+//            cover T = WT*S consecutive steps of the same FW = 64*VEC features.
+//            Chunk id = blockIdx.x, position-major over the G = B * D/FW
+//            feature-group chains, so one dispatch generation covers the same
+//            stretch of every chain.
+//   stash    every load is issued first; the raw inputs stay in registers in
+//            the most compact exact form (fp32 pairs, packed bf16 pairs, or one
+//            gate value per step for the coupled mode) until the carry is known.
+//   level 1  each lane scans its S steps in registers (prod a, h from 0).
+//   level 2  wave summaries go through LDS; one thread per feature folds them
+//            into the chunk aggregate.
+//   level 3  decoupled look-back along the chain.  Every chunk owns one pair of
+//            64-bit words per feature, {tag | f32 A} and {tag | f32 H}, written
+//            with single atomic stores: first the aggregate (tag AGG), then,
+//            in place, the inclusive prefix (tag INC).  A reader accepts a pair
+//            only when both tags agree, so no fences and no separate status
+//            flags are needed, and every feature resolves independently.  One
+//            look-back round reads a window of NR predecessors at once (slice
+//            r of the group's threads reads predecessor hi - r), folds the
+//            window newest-first up to the nearest INC, and repeats only for the
+//            features whose window was incomplete.
+//   output   each lane composes the chunk carry with the summaries of the waves
+//            before it, re-runs its S steps from that state (same order of
+//            operations as the sequential recurrence) and writes every h once.
+//
+// Workspace reuse without clearing: the launch epoch lives in the workspace
+// header; each work-group records that it has read it (one "seen" word per
+// chunk) and the last work-group advances it once every chunk has, so stale
+// words of earlier launches never match a newer tag and the buffer is
+// zero-filled only once (this also holds inside a captured HIP graph).
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace mogt {
+
+enum DiagMode { MODE_DIAG = 0, MODE_COUPLED = 1 };
+
+struct DiagParams {
+    const void* a;      // [B, L, D] (DIAG)            | gate logits z [B, L, R] (COUPLED)
+    const void* b;      // [B, L, D]                    | v [B, L, D]
+    void* h;            // [B, L, D]
+    void* aprefix;      // [B, L, D] or null (DIAG only)
+    int64_t L, D;
+    int n_fg;           // feature groups per batch row
+    int n_ch;           // chunks along L
+    int G;              // B * n_fg look-back chains
+    int R, C;           // COUPLED: gate count and channels per gate (D = R*C)
+    float damping;      // COUPLED: connection damping (identity connection scale)
+    uint32_t* hdr;
+    uint32_t* seen;     // [G * n_ch] per-chunk "epoch read" words
+    uint64_t* pay;      // 2 planes of [G][n_ch][FW] words: A, H
+    int64_t plane;      // words per plane
+};
+
+constexpr uint32_t ST_NONE = 0u;
+
+template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
+          bool PREFIX>
+__global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
+    constexpr int NT = 64 * WT;
+    constexpr int Q = 64 / FWL;       // step groups per wave (rows per vector load)
+    constexpr int VW = WT * Q;        // "virtual waves": groups of S consecutive steps
+    constexpr int FW = FWL * VEC;     // features per chunk (chain width)
+    constexpr int T = VW * S;         // steps per chunk
+    constexpr int NR = NT / FW;       // look-back window (predecessors read per round)
+    static_assert(64 % FWL == 0 && FWL >= 16, "a row spans 16, 32 or 64 lanes");
+    constexpr bool COUPLED = MODE == MODE_COUPLED;
+    constexpr bool BF16_IN = std::is_same<TIn, bf16_t>::value;
+    // Stash layouts (registers per step and lane):
+    //   DIAG fp32:        a[VEC], b[VEC]               2*VEC
+    //   DIAG bf16:        {a|b<<16}[VEC]               VEC
+    //   COUPLED, v bf16:  g, v pairs[ceil(VEC/2)]      1 + ceil(VEC/2)
+    //   COUPLED, v fp32:  g, v[VEC]                    1 + VEC
+    constexpr int NA = COUPLED ? 1 : (BF16_IN ? 1 : VEC);
+    constexpr int NB = COUPLED ? (BF16_IN ? (VEC + 1) / 2 : VEC) : VEC;
+    static_assert(!(PREFIX && COUPLED), "prefix output is a DIAG-mode option");
+
+    __shared__ int s_pending[2];
+    __shared__ float s_cwA[VW][FW];   // level-1 summaries, then exclusive prefixes over VW
+    __shared__ float s_cwH[VW][FW];
+    __shared__ float s_lbA[NR][FW];
+    __shared__ float s_lbH[NR][FW];
+    __shared__ uint32_t s_lbSt[NR][FW];
+    __shared__ int s_hi[FW];
+    __shared__ float s_inA[FW];
+    __shared__ float s_inH[FW];
+
+    const int blk = blockIdx.x;
+    const int pos = blk / p.G;                 // chunk position along L
+    const int g = blk - pos * p.G;             // chain
+    const int bi = g / p.n_fg;
+    const int fg = g - bi * p.n_fg;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane / FWL;                  // step group of this lane inside its wave
+    const int vw = wave * Q + q;
+    const int flane = (lane % FWL) * VEC;      // first feature of this lane inside the chunk
+    const int64_t fbase = static_cast<int64_t>(fg) * FW;
+    const bool fvalid = fbase + flane < p.D;
+    const int64_t tw = static_cast<int64_t>(pos) * T + static_cast<int64_t>(wave) * (Q * S);
+    const int64_t t0 = tw + q * S;             // first step of this lane
+    const int64_t row0 = static_cast<int64_t>(bi) * p.L;
+    const int Di = static_cast<int>(p.D);      // row stride (checked on the host)
+
+    // The launch epoch is read by every lane before the data loads are issued:
+    // memory counters retire in order, so waiting for it never waits for data.
+    const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_relaxed(&p.hdr[2]));
+
+    // ---- stash: issue every load before any use --------------------------
+    float ra[S][NA];
+    uint32_t rb[S][NB];   // DIAG fp32: float bits of b; bf16: packed {a|b<<16}; COUPLED: v
+    {
+        // wave-uniform row base; lanes add (q*S + s) rows and their feature offset
+        const int64_t wbase = (row0 + tw) * p.D + fbase;
+        const TIn* pa = static_cast<const TIn*>(p.a) + wbase;
+        const TIn* pb = static_cast<const TIn*>(p.b) + wbase;
+        const TZ* pz = nullptr;
+        int gi = 0;
+        if constexpr (COUPLED) {
+            pz = static_cast<const TZ*>(p.a) + (row0 + tw) * p.R;
+            gi = static_cast<int>((fbase + flane) / p.C);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const bool ok = fvalid && (t0 + s < p.L);
+            const int off = (q * S + s) * Di + flane;
+            if constexpr (COUPLED) {
+                if (ok) {
+                    ra[s][0] = IO<TZ>::ld(pz[(q * S + s) * p.R + gi]);   // logit; sigmoid below
+                    if constexpr (BF16_IN) {
+                        uint32_t vb[VEC];
+                        load_bits16<VEC>(pb + off, vb);
+#pragma unroll
+                        for (int j = 0; j < NB; ++j)
+                            rb[s][j] = vb[2 * j] | (2 * j + 1 < VEC ? (vb[2 * j + 1] << 16) : 0u);
+                    } else {
+                        float vf[VEC];
+                        load_stream<TIn, VEC>(pb + off, vf);
+#pragma unroll
+                        for (int j = 0; j < VEC; ++j) rb[s][j] = __float_as_uint(vf[j]);
+                    }
+                } else {
+                    ra[s][0] = 0.0f;   // replaced by the identity marker below
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) rb[s][j] = 0u;
+                }
+            } else if constexpr (BF16_IN) {
+                if (ok) {
+                    uint32_t ab[VEC], bb[VEC];
+                    load_bits16<VEC>(pa + off, ab);
+                    load_bits16<VEC>(pb + off, bb);
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) rb[s][v] = ab[v] | (bb[v] << 16);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) rb[s][v] = 0x3f80u;   // a = 1.0, b = 0.0
+                }
+            } else {
+                if (ok) {
+                    float bf[VEC];
+                    load_stream<TIn, VEC>(pa + off, ra[s]);
+                    load_stream<TIn, VEC>(pb + off, bf);
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) rb[s][v] = __float_as_uint(bf[v]);
+                } else {
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) { ra[s][v] = 1.0f; rb[s][v] = 0u; }
+                }
+            }
+        }
+    }
+
+    // Coupled gate: g = sigmoid(z); out-of-range steps become the identity.
+    if constexpr (COUPLED) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const bool ok = fvalid && (t0 + s < p.L);
+            ra[s][0] = ok ? sigmoidf_(ra[s][0]) : -1.0f;   // -1 marks an identity step
+        }
+    }
+    // Element accessors (fp32 values of a and b for step s, feature v).
+    auto step_a = [&](int s, int v) -> float {
+        if constexpr (COUPLED) return ra[s][0] < 0.0f ? 1.0f : p.damping * (1.0f - ra[s][0]);
+        else if constexpr (BF16_IN) return __uint_as_float(rb[s][v] << 16);
+        else return ra[s][v];
+    };
+    auto step_b = [&](int s, int v) -> float {
+        if constexpr (COUPLED) {
+            const float gg = ra[s][0];
+            if (gg < 0.0f) return 0.0f;
+            float vv;
+            if constexpr (BF16_IN) {
+                const uint32_t w = rb[s][v >> 1];
+                vv = __uint_as_float((v & 1) ? (w & 0xffff0000u) : (w << 16));
+            } else {
+                vv = __uint_as_float(rb[s][v]);
+            }
+            // reference: V_t_raw * value_gate.to(V_t_raw.dtype) in V's dtype
+            const float g_io = IO<TIn>::ld(IO<TIn>::st(gg));
+            return IO<TIn>::ld(IO<TIn>::st(vv * g_io));
+        } else if constexpr (BF16_IN) {
+            return __uint_as_float(rb[s][v] & 0xffff0000u);
+        } else {
+            return __uint_as_float(rb[s][v]);
+        }
+    };
+
+    // ---- level 1: in-lane summary (prod a, h from 0) of the S steps -------
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+        float A = 1.0f, hh = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float av = step_a(s, v);
+            hh = fmaf(av, hh, step_b(s, v));
+            A *= av;
+        }
+        s_cwA[vw][flane + v] = A;
+        s_cwH[vw][flane + v] = hh;
+    }
+    if constexpr (BF16_IN || COUPLED) {
+        // Keep only the compact stash live across the look-back: an empty asm
+        // that "rewrites" it stops the compiler from holding unpacked values.
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) asm volatile("" : "+v"(rb[s][j]));
+            if constexpr (COUPLED) asm volatile("" : "+v"(ra[s][0]));
+        }
+    }
+    if (tid == 0) { s_pending[0] = 0; s_pending[1] = 0; }
+    __syncthreads();
+    // Record that this work-group has read the epoch (after the data arrived,
+    // so no wave waits for this store's acknowledgement before level 1).
+    if (tid == 0) st_relaxed(&p.seen[blk], make_tag(epoch, ST_AGG));
+    const uint32_t tagA = make_tag(epoch, ST_AGG);
+    const uint32_t tagI = make_tag(epoch, ST_INC);
+
+    // ---- level 2: per feature, exclusive prefixes over the step groups and
+    // the chunk aggregate; publish the aggregate ----------------------------
+    uint64_t* PA = p.pay;
+    uint64_t* PH = p.pay + p.plane;
+    const int64_t gbase = static_cast<int64_t>(g) * p.n_ch;
+    float gA = 1.0f, gH = 0.0f;   // chunk aggregate of feature tid (tid < FW)
+    if (tid < FW) {
+#pragma unroll 8
+        for (int w = 0; w < VW; ++w) {
+            const float A = s_cwA[w][tid];
+            const float H = s_cwH[w][tid];
+            s_cwA[w][tid] = gA;
+            s_cwH[w][tid] = gH;
+            gH = fmaf(A, gH, H);
+            gA *= A;
+        }
+        const int64_t me = (gbase + pos) * FW + tid;
+        const uint32_t tg = pos == 0 ? tagI : tagA;
+        st_relaxed(&PA[me], pack_word(gA, tg));
+        st_relaxed(&PH[me], pack_word(gH, tg));
+        s_hi[tid] = pos - 1;   // -1: nothing to look back over
+        if (pos == 0) { s_inA[tid] = 1.0f; s_inH[tid] = 0.0f; }
+    }
+
+    // ---- level 3: look-back over the predecessors of this chain ----------
+    if (pos > 0) {
+        float cA = 1.0f, cH = 0.0f;   // composite of the folded predecessors, per feature
+        const int f = tid % FW;
+        const int r = tid / FW;
+        uint32_t rounds = 0;
+        for (int par = 0;; par ^= 1) {
+            __syncthreads();   // s_hi of the previous round visible; s_pending[par] cleared
+            const int hi = s_hi[f];
+            if (hi >= 0 && hi - r >= 0) {
+                const int64_t idx = (gbase + hi - r) * FW + f;
+                const uint64_t wA = ld_relaxed(&PA[idx]);
+                const uint64_t wH = ld_relaxed(&PH[idx]);
+                const uint32_t ta = word_tag(wA), th = word_tag(wH);
+                s_lbSt[r][f] = (ta == th && (ta == tagI || ta == tagA)) ? (ta & 3u) : ST_NONE;
+                s_lbA[r][f] = word_val(wA);
+                s_lbH[r][f] = word_val(wH);
+            }
+            if (tid == 0) s_pending[par ^ 1] = 0;
+            __syncthreads();
+            if (tid < FW && hi >= 0) {
+                int rr = 0;
+                bool done = false;
+                for (; rr < NR && hi - rr >= 0; ++rr) {
+                    const uint32_t st = s_lbSt[rr][tid];
+                    if (st == ST_NONE) break;
+                    cH = fmaf(cA, s_lbH[rr][tid], cH);
+                    cA *= s_lbA[rr][tid];
+                    if (st == ST_INC) { done = true; break; }
+                }
+                s_hi[tid] = done ? -1 : hi - rr;
+                if (!done) s_pending[par] = 1;
+            }
+            __syncthreads();
+            if (!s_pending[par]) break;
+            if (++rounds > MAX_SPIN) {
+                if (tid == 0) note_timeout(p.hdr);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (tid < FW) {
+            s_inA[tid] = cA;
+            s_inH[tid] = cH;
+            const int64_t me = (gbase + pos) * FW + tid;
+            st_relaxed(&PA[me], pack_word(gA * cA, tagI));
+            st_relaxed(&PH[me], pack_word(fmaf(gA, cH, gH), tagI));
+        }
+    }
+    __syncthreads();
+
+    // ---- output: state entering this step group, re-run the steps, write h
+    {
+        float hh[VEC], Ap[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+            const float cwA = s_cwA[vw][flane + v];
+            hh[v] = fmaf(cwA, s_inH[flane + v], s_cwH[vw][flane + v]);
+            Ap[v] = cwA * s_inA[flane + v];
+        }
+        const int64_t wbase = (row0 + tw) * p.D + fbase;
+        TOut* ph = static_cast<TOut*>(p.h) + wbase;
+        TOut* pp = PREFIX ? static_cast<TOut*>(p.aprefix) + wbase : nullptr;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            float o[VEC];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+                const float av = step_a(s, v);
+                hh[v] = fmaf(av, hh[v], step_b(s, v));
+                if constexpr (PREFIX) Ap[v] *= av;
+                o[v] = hh[v];
+            }
+            if (fvalid && t0 + s < p.L) {
+                const int off = (q * S + s) * Di + flane;
+                store_stream<TOut, VEC>(ph + off, o);
+                if constexpr (PREFIX) {
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) o[v] = Ap[v];
+                    store_stream<TOut, VEC>(pp + off, o);
+                }
+            }
+        }
+    }
+
+    // ---- last work-group: advance the epoch once every chunk has read it --
+    if (blk == static_cast<int>(gridDim.x) - 1) {
+        const int64_t n = static_cast<int64_t>(p.G) * p.n_ch;
+        const uint32_t want = make_tag(epoch, ST_AGG);
+        for (int64_t i = tid; i < n; i += NT) {
+            uint32_t spins = 0;
+            while (ld_relaxed(&p.seen[i]) != want) {
+                if (++spins > MAX_SPIN) {
+                    note_timeout(p.hdr);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+        if (tid == 0) st_relaxed(&p.hdr[2], (epoch + 1u) & 0x3fffffffu);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: geometry and launch of one tile configuration.
+// ---------------------------------------------------------------------------
+struct DiagTile { int vec, lanes, steps, waves; };   // lanes per row: 64, 32 or 16
+
+struct DiagGeometry {
+    int n_fg, n_ch, G;
+    int64_t plane;
+    size_t seen_bytes, bytes;
+};
+
+inline DiagGeometry diag_geometry(int64_t B, int64_t L, int64_t D, const DiagTile& t) {
+    DiagGeometry g{};
+    const int64_t FW = static_cast<int64_t>(t.lanes) * t.vec;
+    const int64_t T = static_cast<int64_t>(t.steps) * t.waves * (64 / t.lanes);
+    g.n_fg = static_cast<int>((D + FW - 1) / FW);
+    g.n_ch = static_cast<int>((L + T - 1) / T);
+    g.G = static_cast<int>(B * g.n_fg);
+    g.plane = static_cast<int64_t>(g.G) * g.n_ch * FW;
+    g.seen_bytes = round_up(static_cast<size_t>(g.G) * g.n_ch * sizeof(uint32_t), 256);
+    g.bytes = WS_HDR_BYTES + g.seen_bytes + 2 * static_cast<size_t>(g.plane) * sizeof(uint64_t);
+    return g;
+}
+
+inline int64_t diag_groups(int64_t B, int64_t L, int64_t D, const DiagTile& t) {
+    const DiagGeometry g = diag_geometry(B, L, D, t);
+    return static_cast<int64_t>(g.G) * g.n_ch;
+}
+
+// First tile of a preference list (longest chunks first) with at least 128
+// work-groups; else the last (shortest).  Measured at D = 768, L = 8192: 192
+// long chunks (fewer than the 256 CUs) beat 768 short ones, because short
+// chunks put more chunks of one chain in flight and lengthen the look-back.
+inline DiagTile pick_tile(int64_t B, int64_t L, int64_t D, const DiagTile* list, int n) {
+    for (int i = 0; i < n - 1; ++i)
+        if (diag_groups(B, L, D, list[i]) >= 128) return list[i];
+    return list[n - 1];
+}
+
+// Shape checks shared by every entry point; fills prm (except tensor pointers).
+inline int diag_prepare(DiagParams& prm, int64_t B, int64_t L, int64_t D, const DiagTile& t,
+                        void* ws, size_t ws_bytes) {
+    const DiagGeometry geo = diag_geometry(B, L, D, t);
+    if (static_cast<int64_t>(geo.G) * geo.n_ch > 0x7fffffffLL ||
+        D > (1LL << 31) / (static_cast<int64_t>(t.steps) * (64 / t.lanes) + 1))
+        return set_error(MOGT_E_INVALID, "problem too large for one launch");
+    if (!ws || ws_bytes < geo.bytes)
+        return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", geo.bytes,
+                         ws_bytes);
+    prm.L = L;
+    prm.D = D;
+    prm.n_fg = geo.n_fg;
+    prm.n_ch = geo.n_ch;
+    prm.G = geo.G;
+    char* base = static_cast<char*>(ws);
+    prm.hdr = reinterpret_cast<uint32_t*>(base);
+    prm.seen = reinterpret_cast<uint32_t*>(base + WS_HDR_BYTES);
+    prm.pay = reinterpret_cast<uint64_t*>(base + WS_HDR_BYTES + geo.seen_bytes);
+    prm.plane = geo.plane;
+    return MOGT_OK;
+}
+
+template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
+          bool PREFIX>
+int diag_launch(const DiagParams& prm, hipStream_t stream) {
+    const int grid = prm.G * prm.n_ch;
+    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX>), dim3(grid),
+                       dim3(64 * WT), 0, stream, prm);
+    return check_launch("diag_scan_kernel");
+}
+
+// Tile configurations compiled into the library (features per lane, lanes per
+// row, steps per lane, waves per work-group), per input family.  Every tile
+// keeps rows of at least 256 contiguous bytes (narrower rows cost HBM
+// efficiency) and at most 64 stash registers per lane.
+#define MOGT_DIAG_F32_TILES(X) X(2, 32, 16, 16) X(1, 64, 32, 16) X(2, 32, 8, 16) X(1, 64, 16, 16) X(1, 64, 8, 16) X(2, 64, 16, 16)
+#define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 16) X(4, 64, 8, 16) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_COUPLED_TILES(X) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+
+// Per-family launchers (diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
+int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,
+                   hipStream_t stream);
+int diag_run_bf16in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,
+                    hipStream_t stream);
+bool diag_tile_compiled(int family, const DiagTile& t);   // family: 0 f32, 1 bf16, 2 coupled
+
+}  // namespace mogt

@@ -1,532 +1,87 @@
-// Single-pass diagonal affine scan h_t = a_t * h_{t-1} + b_t for gfx950.
-//
-// Semantics follow the reference's sequential recurrence (affine_scan.py:48-55,
-// H_0 = 0, fp32 state, outputs cast at the end) in the per-feature R=C=1 case,
-// and the coupled write-forget gate of the MOGT mixer (model_mogt.py:166-182).
-//
-// Design (one launch, 3 HBM streams: read a, read b, write h):
-//   tile     one work-group = WT waves x 64 lanes.  A lane owns VEC consecutive
-//            features (one VEC-wide vector load/store per row, rows contiguous
-//            along D), a wave owns S consecutive steps of them; the WT waves of
-//            a group cover T = WT*S consecutive steps of the same FW = 64*VEC
-//            features.
-//   level 1  each lane scans its S steps serially in registers (2 FMA/element).
-//   level 2  wave summaries (prod a, h_end) go through LDS; each wave folds the
-//            summaries of the waves before it to get its in-chunk carry.
-//   level 3  chunks of one feature group are chained with a decoupled look-back
-//            (tagged 64-bit words, see common.h; chunk id = blockIdx.x, chunk-
-//            major over the feature groups): publish the chunk aggregate,
-//            fold predecessors' aggregates until an inclusive prefix is found,
-//            publish the inclusive prefix, then apply the carry in registers and
-//            write h once.
-#include <type_traits>
-
-#include "common.h"
+// C entry points of the single-pass diagonal affine scan (kernel: diag_kernel.h;
+// instantiations: diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
+#include "diag_kernel.h"
 
 namespace mogt {
 
-struct DiagParams {
-    const void* a;      // [B, L, D] (DIAG)            | gate logits z [B, L, R] (COUPLED)
-    const void* b;      // [B, L, D]                    | v [B, L, D]
-    void* h;            // [B, L, D]
-    void* aprefix;      // [B, L, D] or null
-    int64_t L, D;
-    int n_fg;           // feature groups per batch row
-    int n_ch;           // chunks along L
-    int G;              // B * n_fg look-back chains
-    int R, C;           // COUPLED: gate count and channels per gate (D = R*C)
-    float damping;      // COUPLED: connection damping (identity connection scale)
-    uint32_t* hdr;
-    uint32_t* flags;    // [G][n_ch]
-    uint64_t* pay;      // 4 planes of [G][n_ch][FW] words: aggA, aggH, incA, incH
-    int64_t plane;      // words per plane
-};
-
-template <typename TIn, typename TZ, typename TOut, int VEC, int S, int WT, bool PREFIX,
-          bool COUPLED>
-__global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
-    constexpr int NT = 64 * WT;
-    constexpr int FW = 64 * VEC;
-    constexpr int T = WT * S;
-    static_assert(FW <= NT, "look-back needs one thread per feature of the group");
-
-    __shared__ uint32_t s_epoch;
-    __shared__ float s_sumA[WT][FW];
-    __shared__ float s_sumH[WT][FW];
-    __shared__ float s_inA[FW];
-    __shared__ float s_inH[FW];
-    __shared__ float s_partA[NT];
-    __shared__ float s_partH[NT];
-    __shared__ int s_nfold, s_found;
-
-    const uint32_t epoch = ws_epoch(p.hdr, &s_epoch);
-    const int blk = blockIdx.x;
-    const int chunk = blk / p.G;
-    const int g = blk - chunk * p.G;
-    const int bi = g / p.n_fg;
-    const int fg = g - bi * p.n_fg;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (SGPR)
-    const int64_t fbase = static_cast<int64_t>(fg) * FW;          // first feature of the group
-    const int flane = lane * VEC;                                  // lane offset inside the group
-    const bool fvalid = fbase + flane < p.D;
-    const int64_t t0 = static_cast<int64_t>(chunk) * T + wave * S;
-    const int64_t row0 = static_cast<int64_t>(bi) * p.L;
-    // Wave-uniform row pointers; lanes only add their 32-bit feature offset.
-    const int64_t rowoff0 = (row0 + t0) * p.D + fbase;
-
-    // ---- load (all loads issued before any use) -------------------------
-    // The raw per-step inputs stay in registers until the carry is known; the
-    // outputs are then produced by re-running the recurrence from the carry
-    // (same arithmetic order as the sequential reference).  bf16 inputs are
-    // kept as packed bit pairs (one VGPR per step), halving register use.
-    constexpr bool PACKED = !COUPLED && std::is_same<TIn, bf16_t>::value;
-    float ra[PACKED ? 1 : S][VEC], rb[PACKED ? 1 : S][VEC];
-    uint32_t pk[PACKED ? S : 1][VEC];
-    {
-        const TIn* pa = static_cast<const TIn*>(COUPLED ? p.b : p.a) + rowoff0;
-        const TIn* pb = static_cast<const TIn*>(p.b) + rowoff0;
-        const TZ* pz = COUPLED ? static_cast<const TZ*>(p.a) + (row0 + t0) * p.R : nullptr;
-        const int gi = COUPLED ? static_cast<int>((fbase + flane) / p.C) : 0;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const bool tvalid = t0 + s < p.L;   // wave-uniform
-            if (fvalid && tvalid) {
-                if constexpr (COUPLED) {
-                    const float zz = IO<TZ>::ld(pz[gi]);
-                    float vv[VEC];
-                    load_stream<TIn, VEC>(pb + flane, vv);
-                    const float gate = sigmoidf_(zz);
-                    // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)
-                    const float gate_io = IO<TIn>::ld(IO<TIn>::st(gate));
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) {
-                        ra[s][v] = p.damping * (1.0f - gate);
-                        rb[s][v] = IO<TIn>::ld(IO<TIn>::st(vv[v] * gate_io));
-                    }
-                } else if constexpr (PACKED) {
-                    uint32_t ab[VEC], bb[VEC];
-                    load_bits16<VEC>(pa + flane, ab);
-                    load_bits16<VEC>(pb + flane, bb);
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) pk[s][v] = ab[v] | (bb[v] << 16);
-                } else {
-                    load_stream<TIn, VEC>(pa + flane, ra[s]);
-                    load_stream<TIn, VEC>(pb + flane, rb[s]);
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) {
-                    if constexpr (PACKED) pk[s][v] = 0x3f80u;   // a = 1.0, b = 0.0
-                    else { ra[s][v] = 1.0f; rb[s][v] = 0.0f; }
-                }
-            }
-            pa += p.D;
-            pb += p.D;
-            if constexpr (COUPLED) pz += p.R;
-        }
-    }
-    auto step_a = [&](int s, int v) -> float {
-        if constexpr (PACKED) return __uint_as_float(pk[s][v] << 16);
-        else return ra[s][v];
-    };
-    auto step_b = [&](int s, int v) -> float {
-        if constexpr (PACKED) return __uint_as_float(pk[s][v] & 0xffff0000u);
-        else return rb[s][v];
-    };
-
-    // ---- level 1: in-lane summary (prod a, h_end) of the S steps ---------
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-        float A = 1.0f, hh = 0.0f;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const float av = step_a(s, v);
-            hh = fmaf(av, hh, step_b(s, v));
-            A *= av;
-        }
-        s_sumA[wave][lane * VEC + v] = A;
-        s_sumH[wave][lane * VEC + v] = hh;
-    }
-    if constexpr (PACKED) {
-        // Keep only the packed words live across the look-back: an empty asm
-        // that "rewrites" them stops the compiler from holding the unpacked
-        // floats of the first pass until the second.
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) asm volatile("" : "+v"(pk[s][v]));
-    }
-    __syncthreads();
-
-    // ---- level 2: carry into this wave from the waves before it ---------
-    float cwA[VEC], cwH[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) { cwA[v] = 1.0f; cwH[v] = 0.0f; }
-#pragma unroll
-    for (int w = 0; w < WT - 1; ++w) {
-        if (w < wave) {
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) {
-                const float A = s_sumA[w][lane * VEC + v];
-                cwH[v] = fmaf(A, cwH[v], s_sumH[w][lane * VEC + v]);
-                cwA[v] *= A;
-            }
-        }
-    }
-
-    // ---- level 3: decoupled look-back over chunks of this feature group --
-    const uint32_t tagA = make_tag(epoch, ST_AGG);
-    const uint32_t tagI = make_tag(epoch, ST_INC);
-    uint64_t* aggA = p.pay;
-    uint64_t* aggH = p.pay + p.plane;
-    uint64_t* incA = p.pay + 2 * p.plane;
-    uint64_t* incH = p.pay + 3 * p.plane;
-    const int64_t gbase = static_cast<int64_t>(g) * p.n_ch;   // chunk-row of this chain
-
-    float gA = 1.0f, gH = 0.0f;   // chunk aggregate of feature `tid`
-    if (tid < FW) {
-#pragma unroll
-        for (int w = 0; w < WT; ++w) {
-            const float A = s_sumA[w][tid];
-            gH = fmaf(A, gH, s_sumH[w][tid]);
-            gA *= A;
-        }
-        const int64_t idx = (gbase + chunk) * FW + tid;
-        if (chunk == 0) {
-            st_relaxed(&incA[idx], pack_word(gA, tagI));
-            st_relaxed(&incH[idx], pack_word(gH, tagI));
-            s_inA[tid] = 1.0f;
-            s_inH[tid] = 0.0f;
-        } else {
-            st_relaxed(&aggA[idx], pack_word(gA, tagA));
-            st_relaxed(&aggH[idx], pack_word(gH, tagA));
-        }
-    }
-    __syncthreads();
-    if (tid == 0) st_relaxed(&p.flags[gbase + chunk], make_tag(epoch, chunk == 0 ? ST_INC : ST_AGG));
-
-    if (chunk > 0) {
-        float cA = 1.0f, cH = 0.0f;   // composite of folded aggregates (threads tid < FW)
-        int p_hi = chunk - 1;
-        while (true) {
-            if (wave == 0) {
-                // Poll up to 64 predecessor flags at once (lane i <-> chunk p_hi - i).
-                uint32_t spins = 0;
-                while (true) {
-                    const int pc = p_hi - lane;
-                    uint32_t st = 0;
-                    if (pc >= 0) {
-                        const uint32_t w = ld_relaxed(&p.flags[gbase + pc]);
-                        st = ((w >> 2) == epoch) ? (w & 3u) : 0u;
-                    }
-                    const uint64_t inc_m = __ballot(pc >= 0 && st == ST_INC);
-                    const uint64_t nr_m = __ballot(pc >= 0 && st == 0u);
-                    bool ok;
-                    int nf, found;
-                    if (inc_m) {
-                        const int j = __ffsll(static_cast<long long>(inc_m)) - 1;
-                        const uint64_t below = (j == 0) ? 0ull : ((1ull << j) - 1ull);
-                        ok = (nr_m & below) == 0ull;
-                        nf = j;
-                        found = 1;
-                    } else {
-                        ok = (nr_m == 0ull);
-                        nf = 64;
-                        found = 0;
-                    }
-                    if (!ok && ++spins > MAX_SPIN) {
-                        // Give up: fold whatever is there; hdr[3] marks the result invalid.
-                        if (lane == 0) note_timeout(p.hdr);
-                        ok = true;
-                        if (!inc_m) { nf = p_hi + 1 < 64 ? p_hi + 1 : 64; found = 0; }
-                        if (p_hi - nf < 0) { nf = p_hi; found = 1; }
-                    }
-                    if (ok) {
-                        if (lane == 0) { s_nfold = nf; s_found = found; }
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-            }
-            __syncthreads();
-            const int nf = s_nfold;
-            const int found = s_found;
-            {
-                // Fold the aggregates of chunks p_hi, ..., p_hi-nf+1 (newest first) and,
-                // if found, the inclusive prefix of chunk p_hi-nf.  The window is split
-                // into NR contiguous slices folded concurrently (feature f = tid % FW,
-                // slice r = tid / FW), each issuing all its loads before the first use,
-                // so one window costs about one memory round trip.
-                constexpr int NR = NT / FW;
-                constexpr int BATCH = 4;
-                const int f = tid % FW;
-                const int r = tid / FW;
-                const int per = (nf + NR - 1) / NR;
-                const int q_lo = r * per;
-                const int q_hi = min(nf, q_lo + per);
-                const int64_t iidx = (gbase + p_hi - nf) * FW + f;
-                uint64_t iwA = 0, iwH = 0;
-                if (found && r == 0) {
-                    iwA = ld_relaxed(&incA[iidx]);
-                    iwH = ld_relaxed(&incH[iidx]);
-                }
-                float rA = 1.0f, rH = 0.0f;
-                for (int q0 = q_lo; q0 < q_hi; q0 += BATCH) {
-                    uint64_t wA[BATCH], wH[BATCH];
-#pragma unroll
-                    for (int q = 0; q < BATCH; ++q) {
-                        if (q0 + q < q_hi) {
-                            const int64_t idx = (gbase + p_hi - q0 - q) * FW + f;
-                            wA[q] = ld_relaxed(&aggA[idx]);
-                            wH[q] = ld_relaxed(&aggH[idx]);
-                        }
-                    }
-#pragma unroll
-                    for (int q = 0; q < BATCH; ++q) {
-                        if (q0 + q < q_hi) {
-                            const int64_t idx = (gbase + p_hi - q0 - q) * FW + f;
-                            const float A = word_tag(wA[q]) == tagA ? word_val(wA[q])
-                                                                    : wait_word(&aggA[idx], tagA, p.hdr);
-                            const float H = word_tag(wH[q]) == tagA ? word_val(wH[q])
-                                                                    : wait_word(&aggH[idx], tagA, p.hdr);
-                            rH = fmaf(rA, H, rH);
-                            rA *= A;
-                        }
-                    }
-                }
-                if constexpr (NR > 1) {
-                    s_partA[tid] = rA;
-                    s_partH[tid] = rH;
-                    __syncthreads();
-                }
-                if (r == 0) {
-                    if constexpr (NR > 1) {
-#pragma unroll
-                        for (int rr = 0; rr < NR; ++rr) {
-                            cH = fmaf(cA, s_partH[rr * FW + f], cH);
-                            cA *= s_partA[rr * FW + f];
-                        }
-                    } else {
-                        cH = fmaf(cA, rH, cH);
-                        cA *= rA;
-                    }
-                    if (found) {
-                        const float iA = word_tag(iwA) == tagI ? word_val(iwA)
-                                                               : wait_word(&incA[iidx], tagI, p.hdr);
-                        const float iH = word_tag(iwH) == tagI ? word_val(iwH)
-                                                               : wait_word(&incH[iidx], tagI, p.hdr);
-                        const float inH = fmaf(cA, iH, cH);
-                        const float inA = cA * iA;
-                        s_inA[f] = inA;
-                        s_inH[f] = inH;
-                        const int64_t me = (gbase + chunk) * FW + f;
-                        st_relaxed(&incA[me], pack_word(gA * inA, tagI));
-                        st_relaxed(&incH[me], pack_word(fmaf(gA, inH, gH), tagI));
-                    }
-                }
-            }
-            if (found) break;
-            p_hi -= nf;
-            __syncthreads();   // s_nfold/s_found are rewritten by the next poll
-        }
-        __syncthreads();
-        if (tid == 0) st_relaxed(&p.flags[gbase + chunk], make_tag(epoch, ST_INC));
-    } else {
-        __syncthreads();
-    }
-
-    // ---- apply carry and write each output once -------------------------
-    float stH[VEC], stA[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-        const float inH = s_inH[lane * VEC + v];
-        const float inA = s_inA[lane * VEC + v];
-        stH[v] = fmaf(cwA[v], inH, cwH[v]);
-        stA[v] = cwA[v] * inA;
-    }
-    {
-        TOut* ph = static_cast<TOut*>(p.h) + rowoff0;
-        TOut* pp = PREFIX ? static_cast<TOut*>(p.aprefix) + rowoff0 : nullptr;
-        float hh[VEC], Ap[VEC];
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) { hh[v] = stH[v]; Ap[v] = stA[v]; }
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            float o[VEC];
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) {
-                const float av = step_a(s, v);
-                hh[v] = fmaf(av, hh[v], step_b(s, v));
-                if constexpr (PREFIX) Ap[v] *= av;
-                o[v] = hh[v];
-            }
-            if (fvalid && t0 + s < p.L) {
-                store_stream<TOut, VEC>(ph + flane, o);
-                if constexpr (PREFIX) {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) o[v] = Ap[v];
-                    store_stream<TOut, VEC>(pp + flane, o);
-                }
-            }
-            ph += p.D;
-            if constexpr (PREFIX) pp += p.D;
-        }
-    }
-
-    ws_finish(p.hdr, p.flags, static_cast<int64_t>(p.G) * p.n_ch, epoch);
-}
-
-// ---------------------------------------------------------------------------
-// Host side
-// ---------------------------------------------------------------------------
-namespace {
-
-struct TileCfg { int vec, steps, waves; };
-
-// Tile configurations compiled into the library (vec, steps, waves).
-constexpr TileCfg kCfgs[] = {
-    {1, 32, 16}, {1, 64, 16}, {1, 48, 16}, {1, 40, 8}, {1, 32, 8}, {1, 16, 8},
-    {2, 32, 16}, {2, 16, 8}, {4, 16, 8}, {4, 8, 8},
-};
-
-bool cfg_known(int vec, int steps, int waves) {
-    for (const auto& c : kCfgs)
-        if (c.vec == vec && c.steps == steps && c.waves == waves) return true;
+bool diag_tile_compiled(int family, const DiagTile& t) {
+#define MOGT_MATCH(V_, F_, S_, W_) \
+    if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) return true;
+    if (family == 0) { MOGT_DIAG_F32_TILES(MOGT_MATCH) }
+    if (family == 1) { MOGT_DIAG_BF16_TILES(MOGT_MATCH) }
+    if (family == 2) { MOGT_COUPLED_TILES(MOGT_MATCH) }
+#undef MOGT_MATCH
     return false;
 }
 
-struct Geometry {
-    int n_fg, n_ch, G;
-    int64_t plane;
-    size_t flags_bytes, bytes;
-};
-
-Geometry geometry(int64_t B, int64_t L, int64_t D, int vec, int steps, int waves) {
-    Geometry g{};
-    const int64_t FW = 64 * vec;
-    const int64_t T = static_cast<int64_t>(steps) * waves;
-    g.n_fg = static_cast<int>((D + FW - 1) / FW);
-    g.n_ch = static_cast<int>((L + T - 1) / T);
-    g.G = static_cast<int>(B * g.n_fg);
-    g.plane = static_cast<int64_t>(g.G) * g.n_ch * FW;
-    g.flags_bytes = round_up(static_cast<size_t>(g.G) * g.n_ch * sizeof(uint32_t), 256);
-    g.bytes = WS_HDR_BYTES + g.flags_bytes + 4 * static_cast<size_t>(g.plane) * sizeof(uint64_t);
-    return g;
-}
-
-template <typename TIn, typename TZ, typename TOut, int VEC, int S, int WT, bool PREFIX, bool COUPLED>
-int launch_one(const DiagParams& prm, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((diag_scan_kernel<TIn, TZ, TOut, VEC, S, WT, PREFIX, COUPLED>), dim3(grid),
-                       dim3(64 * WT), 0, stream, prm);
-    return check_launch("diag_scan_kernel");
-}
-
-template <typename TIn, typename TZ, typename TOut, bool PREFIX, bool COUPLED>
-int launch_cfg(const DiagParams& prm, int grid, int vec, int steps, int waves, hipStream_t st) {
-#define MOGT_DIAG_CASE(V_, S_, W_)                                                     \
-    if (vec == V_ && steps == S_ && waves == W_)                                        \
-        return launch_one<TIn, TZ, TOut, V_, S_, W_, PREFIX, COUPLED>(prm, grid, st);
-    MOGT_DIAG_CASE(1, 32, 16)
-    MOGT_DIAG_CASE(1, 64, 16)
-    MOGT_DIAG_CASE(1, 48, 16)
-    MOGT_DIAG_CASE(1, 40, 8)
-    MOGT_DIAG_CASE(1, 32, 8)
-    MOGT_DIAG_CASE(1, 16, 8)
-    MOGT_DIAG_CASE(2, 32, 16)
-    MOGT_DIAG_CASE(2, 16, 8)
-    MOGT_DIAG_CASE(4, 16, 8)
-    MOGT_DIAG_CASE(4, 8, 8)
-#undef MOGT_DIAG_CASE
-    return set_error(MOGT_E_INVALID, "diag scan: tile (vec=%d, steps=%d, waves=%d) not compiled", vec,
-                     steps, waves);
-}
-
-// Default tile (measured on MI355X, D = 768, L = 8k..32k): fp32 I/O runs best
-// with one feature per lane (256 B coalesced rows per wave) and 512-step chunks
-// (16 waves x 32 steps), which keeps look-back chains at L/512 links; bf16
-// I/O with two features per lane (4-byte loads, 256 B rows).  Small problems
-// fall back to 128-step chunks so the grid still fills the GPU.
-int64_t n_groups(int64_t B, int64_t L, int64_t D, const TileCfg& c) {
-    const int64_t FW = 64 * c.vec;
-    const int64_t T = static_cast<int64_t>(c.steps) * c.waves;
-    return B * ((D + FW - 1) / FW) * ((L + T - 1) / T);
-}
-
-TileCfg default_cfg(int64_t B, int64_t L, int64_t D, bool bf16_in, bool vec2_aligned) {
-    if (bf16_in && D % 2 == 0 && vec2_aligned) {
-        const TileCfg big{2, 32, 16};
-        if (n_groups(B, L, D, big) >= 192) return big;
-        return {2, 16, 8};
-    }
-    const TileCfg big{1, 32, 16};
-    if (n_groups(B, L, D, big) >= 128) return big;
-    return {1, 16, 8};
-}
+namespace {
 
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 
+// Default tile (measured on MI355X, B = 1, D = 768, L = 8k..32k): chunks of
+// 512 steps x 64 features, rows of 256 B.  fp32: two features per lane, 32
+// lanes per row; bf16: four features per lane, 16 lanes per row (the packed
+// stash holds both inputs in one register per element).  Vectors need D to be
+// a multiple of the vector and aligned pointers; short problems fall back to
+// shorter chunks so the grid still covers the GPU.
+DiagTile default_tile(int64_t B, int64_t L, int64_t D, bool bf16_in, int align_elems) {
+    if (bf16_in) {
+        static const DiagTile v4[] = {{4, 16, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
+        static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
+        static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
+        if (D % 4 == 0 && align_elems % 4 == 0) return pick_tile(B, L, D, v4, 3);
+        if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 3);
+        return pick_tile(B, L, D, v1, 3);
+    }
+    static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
+    static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
+    if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 3);
+    return pick_tile(B, L, D, v1, 3);
+}
+
 int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, int64_t L,
-             int64_t D, int R, int C, float damping, int in_dtype, int z_dtype, int out_dtype,
-             bool coupled, int vec, int steps, int waves, void* ws, size_t ws_bytes,
+             int64_t D, int in_dtype, int out_dtype, const DiagTile& t, void* ws, size_t ws_bytes,
              void* stream) {
     clear_error();
     if (B < 0 || L < 0 || D < 0) return set_error(MOGT_E_INVALID, "negative size");
-    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype) || !dtype_ok(z_dtype))
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
         return set_error(MOGT_E_INVALID, "unsupported dtype code");
     if (B == 0 || L == 0 || D == 0) return MOGT_OK;
     if (!a || !b || !h) return set_error(MOGT_E_INVALID, "null tensor pointer");
-    if (!cfg_known(vec, steps, waves))
-        return set_error(MOGT_E_INVALID, "diag scan: tile (%d,%d,%d) not compiled", vec, steps, waves);
-    if (D % vec != 0) return set_error(MOGT_E_INVALID, "features %lld not a multiple of vec %d",
-                                       (long long)D, vec);
-    if (coupled && C % vec != 0)
-        return set_error(MOGT_E_INVALID, "channels %d not a multiple of vec %d", C, vec);
-    const Geometry geo = geometry(B, L, D, vec, steps, waves);
-    if (static_cast<int64_t>(geo.G) * geo.n_ch > 0x7fffffffLL)
-        return set_error(MOGT_E_INVALID, "problem too large for one launch");
-    if (!ws || ws_bytes < geo.bytes)
-        return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", geo.bytes,
-                         ws_bytes);
-
+    const int family = in_dtype == MOGT_BF16 ? 1 : 0;
+    if (!diag_tile_compiled(family, t))
+        return set_error(MOGT_E_INVALID, "diag scan: tile (%d,%d,%d,%d) not compiled", t.vec,
+                         t.lanes, t.steps, t.waves);
+    if (D % t.vec != 0)
+        return set_error(MOGT_E_INVALID, "features %lld not a multiple of vec %d", (long long)D,
+                         t.vec);
     DiagParams prm{};
-    prm.a = a; prm.b = b; prm.h = h; prm.aprefix = aprefix;
-    prm.L = L; prm.D = D;
-    prm.n_fg = geo.n_fg; prm.n_ch = geo.n_ch; prm.G = geo.G;
-    prm.R = R; prm.C = C; prm.damping = damping;
-    char* base = static_cast<char*>(ws);
-    prm.hdr = reinterpret_cast<uint32_t*>(base);
-    prm.flags = reinterpret_cast<uint32_t*>(base + WS_HDR_BYTES);
-    prm.pay = reinterpret_cast<uint64_t*>(base + WS_HDR_BYTES + geo.flags_bytes);
-    prm.plane = geo.plane;
-    const int grid = geo.G * geo.n_ch;
+    const int rc = diag_prepare(prm, B, L, D, t, ws, ws_bytes);
+    if (rc) return rc;
+    prm.a = a;
+    prm.b = b;
+    prm.h = h;
+    prm.aprefix = aprefix;
+    prm.R = 1;
+    prm.C = 1;
+    prm.damping = 1.0f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool pre = aprefix != nullptr;
+    return family == 1 ? diag_run_bf16in(prm, t, out_dtype, pre, st)
+                       : diag_run_f32in(prm, t, out_dtype, pre, st);
+}
 
-#define MOGT_DT(TI, TZ_, TO)                                                                   \
-    if (coupled) return launch_cfg<TI, TZ_, TO, false, true>(prm, grid, vec, steps, waves, st); \
-    if (pre) return launch_cfg<TI, TZ_, TO, true, false>(prm, grid, vec, steps, waves, st);     \
-    return launch_cfg<TI, TZ_, TO, false, false>(prm, grid, vec, steps, waves, st);
-
-    if (coupled) {
-        if (in_dtype == MOGT_BF16 && z_dtype == MOGT_F32 && out_dtype == MOGT_F32) { MOGT_DT(bf16_t, float, float) }
-        if (in_dtype == MOGT_BF16 && z_dtype == MOGT_BF16 && out_dtype == MOGT_F32) { MOGT_DT(bf16_t, bf16_t, float) }
-        if (in_dtype == MOGT_BF16 && z_dtype == MOGT_F32 && out_dtype == MOGT_BF16) { MOGT_DT(bf16_t, float, bf16_t) }
-        if (in_dtype == MOGT_BF16 && z_dtype == MOGT_BF16 && out_dtype == MOGT_BF16) { MOGT_DT(bf16_t, bf16_t, bf16_t) }
-        if (in_dtype == MOGT_F32 && z_dtype == MOGT_F32 && out_dtype == MOGT_F32) { MOGT_DT(float, float, float) }
-        if (in_dtype == MOGT_F32 && z_dtype == MOGT_BF16 && out_dtype == MOGT_F32) { MOGT_DT(float, bf16_t, float) }
-        if (in_dtype == MOGT_F32 && z_dtype == MOGT_F32 && out_dtype == MOGT_BF16) { MOGT_DT(float, float, bf16_t) }
-        if (in_dtype == MOGT_F32 && z_dtype == MOGT_BF16 && out_dtype == MOGT_BF16) { MOGT_DT(float, bf16_t, bf16_t) }
-    } else {
-        if (in_dtype == MOGT_F32 && out_dtype == MOGT_F32) { MOGT_DT(float, float, float) }
-        if (in_dtype == MOGT_F32 && out_dtype == MOGT_BF16) { MOGT_DT(float, float, bf16_t) }
-        if (in_dtype == MOGT_BF16 && out_dtype == MOGT_F32) { MOGT_DT(bf16_t, float, float) }
-        if (in_dtype == MOGT_BF16 && out_dtype == MOGT_BF16) { MOGT_DT(bf16_t, float, bf16_t) }
+// Largest vector width (in elements, 4, 2 or 1) every pointer is aligned to.
+int common_alignment(const void* a, const void* b, const void* h, const void* p, int in_dtype,
+                     int out_dtype) {
+    const uintptr_t ie = in_dtype == MOGT_BF16 ? 2 : 4, oe = out_dtype == MOGT_BF16 ? 2 : 4;
+    for (int v : {4, 2}) {
+        auto ok = [&](const void* ptr, uintptr_t es) {
+            return ptr == nullptr || reinterpret_cast<uintptr_t>(ptr) % (es * v) == 0;
+        };
+        if (ok(a, ie) && ok(b, ie) && ok(h, oe) && ok(p, oe)) return v;
     }
-#undef MOGT_DT
-    return set_error(MOGT_E_INVALID, "unsupported dtype combination");
+    return 1;
 }
 
 }  // namespace
@@ -535,29 +90,35 @@ int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, in
 using namespace mogt;
 
 extern "C" size_t mogt_diag_scan_workspace_bytes_cfg(int64_t batch, int64_t length,
-                                                     int64_t features, int vec, int steps,
-                                                     int waves) {
-    if (batch <= 0 || length <= 0 || features <= 0 || vec <= 0 || steps <= 0 || waves <= 0)
+                                                     int64_t features, int vec, int lanes,
+                                                     int steps, int waves) {
+    if (batch <= 0 || length <= 0 || features <= 0 || vec <= 0 || steps <= 0 || waves <= 0 ||
+        (lanes != 16 && lanes != 32 && lanes != 64))
         return WS_HDR_BYTES;
-    return geometry(batch, length, features, vec, steps, waves).bytes;
+    return diag_geometry(batch, length, features, DiagTile{vec, lanes, steps, waves}).bytes;
 }
 
 extern "C" size_t mogt_diag_scan_workspace_bytes(int64_t batch, int64_t length, int64_t features,
                                                  int in_dtype) {
+    if (batch <= 0 || length <= 0 || features <= 0) return WS_HDR_BYTES;
     // Largest requirement over the tiles the entry point may pick.
-    const TileCfg a = default_cfg(batch, length, features, in_dtype == MOGT_BF16, true);
-    const TileCfg b = default_cfg(batch, length, features, in_dtype == MOGT_BF16, false);
-    const size_t sa = mogt_diag_scan_workspace_bytes_cfg(batch, length, features, a.vec, a.steps, a.waves);
-    const size_t sb = mogt_diag_scan_workspace_bytes_cfg(batch, length, features, b.vec, b.steps, b.waves);
-    return sa > sb ? sa : sb;
+    const bool bf = in_dtype == MOGT_BF16;
+    size_t best = 0;
+    for (int al : {4, 2, 1}) {
+        const size_t n = diag_geometry(batch, length, features,
+                                       default_tile(batch, length, features, bf, al)).bytes;
+        best = n > best ? n : best;
+    }
+    return best;
 }
 
 extern "C" int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix,
                                       int64_t batch, int64_t length, int64_t features,
-                                      int in_dtype, int out_dtype, int vec, int steps, int waves,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
-    return run_scan(a, b, h, a_prefix, batch, length, features, 1, 1, 1.0f, in_dtype, MOGT_F32,
-                    out_dtype, false, vec, steps, waves, workspace, workspace_bytes, stream);
+                                      int in_dtype, int out_dtype, int vec, int lanes, int steps,
+                                      int waves, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    return run_scan(a, b, h, a_prefix, batch, length, features, in_dtype, out_dtype,
+                    DiagTile{vec, lanes, steps, waves}, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a_prefix,
@@ -568,40 +129,30 @@ extern "C" int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a
         clear_error();
         return set_error(MOGT_E_INVALID, "unsupported dtype code");
     }
-    // Two-feature vectors need every pointer aligned to two elements.
-    auto aligned = [](const void* ptr, uintptr_t n) {
-        return ptr == nullptr || reinterpret_cast<uintptr_t>(ptr) % n == 0;
+    const int al = common_alignment(a, b, h, a_prefix, in_dtype, out_dtype);
+    const DiagTile t = default_tile(batch, length, features, in_dtype == MOGT_BF16, al);
+    return run_scan(a, b, h, a_prefix, batch, length, features, in_dtype, out_dtype, t, workspace,
+                    workspace_bytes, stream);
+}
+
+extern "C" int mogt_diag_scan_tiles(int family, int* out, int max_tiles) {
+    static const DiagTile f32[] = {
+#define MOGT_T(V_, F_, S_, W_) DiagTile{V_, F_, S_, W_},
+        MOGT_DIAG_F32_TILES(MOGT_T)
     };
-    const uintptr_t in2 = in_dtype == MOGT_BF16 ? 4 : 8;
-    const uintptr_t out2 = out_dtype == MOGT_BF16 ? 4 : 8;
-    const bool al2 = aligned(a, in2) && aligned(b, in2) && aligned(h, out2) && aligned(a_prefix, out2);
-    const TileCfg c = default_cfg(batch, length, features, in_dtype == MOGT_BF16, al2);
-    return run_scan(a, b, h, a_prefix, batch, length, features, 1, 1, 1.0f, in_dtype, MOGT_F32,
-                    out_dtype, false, c.vec, c.steps, c.waves, workspace, workspace_bytes, stream);
-}
-
-extern "C" size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t length,
-                                                         int64_t rank, int64_t channels,
-                                                         int v_dtype) {
-    (void)v_dtype;
-    if (batch <= 0 || length <= 0 || rank <= 0 || channels <= 0) return WS_HDR_BYTES;
-    const TileCfg c = default_cfg(batch, length, rank * channels, false, false);
-    return mogt_diag_scan_workspace_bytes_cfg(batch, length, rank * channels, c.vec, c.steps,
-                                              c.waves);
-}
-
-extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h, int64_t batch,
-                                          int64_t length, int64_t rank, int64_t channels,
-                                          float damping, int z_dtype, int v_dtype, int out_dtype,
-                                          void* workspace, size_t workspace_bytes, void* stream) {
-    clear_error();
-    if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
-        return set_error(MOGT_E_INVALID, "rank and channels must be positive");
-    if (!dtype_ok(z_dtype) || !dtype_ok(v_dtype) || !dtype_ok(out_dtype))
-        return set_error(MOGT_E_INVALID, "unsupported dtype code");
-    const int64_t D = rank * channels;
-    const TileCfg c = default_cfg(batch, length, D, false, false);
-    return run_scan(z, v, h, nullptr, batch, length, D, static_cast<int>(rank),
-                    static_cast<int>(channels), damping, v_dtype, z_dtype, out_dtype, true, c.vec,
-                    c.steps, c.waves, workspace, workspace_bytes, stream);
+    static const DiagTile b16[] = {MOGT_DIAG_BF16_TILES(MOGT_T)};
+    static const DiagTile cpl[] = {MOGT_COUPLED_TILES(MOGT_T)};
+#undef MOGT_T
+    const DiagTile* list = family == 0 ? f32 : family == 1 ? b16 : family == 2 ? cpl : nullptr;
+    const int n = family == 0   ? static_cast<int>(sizeof(f32) / sizeof(f32[0]))
+                  : family == 1 ? static_cast<int>(sizeof(b16) / sizeof(b16[0]))
+                  : family == 2 ? static_cast<int>(sizeof(cpl) / sizeof(cpl[0]))
+                                : 0;
+    for (int i = 0; i < n && i < max_tiles && out; ++i) {
+        out[4 * i] = list[i].vec;
+        out[4 * i + 1] = list[i].lanes;
+        out[4 * i + 2] = list[i].steps;
+        out[4 * i + 3] = list[i].waves;
+    }
+    return n;
 }

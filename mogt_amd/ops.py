@@ -73,7 +73,8 @@ def require_cuda(what: str, *tensors: torch.Tensor) -> None:
 # diag_scan: h_t = a_t * h_{t-1} + b_t over [B, L, D]
 # ---------------------------------------------------------------------------
 def _diag_scan_launch(a: torch.Tensor, b: torch.Tensor, h: torch.Tensor,
-                      prefix: torch.Tensor | None, cfg: tuple[int, int, int] | None = None) -> None:
+                      prefix: torch.Tensor | None,
+                      cfg: tuple[int, int, int, int] | None = None) -> None:
     lib = _lib.load()
     B, L, D = a.shape
     in_code = dtype_code(a.dtype, "diag_scan")
@@ -90,7 +91,7 @@ def _diag_scan_launch(a: torch.Tensor, b: torch.Tensor, h: torch.Tensor,
                                     in_code, out_code, ws.data_ptr(), ws.numel(), stream)
     else:
         rc = lib.mogt_diag_scan_fwd_cfg(a.data_ptr(), b.data_ptr(), h.data_ptr(), pre, B, L, D,
-                                        in_code, out_code, cfg[0], cfg[1], cfg[2],
+                                        in_code, out_code, cfg[0], cfg[1], cfg[2], cfg[3],
                                         ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "mogt_diag_scan_fwd")
 

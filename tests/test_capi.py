@@ -42,7 +42,8 @@ def test_abi_version(lib):
 def test_workspace_queries_are_host_only(lib):
     n = lib.mogt_diag_scan_workspace_bytes(1, 32768, 768, _lib.MOGT_F32)
     assert 256 < n < 64 << 20
-    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 1, 32, 16) == n
+    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 2, 32, 16, 16) == n
+    assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 2, 24, 16, 16) == 256
     assert lib.mogt_coupled_rank_scan_workspace_bytes(1, 1024, 16, 48, _lib.MOGT_BF16) > 256
 
 
@@ -50,14 +51,31 @@ def test_argument_errors_without_device(lib):
     # Validation happens on the host before any HIP call.
     rc = lib.mogt_diag_scan_fwd(None, None, None, None, 1, 8, 8, 7, 0, None, 0, None)
     assert rc == -1 and b"dtype" in lib.mogt_last_error()
-    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 3, 8, 4, None, 0, None)
+    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 3, 64, 8, 4, None, 0, None)
     assert rc == -1 and b"not compiled" in lib.mogt_last_error()
-    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 4, 8, 8, None, 0, None)
+    rc = lib.mogt_diag_scan_fwd_cfg(1, 1, 1, None, 1, 8, 8, 0, 0, 1, 64, 8, 16, None, 0, None)
     assert rc == -2 and b"workspace" in lib.mogt_last_error()
     rc = lib.mogt_coupled_rank_scan_fwd(1, 1, 1, 1, 8, 0, 48, 1.0, 0, 0, 0, None, 0, None)
     assert rc == -1
     # zero-size problems are a no-op success
     assert lib.mogt_diag_scan_fwd(None, None, None, None, 0, 8, 8, 0, 0, None, 0, None) == 0
+
+
+def test_tile_lists(lib):
+    for fam in (0, 1, 2):
+        tiles = _lib.diag_tiles(fam)
+        assert tiles, fam
+        for vec, lanes, steps, waves in tiles:
+            # rows of >= 256 contiguous bytes at fp32 / bf16 input
+            assert lanes in (16, 32, 64) and lanes * vec >= 64
+            assert steps * waves * (64 // lanes) >= 128
+
+
+def test_gpu_tile_lists_match_library(lib):
+    from test_gpu_diag_scan import TILES_BF16, TILES_F32
+
+    assert _lib.diag_tiles(0) == TILES_F32
+    assert _lib.diag_tiles(1) == TILES_BF16
 
 
 def test_check_maps_codes_to_python_errors(lib):

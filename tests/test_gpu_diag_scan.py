@@ -18,9 +18,12 @@ pytestmark = pytest.mark.gpu
 FP32_TOL = 1e-4
 BF16_TOL = 2e-2
 
-# every compiled tile (vec, steps per thread, waves)
-TILES = [(1, 32, 16), (1, 64, 16), (1, 48, 16), (1, 40, 8), (1, 32, 8), (1, 16, 8),
-         (2, 32, 16), (2, 16, 8), (4, 16, 8), (4, 8, 8)]
+# every compiled tile (vec, lanes per row, steps per lane, waves); the CPU test
+# test_capi.py::test_gpu_tile_lists_match_library keeps these in step
+TILES_F32 = [(2, 32, 16, 16), (1, 64, 32, 16), (2, 32, 8, 16), (1, 64, 16, 16), (1, 64, 8, 16),
+             (2, 64, 16, 16)]
+TILES_BF16 = [(4, 16, 16, 16), (4, 64, 8, 16), (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16),
+              (1, 64, 16, 16), (1, 64, 8, 16)]
 
 
 def _run_cfg(a, b, out_dtype, cfg, prefix=False):
@@ -44,8 +47,7 @@ def test_cfg1_fp32(gpu):
     assert rel_err(to_np(h), ref) <= FP32_TOL
 
 
-@pytest.mark.parametrize("tile", TILES)
-@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("dt,tile", [("fp32", t) for t in TILES_F32] + [("bf16", t) for t in TILES_BF16])
 def test_every_tile_ragged(gpu, tile, dt):
     """Ragged L (not a multiple of any chunk), several chunks per chain, D a
     multiple of the vector but not of the feature-group width; with prefix."""
