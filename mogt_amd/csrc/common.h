@@ -22,9 +22,8 @@ void clear_error();
 int check_launch(const char* what);
 
 // ---------------------------------------------------------------------------
-// bf16 <-> f32.  Storage is the raw 16-bit pattern.  f32 -> bf16 uses
-// round-to-nearest-even on the upper half of the IEEE-754 word (the standard
-// bit-level method; NaNs are kept quiet).
+// bf16 <-> f32.  Storage is the raw 16-bit pattern.  f32 -> bf16 rounds to
+// nearest even (the hardware conversion of gfx950).
 // ---------------------------------------------------------------------------
 typedef uint16_t bf16_t;
 
@@ -33,10 +32,8 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
 }
 
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<bf16_t>(u >> 16);
+    // one v_cvt_pk_bf16_f32 on gfx950 (round to nearest even, NaN stays NaN)
+    return __builtin_bit_cast(bf16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -211,6 +208,34 @@ __device__ __forceinline__ void load_bits16(const bf16_t* __restrict__ p, uint32
 #pragma unroll
         for (int i = 0; i < N; ++i) out[i] = u.v[i];
     }
+}
+
+// BYTES consecutive bytes (2, 4, 8 or 16) as raw 32-bit words, streaming
+// (non-temporal) or cached.  No value is extracted, so a run of these loads
+// issues back to back without waiting.
+template <int BYTES, bool NT>
+__device__ __forceinline__ void load_raw_impl(const void* p, uint32_t (&w)[(BYTES + 3) / 4]) {
+    if constexpr (BYTES == 2) {
+        const uint16_t* q = static_cast<const uint16_t*>(p);
+        w[0] = NT ? __builtin_nontemporal_load(q) : *q;
+    } else if constexpr (BYTES == 4) {
+        const uint32_t* q = static_cast<const uint32_t*>(p);
+        w[0] = NT ? __builtin_nontemporal_load(q) : *q;
+    } else {
+        typedef typename WordVec<BYTES>::type W;
+        const W* q = static_cast<const W*>(p);
+        const W x = NT ? __builtin_nontemporal_load(q) : *q;
+#pragma unroll
+        for (int i = 0; i < BYTES / 4; ++i) w[i] = x[i];
+    }
+}
+template <int BYTES>
+__device__ __forceinline__ void load_raw(const void* p, uint32_t (&w)[(BYTES + 3) / 4]) {
+    load_raw_impl<BYTES, true>(p, w);
+}
+template <int BYTES>
+__device__ __forceinline__ void load_raw_cached(const void* p, uint32_t (&w)[(BYTES + 3) / 4]) {
+    load_raw_impl<BYTES, false>(p, w);
 }
 
 template <typename T, int N>

@@ -22,15 +22,26 @@ int coupled_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
 
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 
-// Default tile (measured on MI355X at r = 16, c = 48, L = 8k..32k): two
-// channels per lane (the lanes of one vector must share a gate, so the vector
-// must divide the channel count), 32 lanes per row, 512-step chunks; short
-// problems fall back to shorter chunks.
-DiagTile coupled_tile(int64_t B, int64_t L, int64_t R, int64_t C, bool aligned2) {
+// Default tile (measured on MI355X at r = 16, c = 48, L = 8k..32k): four
+// channels per lane where the channel count and the pointers allow it (the
+// lanes of one vector must share a gate, so the vector must divide the channel
+// count), 512-step chunks; short problems fall back to shorter chunks.
+DiagTile coupled_tile(int64_t B, int64_t L, int64_t R, int64_t C, int align_elems) {
+    static const DiagTile v4[] = {{4, 16, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
     static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
     static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
-    if (C % 2 == 0 && aligned2) return pick_tile(B, L, R * C, v2, 3);
+    if (C % 4 == 0 && align_elems % 4 == 0) return pick_tile(B, L, R * C, v4, 3);
+    if (C % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, R * C, v2, 3);
     return pick_tile(B, L, R * C, v1, 3);
+}
+
+// Largest vector width (4, 2 or 1 elements) both v and h are aligned to.
+int coupled_alignment(const void* v, const void* h, int v_dtype, int out_dtype) {
+    const uintptr_t ve = v_dtype == MOGT_BF16 ? 2 : 4, he = out_dtype == MOGT_BF16 ? 2 : 4;
+    for (int n : {4, 2})
+        if (reinterpret_cast<uintptr_t>(v) % (ve * n) == 0 && reinterpret_cast<uintptr_t>(h) % (he * n) == 0)
+            return n;
+    return 1;
 }
 
 }  // namespace
@@ -72,12 +83,14 @@ extern "C" size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t 
                                                          int v_dtype) {
     if (batch <= 0 || length <= 0 || rank <= 0 || channels <= 0) return WS_HDR_BYTES;
     // Largest requirement over the tiles the entry point may pick.
-    const size_t a = diag_geometry(batch, length, rank * channels,
-                                   coupled_tile(batch, length, rank, channels, true)).bytes;
-    const size_t b = diag_geometry(batch, length, rank * channels,
-                                   coupled_tile(batch, length, rank, channels, false)).bytes;
     (void)v_dtype;
-    return a > b ? a : b;
+    size_t best = 0;
+    for (int al : {4, 2, 1}) {
+        const size_t n = diag_geometry(batch, length, rank * channels,
+                                       coupled_tile(batch, length, rank, channels, al)).bytes;
+        best = n > best ? n : best;
+    }
+    return best;
 }
 
 extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h, int64_t batch,
@@ -92,9 +105,8 @@ extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
         return set_error(MOGT_E_INVALID, "unsupported dtype code");
     if (batch == 0 || length == 0) return MOGT_OK;
     if (!z || !v || !h) return set_error(MOGT_E_INVALID, "null tensor pointer");
-    auto aligned = [](const void* ptr, uintptr_t n) { return reinterpret_cast<uintptr_t>(ptr) % n == 0; };
-    const bool al2 = aligned(v, v_dtype == MOGT_BF16 ? 4 : 8) && aligned(h, out_dtype == MOGT_BF16 ? 4 : 8);
-    const DiagTile t = coupled_tile(batch, length, rank, channels, al2);
+    const DiagTile t = coupled_tile(batch, length, rank, channels,
+                                    coupled_alignment(v, h, v_dtype, out_dtype));
     return coupled_run(z, v, h, batch, length, rank, channels, damping, z_dtype, v_dtype, out_dtype,
                        t, workspace, workspace_bytes, stream);
 }

@@ -80,13 +80,9 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     static_assert(64 % FWL == 0 && FWL >= 16, "a row spans 16, 32 or 64 lanes");
     constexpr bool COUPLED = MODE == MODE_COUPLED;
     constexpr bool BF16_IN = std::is_same<TIn, bf16_t>::value;
-    // Stash layouts (registers per step and lane):
-    //   DIAG fp32:        a[VEC], b[VEC]               2*VEC
-    //   DIAG bf16:        {a|b<<16}[VEC]               VEC
-    //   COUPLED, v bf16:  g, v pairs[ceil(VEC/2)]      1 + ceil(VEC/2)
-    //   COUPLED, v fp32:  g, v[VEC]                    1 + VEC
-    constexpr int NA = COUPLED ? 1 : (BF16_IN ? 1 : VEC);
-    constexpr int NB = COUPLED ? (BF16_IN ? (VEC + 1) / 2 : VEC) : VEC;
+    // Stash (32-bit registers per step and lane): DIAG fp32 a[VEC], b[VEC];
+    // DIAG bf16 raw a and b words (two values per word); COUPLED the gate logit
+    // (then the gate) and the raw v words.
     static_assert(!(PREFIX && COUPLED), "prefix output is a DIAG-mode option");
 
     __shared__ int s_pending[2];
@@ -123,10 +119,20 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     const uint32_t epoch = __builtin_amdgcn_readfirstlane(ld_relaxed(&p.hdr[2]));
 
     // ---- stash: issue every load before any use --------------------------
-    float ra[S][NA];
-    uint32_t rb[S][NB];   // DIAG fp32: float bits of b; bf16: packed {a|b<<16}; COUPLED: v
+    // Loads are unconditional (rows past L and features past D read a clamped,
+    // in-bounds location) and land in raw registers, so they issue back to back
+    // with no wait in between; steps outside the problem are replaced by the
+    // identity (a = 1, b = 0) where the values are used.
+    constexpr int NWB = BF16_IN ? (VEC + 1) / 2 : VEC;   // raw 32-bit words per row of b or v
+    constexpr int NA = COUPLED ? 1 : (BF16_IN ? NWB : VEC);
+    float ra[S][NA];      // DIAG fp32: a; DIAG bf16: raw a words; COUPLED: raw z, then gate g
+    uint32_t rb[S][NWB];  // raw words of b (DIAG) or v (COUPLED)
+    int nv;               // valid steps of this lane (0 .. S)
     {
-        // wave-uniform row base; lanes add (q*S + s) rows and their feature offset
+        const int64_t r = p.L - t0;
+        nv = !fvalid || r <= 0 ? 0 : (r >= S ? S : static_cast<int>(r));
+        const int lastrel = static_cast<int>(p.L - 1 - tw);   // last row of the problem, from tw
+        const int flc = fvalid ? flane : 0;
         const int64_t wbase = (row0 + tw) * p.D + fbase;
         const TIn* pa = static_cast<const TIn*>(p.a) + wbase;
         const TIn* pb = static_cast<const TIn*>(p.b) + wbase;
@@ -134,91 +140,69 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         int gi = 0;
         if constexpr (COUPLED) {
             pz = static_cast<const TZ*>(p.a) + (row0 + tw) * p.R;
-            gi = static_cast<int>((fbase + flane) / p.C);
+            gi = static_cast<int>((fbase + flc) / p.C);
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const bool ok = fvalid && (t0 + s < p.L);
-            const int off = (q * S + s) * Di + flane;
+            const int rel = min(q * S + s, lastrel);
+            const int off = rel * Di + flc;
+            load_raw<sizeof(TIn) * VEC>(pb + off, rb[s]);
             if constexpr (COUPLED) {
-                if (ok) {
-                    ra[s][0] = IO<TZ>::ld(pz[(q * S + s) * p.R + gi]);   // logit; sigmoid below
-                    if constexpr (BF16_IN) {
-                        uint32_t vb[VEC];
-                        load_bits16<VEC>(pb + off, vb);
-#pragma unroll
-                        for (int j = 0; j < NB; ++j)
-                            rb[s][j] = vb[2 * j] | (2 * j + 1 < VEC ? (vb[2 * j + 1] << 16) : 0u);
-                    } else {
-                        float vf[VEC];
-                        load_stream<TIn, VEC>(pb + off, vf);
-#pragma unroll
-                        for (int j = 0; j < VEC; ++j) rb[s][j] = __float_as_uint(vf[j]);
-                    }
-                } else {
-                    ra[s][0] = 0.0f;   // replaced by the identity marker below
-#pragma unroll
-                    for (int j = 0; j < NB; ++j) rb[s][j] = 0u;
-                }
-            } else if constexpr (BF16_IN) {
-                if (ok) {
-                    uint32_t ab[VEC], bb[VEC];
-                    load_bits16<VEC>(pa + off, ab);
-                    load_bits16<VEC>(pb + off, bb);
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) rb[s][v] = ab[v] | (bb[v] << 16);
-                } else {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) rb[s][v] = 0x3f80u;   // a = 1.0, b = 0.0
-                }
+                uint32_t zw[1];
+                load_raw_cached<sizeof(TZ)>(pz + rel * p.R + gi, zw);
+                ra[s][0] = __uint_as_float(zw[0]);
             } else {
-                if (ok) {
-                    float bf[VEC];
-                    load_stream<TIn, VEC>(pa + off, ra[s]);
-                    load_stream<TIn, VEC>(pb + off, bf);
+                uint32_t aw[NA];
+                load_raw<sizeof(TIn) * VEC>(pa + off, aw);
 #pragma unroll
-                    for (int v = 0; v < VEC; ++v) rb[s][v] = __float_as_uint(bf[v]);
-                } else {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) { ra[s][v] = 1.0f; rb[s][v] = 0u; }
-                }
+                for (int j = 0; j < NA; ++j) ra[s][j] = __uint_as_float(aw[j]);
             }
         }
     }
 
-    // Coupled gate: g = sigmoid(z); out-of-range steps become the identity.
+    // Coupled gate, once per step when the data arrives: g = sigmoid(z),
+    // a = damping * (1 - g) replaces the logit, and b = v * g (rounded to v's
+    // dtype exactly where the reference's product is) replaces v in place --
+    // b is exactly representable in v's dtype, so the stash keeps its size.
+    // Steps outside the problem become the identity (a = 1, b = 0).
     if constexpr (COUPLED) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const bool ok = fvalid && (t0 + s < p.L);
-            ra[s][0] = ok ? sigmoidf_(ra[s][0]) : -1.0f;   // -1 marks an identity step
+            const uint32_t zb = __float_as_uint(ra[s][0]);
+            const float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
+            const bool ok = s < nv;
+            const float gg = sigmoidf_(z);
+            // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)
+            const float g_io = IO<TIn>::ld(IO<TIn>::st(gg));
+            ra[s][0] = ok ? p.damping * (1.0f - gg) : 1.0f;
+#pragma unroll
+            for (int j = 0; j < NWB; ++j) {
+                uint32_t w = rb[s][j];
+                if constexpr (BF16_IN) {
+                    const uint32_t lo = f32_to_bf16(__uint_as_float(w << 16) * g_io);
+                    const uint32_t hi = f32_to_bf16(__uint_as_float(w & 0xffff0000u) * g_io);
+                    w = lo | (hi << 16);
+                } else {
+                    w = __float_as_uint(__uint_as_float(w) * g_io);
+                }
+                rb[s][j] = ok ? w : 0u;
+            }
         }
     }
+    // bf16 element v of a raw word array (two per word, low half first).
+    auto bf16_at = [](uint32_t w, int v) -> float {
+        return __uint_as_float((v & 1) ? (w & 0xffff0000u) : (w << 16));
+    };
     // Element accessors (fp32 values of a and b for step s, feature v).
     auto step_a = [&](int s, int v) -> float {
-        if constexpr (COUPLED) return ra[s][0] < 0.0f ? 1.0f : p.damping * (1.0f - ra[s][0]);
-        else if constexpr (BF16_IN) return __uint_as_float(rb[s][v] << 16);
-        else return ra[s][v];
+        if constexpr (COUPLED) return ra[s][0];
+        else if constexpr (BF16_IN) return s < nv ? bf16_at(__float_as_uint(ra[s][v >> 1]), v) : 1.0f;
+        else return s < nv ? ra[s][v] : 1.0f;
     };
     auto step_b = [&](int s, int v) -> float {
-        if constexpr (COUPLED) {
-            const float gg = ra[s][0];
-            if (gg < 0.0f) return 0.0f;
-            float vv;
-            if constexpr (BF16_IN) {
-                const uint32_t w = rb[s][v >> 1];
-                vv = __uint_as_float((v & 1) ? (w & 0xffff0000u) : (w << 16));
-            } else {
-                vv = __uint_as_float(rb[s][v]);
-            }
-            // reference: V_t_raw * value_gate.to(V_t_raw.dtype) in V's dtype
-            const float g_io = IO<TIn>::ld(IO<TIn>::st(gg));
-            return IO<TIn>::ld(IO<TIn>::st(vv * g_io));
-        } else if constexpr (BF16_IN) {
-            return __uint_as_float(rb[s][v] & 0xffff0000u);
-        } else {
-            return __uint_as_float(rb[s][v]);
-        }
+        if constexpr (COUPLED) return BF16_IN ? bf16_at(rb[s][v >> 1], v) : __uint_as_float(rb[s][v]);
+        else if constexpr (BF16_IN) return s < nv ? bf16_at(rb[s][v >> 1], v) : 0.0f;
+        else return s < nv ? __uint_as_float(rb[s][v]) : 0.0f;
     };
 
     // ---- level 1: in-lane summary (prod a, h from 0) of the S steps -------
@@ -240,8 +224,9 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) asm volatile("" : "+v"(rb[s][j]));
-            if constexpr (COUPLED) asm volatile("" : "+v"(ra[s][0]));
+            for (int j = 0; j < NWB; ++j) asm volatile("" : "+v"(rb[s][j]));
+#pragma unroll
+            for (int j = 0; j < NA; ++j) asm volatile("" : "+v"(ra[s][j]));
         }
     }
     if (tid == 0) { s_pending[0] = 0; s_pending[1] = 0; }
@@ -349,7 +334,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 if constexpr (PREFIX) Ap[v] *= av;
                 o[v] = hh[v];
             }
-            if (fvalid && t0 + s < p.L) {
+            if (s < nv) {
                 const int off = (q * S + s) * Di + flane;
                 store_stream<TOut, VEC>(ph + off, o);
                 if constexpr (PREFIX) {
@@ -457,7 +442,7 @@ int diag_launch(const DiagParams& prm, hipStream_t stream) {
 // efficiency) and at most 64 stash registers per lane.
 #define MOGT_DIAG_F32_TILES(X) X(2, 32, 16, 16) X(1, 64, 32, 16) X(2, 32, 8, 16) X(1, 64, 16, 16) X(1, 64, 8, 16) X(2, 64, 16, 16)
 #define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 16) X(4, 64, 8, 16) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
-#define MOGT_COUPLED_TILES(X) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_COUPLED_TILES(X) X(2, 32, 16, 16) X(4, 16, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 
 // Per-family launchers (diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
 int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,

@@ -2,17 +2,24 @@
 //   S_t = f_t S_{t-1} + (1 - f_t) v_t k_t^T,   y_t = S_t q_t,   S_0 = 0
 // i.e. the affine recurrence of affine_scan.py:48-55 with U_t = f_t I and the
 // rank-1 write V_t = (1 - f_t) v_t k_t^T, read out through q_t.  S_t (d x d per
-// step) is never written to memory.  Chunked form over T steps, with
-// Lc_t = sum_{u<=t} log f_u inside the chunk and S_in the state before it:
-//   y_t  = exp(Lc_t) S_in q_t + sum_{s<=t} exp(Lc_t - Lc_s) (1 - f_s) (q_t . k_s) v_s
-//   S_out = exp(Lc_T) S_in + sum_s exp(Lc_T - Lc_s) (1 - f_s) v_s k_s^T
-// Three launches:
-//   K_A  per chunk: dS = V^T diag(w) K on bf16 MFMA (32x32x16), chunk log-decay
-//   K_B  per (sequence, state element): S_in(k) = exp(LcT(k-1)) S_in(k-1) + dS(k-1)
-//        -- the chunk carries compose element-wise, so this is a plain scan
-//   K_C  per chunk: (Q K^T masked by the decay) V + exp(Lc) Q S_in^T on MFMA; the
-//        state operand is split into bf16 hi + lo parts for fp32-level accuracy.
-// Layouts: f [B, L, H]; q, k, v, y [B, L, H, DH] (the reference's flattening).
+// step) is never written to memory.
+//
+// Chunked form.  Inside a block of steps with Lc_t = sum_{u<=t} log f_u (block
+// local) and S_in the state before the block:
+//   y_t   = exp(Lc_t) S_in q_t + sum_{s<=t} exp(Lc_t - Lc_s) (1 - f_s) (q_t . k_s) v_s
+//   S_out = exp(Lc_T) S_in + V^T diag(w) K,   w_s = exp(Lc_T - Lc_s) (1 - f_s)
+// Three launches over super-chunks of RS = 256 steps:
+//   K_A  per super-chunk: dS = V^T diag(w) K over its 256 steps (one bf16 MFMA
+//        chain, K = 256) and its total log-decay.
+//   K_B  per (sequence, state element): S_in of every super-chunk -- the carries
+//        compose element-wise with a scalar decay, so this is a plain scan.
+//   K_C  per super-chunk: four 64-step sub-chunks in order, the 64 x 64 state
+//        carried in MFMA accumulators; per sub-chunk the masked, decayed
+//        (Q K^T) V plus exp(Lc) Q S^T (state split into bf16 hi + lo parts for
+//        fp32-level accuracy), then S <- exp(Lc_T) S + V^T diag(w) K.  The next
+//        sub-chunk's q, k, v are loaded into registers while this one computes.
+// K_A reads k and v with ordinary (cache-allocating) loads, so K_C usually finds
+// them in the Infinity Cache.  Layouts: f [B, L, H]; q, k, v, y [B, L, H, DH].
 #include "common.h"
 
 namespace mogt {
@@ -20,10 +27,13 @@ namespace mogt {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int R1_DH = 64;        // head dimension
-constexpr int R1_T = 64;         // chunk length
-constexpr int R1_THREADS = 256;  // 4 waves
-constexpr int R1_PAD = 8;        // LDS row padding (bf16): rows of 144 B, conflict-free 16 B reads
+constexpr int R1_DH = 64;         // head dimension
+constexpr int R1_T = 64;          // sub-chunk length
+constexpr int R1_SUB = 4;         // sub-chunks per super-chunk
+constexpr int R1_RS = R1_T * R1_SUB;
+constexpr int R1_THREADS = 256;   // 4 waves
+constexpr int R1_PAD = 8;         // LDS row padding (bf16): rows of 144 B
+constexpr int R1_SR = R1_DH + R1_PAD;
 constexpr float R1_LOG_MIN = -80.0f;
 
 struct Rank1Params {
@@ -32,16 +42,17 @@ struct Rank1Params {
     const void* v;
     const void* q;
     void* y;
-    float* dS;      // [n_seq][nch][DH*DH]
-    float* lcT;     // [n_seq][nch]
-    float* Sin;     // [n_seq][nch][DH*DH]
+    float* dS;      // [n_seq][nsc][DH*DH]
+    float* lcT;     // [n_seq][nsc]
+    float* Sin;     // [n_seq][nsc][DH*DH]
     int64_t L;
-    int H, nch;
+    int H, nsc;
 };
 
 // 32x32 fp32 tile += A[32 x K] B[K x 32]; A rows in `a` (row stride sa, k contiguous),
 // B columns in `b` (column stride sb, k contiguous), both bf16 in LDS.
-__device__ __forceinline__ f32x16 mma32(const bf16_t* a, int sa, const bf16_t* b, int sb, int K, f32x16 acc) {
+__device__ __forceinline__ f32x16 mma32(const bf16_t* a, int sa, const bf16_t* b, int sb, int K,
+                                        f32x16 acc) {
     const int l = threadIdx.x & 63;
     for (int k0 = 0; k0 < K; k0 += 16) {
         const bf16x8 av = *reinterpret_cast<const bf16x8*>(a + (l & 31) * sa + k0 + 8 * (l >> 5));
@@ -72,179 +83,337 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
     return x;
 }
 
-// Load a T x DH tile of q/k/v rows (zero past L) into LDS, row-major or transposed.
-template <typename TI, bool TRANSPOSE>
-__device__ __forceinline__ void load_rows(const TI* __restrict__ src, bf16_t* dst, int64_t rowbase,
-                                          int64_t t0, int64_t L, int H) {
-    constexpr int SEG = R1_DH / 8;   // 8-element segments per row
-    for (int e = threadIdx.x; e < R1_T * SEG; e += R1_THREADS) {
-        const int t = e / SEG, sg = e - (e / SEG) * SEG;
-        float x[8];
-        if (t0 + t < L) {
-            load_vec<TI, 8>(src + (rowbase + (t0 + t) * H) * R1_DH + sg * 8, x);
-        } else {
+// One 64-step x 64-wide tile of q, k or v held in registers: thread e covers
+// row (e + 256 u) / 8, segment (e + 256 u) % 8 of 8 consecutive elements, so
+// 8 consecutive lanes read one 128-byte row (u = 0, 1).  Rows past L are read
+// from row L - 1 (every load is unconditional, so no wait is forced between
+// them) and zeroed when the tile is staged into LDS.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename TI>
+struct Tile8 {
+    static constexpr int NW = sizeof(TI) == 2 ? 1 : 2;   // 16-byte words per segment
+    u32x4 x[2][NW];
+    bool ok[2];
+};
+
+template <typename TI>
+__device__ __forceinline__ Tile8<TI> load_tile(const TI* __restrict__ src, int64_t rowbase, int64_t t0,
+                                               int64_t L, int H) {
+    Tile8<TI> r;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = 0.0f;
-        }
+    for (int u = 0; u < 2; ++u) {
+        const int e = threadIdx.x + R1_THREADS * u;
+        const int t = e >> 3, sg = e & 7;
+        r.ok[u] = t0 + t < L;
+        const int64_t row = r.ok[u] ? t0 + t : L - 1;
+        const u32x4* ptr = reinterpret_cast<const u32x4*>(src + (rowbase + row * H) * R1_DH + sg * 8);
+#pragma unroll
+        for (int j = 0; j < Tile8<TI>::NW; ++j) r.x[u][j] = ptr[j];
+    }
+    return r;
+}
+
+// The 8 elements of segment u as bf16 (zero past L).
+template <typename TI>
+__device__ __forceinline__ bf16x8 seg_bf16(const Tile8<TI>& r, int u) {
+    bf16x8 o;
+    if constexpr (sizeof(TI) == 2) {
+        o = __builtin_bit_cast(bf16x8, r.x[u][0]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[4 * j + i] = static_cast<__bf16>(__uint_as_float(r.x[u][j][i]));
+    }
+    if (!r.ok[u]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = static_cast<__bf16>(0.0f);
+    }
+    return o;
+}
+
+// Tile into LDS: row-major [t][d] (row stride R1_SR) and/or transposed [d][t].
+template <typename TI>
+__device__ __forceinline__ void put_rows(const Tile8<TI>& r, bf16_t* dst) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int e = threadIdx.x + R1_THREADS * u;
+        const int t = e >> 3, sg = e & 7;
+        *reinterpret_cast<bf16x8*>(dst + t * R1_SR + sg * 8) = seg_bf16(r, u);
+    }
+}
+template <typename TI>
+__device__ __forceinline__ void put_cols(const Tile8<TI>& r, bf16_t* dst) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int e = threadIdx.x + R1_THREADS * u;
+        const int t = e >> 3, sg = e & 7;
+        const bf16x8 o = seg_bf16(r, u);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const bf16_t bv = f32_to_bf16(x[i]);
-            if (TRANSPOSE) dst[(sg * 8 + i) * (R1_T + R1_PAD) + t] = bv;
-            else dst[t * (R1_DH + R1_PAD) + sg * 8 + i] = bv;
+            const __bf16 b = o[i];
+            dst[(sg * 8 + i) * R1_SR + t] = *reinterpret_cast<const bf16_t*>(&b);
         }
     }
 }
 
-// Lc (inclusive log-decay cumsum) and 1 - f of the chunk into LDS (wave 0).
+// Raw f of step t (row L - 1 past the end; see fval).
 template <typename TF>
-__device__ __forceinline__ void chunk_decay(const TF* __restrict__ f, int64_t fbase, int64_t t0, int64_t L, int H,
-                                            float* sLc, float* sOmf) {
-    if (threadIdx.x < 64) {
-        const int t = threadIdx.x;
-        float fv = 1.0f;
-        if (t0 + t < L) fv = IO<TF>::ld(f[fbase + (t0 + t) * H]);
-        const float lg = fmaxf(logf(fv), R1_LOG_MIN);
-        sLc[t] = wave_incl_scan(lg);
-        sOmf[t] = 1.0f - fv;
-    }
+__device__ __forceinline__ TF load_f(const TF* __restrict__ f, int64_t rowbase, int64_t t, int64_t L,
+                                     int H) {
+    return f[rowbase + (t < L ? t : L - 1) * H];
+}
+// Padding steps past L act as f = 1 with k = v = q = 0 (no write, no decay).
+template <typename TF>
+__device__ __forceinline__ float fval(TF raw, int64_t t, int64_t L) {
+    return t < L ? IO<TF>::ld(raw) : 1.0f;
 }
 
+// ---------------------------------------------------------------------------
+// K_A: dS = V^T diag(w) K over one 256-step super-chunk.
+// ---------------------------------------------------------------------------
 template <typename TF, typename TI>
 __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p) {
-    __shared__ __attribute__((aligned(16))) bf16_t sVT[R1_DH * (R1_T + R1_PAD)];
-    __shared__ __attribute__((aligned(16))) bf16_t sKT[R1_DH * (R1_T + R1_PAD)];
-    __shared__ float sLc[R1_T], sOmf[R1_T];
-    const int kc = blockIdx.x;               // chunk
-    const int seq = blockIdx.y;              // b * H + h
+    __shared__ __attribute__((aligned(16))) bf16_t sVT[R1_DH * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sKT[R1_DH * R1_SR];
+    __shared__ float sW[R1_RS];
+    __shared__ float sWave[4];
+    const int sc = blockIdx.x;
+    const int seq = blockIdx.y;
     const int b = seq / p.H, h = seq - (seq / p.H) * p.H;
-    const int64_t t0 = static_cast<int64_t>(kc) * R1_T;
-    const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + h;   // (b*L + t)*H + h = rowbase + t*H
-    load_rows<TI, true>(static_cast<const TI*>(p.v), sVT, rowbase, t0, p.L, p.H);
-    load_rows<TI, true>(static_cast<const TI*>(p.k), sKT, rowbase, t0, p.L, p.H);
-    chunk_decay<TF>(static_cast<const TF*>(p.f), rowbase, t0, p.L, p.H, sLc, sOmf);
+    const int64_t t0 = static_cast<int64_t>(sc) * R1_RS;
+    const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + h;   // (b*L + t)*H + h
+    const TI* kp = static_cast<const TI*>(p.k);
+    const TI* vp = static_cast<const TI*>(p.v);
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const TF fraw = load_f<TF>(static_cast<const TF*>(p.f), rowbase, t0 + tid, p.L, p.H);
+    Tile8<TI> kt = load_tile<TI>(kp, rowbase, t0, p.L, p.H);
+    Tile8<TI> vt = load_tile<TI>(vp, rowbase, t0, p.L, p.H);
+
+    // block-wide inclusive log-decay cumsum over the 256 steps (one per thread)
+    const float fv = fval<TF>(fraw, t0 + tid, p.L);
+    float lc = wave_incl_scan(fmaxf(logf(fv), R1_LOG_MIN));
+    if (lane == 63) sWave[w] = lc;
     __syncthreads();
-    // scale V^T columns by w_s = exp(LcT - Lc_s) (1 - f_s)
-    const float lct = sLc[R1_T - 1];
-    for (int e = threadIdx.x; e < R1_DH * R1_T; e += R1_THREADS) {
-        const int i = e / R1_T, s = e - (e / R1_T) * R1_T;
-        bf16_t& x = sVT[i * (R1_T + R1_PAD) + s];
-        x = f32_to_bf16(bf16_to_f32(x) * expf(lct - sLc[s]) * sOmf[s]);
+    for (int i = 0; i < w; ++i) lc += sWave[i];
+    const float lcT = sWave[0] + sWave[1] + sWave[2] + sWave[3];
+    sW[tid] = expf(lcT - lc) * (1.0f - fv);
+
+    const int ib = w >> 1, jb = w & 1;   // this wave's 32x32 tile of dS[i][j]
+    f32x16 acc = zero16();
+    for (int sub = 0; sub < R1_SUB; ++sub) {
+        __syncthreads();   // previous sub-block's tiles consumed; sW visible
+        put_cols(kt, sKT);
+        {
+            // V^T scaled by w_s (rounded to bf16 for the MFMA)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int e = tid + R1_THREADS * u;
+                const int t = e >> 3, sg = e & 7;
+                const float ws = sW[sub * R1_T + t];
+                const bf16x8 vs = seg_bf16(vt, u);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const __bf16 bv = static_cast<__bf16>(static_cast<float>(vs[i]) * ws);
+                    sVT[(sg * 8 + i) * R1_SR + t] = *reinterpret_cast<const bf16_t*>(&bv);
+                }
+            }
+        }
+        if (sub + 1 < R1_SUB) {   // prefetch the next sub-block while this one multiplies
+            kt = load_tile<TI>(kp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
+            vt = load_tile<TI>(vp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
+        }
+        __syncthreads();
+        acc = mma32(sVT + ib * 32 * R1_SR, R1_SR, sKT + jb * 32 * R1_SR, R1_SR, R1_T, acc);
     }
-    __syncthreads();
-    const int w = threadIdx.x >> 6;           // output tile (ib, jb) of dS [i][j]
-    const int ib = w >> 1, jb = w & 1;
-    f32x16 acc = mma32(sVT + ib * 32 * (R1_T + R1_PAD), R1_T + R1_PAD,
-                       sKT + jb * 32 * (R1_T + R1_PAD), R1_T + R1_PAD, R1_T, zero16());
-    float* out = p.dS + (static_cast<int64_t>(seq) * p.nch + kc) * R1_DH * R1_DH;
-    const int col = jb * 32 + (threadIdx.x & 31);
+    float* out = p.dS + (static_cast<int64_t>(seq) * p.nsc + sc) * R1_DH * R1_DH;
+    const int col = jb * 32 + (lane & 31);
 #pragma unroll
     for (int r = 0; r < 16; ++r) out[(ib * 32 + mrow(r)) * R1_DH + col] = acc[r];
-    if (threadIdx.x == 0) p.lcT[static_cast<int64_t>(seq) * p.nch + kc] = lct;
+    if (tid == 0) p.lcT[static_cast<int64_t>(seq) * p.nsc + sc] = lcT;
 }
 
-// Carries: one thread per state element, scan over the chunks of one sequence.
+// ---------------------------------------------------------------------------
+// K_B: carries.  One thread per state element; the super-chunk summaries are
+// loaded in batches of 8 ahead of the dependent multiply-adds.
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rank1_carry_kernel(Rank1Params p) {
     const int seq = blockIdx.y;
     const int e = blockIdx.x * 256 + threadIdx.x;   // < DH*DH
-    const int64_t base = static_cast<int64_t>(seq) * p.nch;
+    const int64_t base = static_cast<int64_t>(seq) * p.nsc;
+    constexpr int64_t SZ = R1_DH * R1_DH;
     float S = 0.0f;
-    for (int kc = 0; kc < p.nch; ++kc) {
-        p.Sin[(base + kc) * R1_DH * R1_DH + e] = S;
-        S = fmaf(expf(p.lcT[base + kc]), S, p.dS[(base + kc) * R1_DH * R1_DH + e]);
-    }
-}
-
-template <typename TF, typename TI, typename TO>
-__global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p) {
-    constexpr int SR = R1_DH + R1_PAD;   // row stride of [t][d] / [i][j] tiles
-    constexpr int SP = R1_T + R1_PAD;    // row stride of [.][t] tiles
-    __shared__ __attribute__((aligned(16))) bf16_t sQ[R1_T * SR];
-    __shared__ __attribute__((aligned(16))) bf16_t sK[R1_T * SR];
-    __shared__ __attribute__((aligned(16))) bf16_t sVT[R1_DH * SP];
-    __shared__ __attribute__((aligned(16))) bf16_t sP[R1_T * SP];
-    __shared__ __attribute__((aligned(16))) bf16_t sShi[R1_DH * SR];
-    __shared__ __attribute__((aligned(16))) bf16_t sSlo[R1_DH * SR];
-    __shared__ float sLc[R1_T], sOmf[R1_T];
-    const int kc = blockIdx.x;
-    const int seq = blockIdx.y;
-    const int b = seq / p.H, h = seq - (seq / p.H) * p.H;
-    const int64_t t0 = static_cast<int64_t>(kc) * R1_T;
-    const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + h;
-    load_rows<TI, false>(static_cast<const TI*>(p.q), sQ, rowbase, t0, p.L, p.H);
-    load_rows<TI, false>(static_cast<const TI*>(p.k), sK, rowbase, t0, p.L, p.H);
-    load_rows<TI, true>(static_cast<const TI*>(p.v), sVT, rowbase, t0, p.L, p.H);
-    chunk_decay<TF>(static_cast<const TF*>(p.f), rowbase, t0, p.L, p.H, sLc, sOmf);
-    {
-        const float* S = p.Sin + (static_cast<int64_t>(seq) * p.nch + kc) * R1_DH * R1_DH;
-        for (int e = threadIdx.x; e < R1_DH * R1_DH; e += R1_THREADS) {
-            const int i = e / R1_DH, j = e - (e / R1_DH) * R1_DH;
-            const float x = S[e];
-            const bf16_t hi = f32_to_bf16(x);
-            sShi[i * SR + j] = hi;
-            sSlo[i * SR + j] = f32_to_bf16(x - bf16_to_f32(hi));
-        }
-    }
-    __syncthreads();
-    const int w = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int tb = w >> 1, xb = w & 1;   // this wave's 32-row block and 32-column block
-    // P = (Q K^T) o exp(Lc_t - Lc_s) (1 - f_s) on s <= t  (tile (tb, xb); s-block xb > tb is zero)
-    {
-        const int t_of = tb * 32, s_of = xb * 32;
-        if (xb <= tb) {
-            f32x16 acc = mma32(sQ + t_of * SR, SR, sK + s_of * SR, SR, R1_DH, zero16());
-            const int s = s_of + (lane & 31);
+    for (int c0 = 0; c0 < p.nsc; c0 += 8) {
+        float d[8], dec[8];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int t = t_of + mrow(r);
-                const float pv = (s <= t) ? acc[r] * expf(sLc[t] - sLc[s]) * sOmf[s] : 0.0f;
-                sP[t * SP + s] = f32_to_bf16(pv);
+        for (int i = 0; i < 8; ++i) {
+            const bool ok = c0 + i < p.nsc;
+            d[i] = ok ? p.dS[(base + c0 + i) * SZ + e] : 0.0f;
+            dec[i] = ok ? p.lcT[base + c0 + i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (c0 + i < p.nsc) {
+                p.Sin[(base + c0 + i) * SZ + e] = S;
+                S = fmaf(expf(dec[i]), S, d[i]);
             }
         }
     }
-    __syncthreads();
-    // y tile (rows tb, columns xb): intra-chunk P V + decayed inter-chunk Q S_in^T
-    const int t_of = tb * 32, i_of = xb * 32;
-    f32x16 intra = zero16();
-    for (int sb = 0; sb <= tb; ++sb)
-        intra = mma32(sP + t_of * SP + sb * 32, SP, sVT + i_of * SP + sb * 32, SP, 32, intra);
-    f32x16 inter = mma32(sQ + t_of * SR, SR, sShi + i_of * SR, SR, R1_DH, zero16());
-    inter = mma32(sQ + t_of * SR, SR, sSlo + i_of * SR, SR, R1_DH, inter);
-    TO* y = static_cast<TO*>(p.y);
-    const int col = i_of + (lane & 31);
+}
+
+// ---------------------------------------------------------------------------
+// K_C: outputs of one super-chunk, four sub-chunks in order.
+// ---------------------------------------------------------------------------
+template <typename TF, typename TI, typename TO>
+__global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p) {
+    __shared__ __attribute__((aligned(16))) bf16_t sQ[R1_T * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sK[R1_T * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sVT[R1_DH * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sKT[R1_DH * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sP[R1_T * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sShi[R1_DH * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sSlo[R1_DH * R1_SR];
+    __shared__ float sLc[R1_T], sOmf[R1_T];
+    const int sc = blockIdx.x;
+    const int seq = blockIdx.y;
+    const int b = seq / p.H, h = seq - (seq / p.H) * p.H;
+    const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + h;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tb = w >> 1, xb = w & 1;   // this wave's 32-row block and 32-column block
+    const TI* qp = static_cast<const TI*>(p.q);
+    const TI* kp = static_cast<const TI*>(p.k);
+    const TI* vp = static_cast<const TI*>(p.v);
+    const TF* fp = static_cast<const TF*>(p.f);
+    TO* yp = static_cast<TO*>(p.y);
+
+    const int64_t tsc = static_cast<int64_t>(sc) * R1_RS;
+    TF fraw = load_f<TF>(fp, rowbase, tsc + lane, p.L, p.H);
+    Tile8<TI> qt = load_tile<TI>(qp, rowbase, tsc, p.L, p.H);
+    Tile8<TI> kt = load_tile<TI>(kp, rowbase, tsc, p.L, p.H);
+    Tile8<TI> vt = load_tile<TI>(vp, rowbase, tsc, p.L, p.H);
+
+    // state tile (rows tb, columns xb) of S_in in the accumulator layout
+    f32x16 S;
+    {
+        const float* src = p.Sin + (static_cast<int64_t>(seq) * p.nsc + sc) * R1_DH * R1_DH;
+        const int col = xb * 32 + (lane & 31);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int t = t_of + mrow(r);
-        if (t0 + t < p.L) {
-            const float val = intra[r] + expf(sLc[t]) * inter[r];
-            y[(rowbase + (t0 + t) * p.H) * R1_DH + col] = IO<TO>::st(val);
+        for (int r = 0; r < 16; ++r) S[r] = src[(tb * 32 + mrow(r)) * R1_DH + col];
+    }
+    auto put_state = [&]() {
+        const int col = xb * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float x = S[r];
+            const bf16_t hi = f32_to_bf16(x);
+            sShi[(tb * 32 + mrow(r)) * R1_SR + col] = hi;
+            sSlo[(tb * 32 + mrow(r)) * R1_SR + col] = f32_to_bf16(x - bf16_to_f32(hi));
         }
+    };
+    put_state();
+
+    const int nsub = static_cast<int>((p.L - tsc + R1_T - 1) / R1_T) < R1_SUB
+                         ? static_cast<int>((p.L - tsc + R1_T - 1) / R1_T)
+                         : R1_SUB;
+    for (int sub = 0; sub < nsub; ++sub) {
+        const int64_t t0 = tsc + static_cast<int64_t>(sub) * R1_T;
+        // stage this sub-chunk; then start loading the next one
+        put_rows(qt, sQ);
+        put_rows(kt, sK);
+        put_cols(kt, sKT);
+        put_cols(vt, sVT);
+        if (w == 0) {
+            const float fv = fval<TF>(fraw, t0 + lane, p.L);
+            sLc[lane] = wave_incl_scan(fmaxf(logf(fv), R1_LOG_MIN));
+            sOmf[lane] = 1.0f - fv;
+        }
+        __syncthreads();
+        if (sub + 1 < nsub) {
+            qt = load_tile<TI>(qp, rowbase, t0 + R1_T, p.L, p.H);
+            kt = load_tile<TI>(kp, rowbase, t0 + R1_T, p.L, p.H);
+            vt = load_tile<TI>(vp, rowbase, t0 + R1_T, p.L, p.H);
+            fraw = load_f<TF>(fp, rowbase, t0 + R1_T + lane, p.L, p.H);
+        }
+        // P = (Q K^T) o exp(Lc_t - Lc_s) (1 - f_s) on s <= t (tile (tb, xb); xb > tb unused)
+        if (xb <= tb) {
+            const int t_of = tb * 32, s_of = xb * 32;
+            f32x16 acc = mma32(sQ + t_of * R1_SR, R1_SR, sK + s_of * R1_SR, R1_SR, R1_DH, zero16());
+            const int s = s_of + (lane & 31);
+            const float lcs = sLc[s], omf = sOmf[s];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = t_of + mrow(r);
+                const float pv = (s <= t) ? acc[r] * expf(sLc[t] - lcs) * omf : 0.0f;
+                sP[t * R1_SR + s] = f32_to_bf16(pv);
+            }
+        }
+        __syncthreads();
+        // y tile (rows tb, columns xb): intra-chunk P V + decayed inter-chunk Q S^T
+        {
+            const int t_of = tb * 32, i_of = xb * 32;
+            f32x16 intra = zero16();
+            for (int sb = 0; sb <= tb; ++sb)
+                intra = mma32(sP + t_of * R1_SR + sb * 32, R1_SR, sVT + i_of * R1_SR + sb * 32, R1_SR,
+                              32, intra);
+            f32x16 inter = mma32(sQ + t_of * R1_SR, R1_SR, sShi + i_of * R1_SR, R1_SR, R1_DH, zero16());
+            inter = mma32(sQ + t_of * R1_SR, R1_SR, sSlo + i_of * R1_SR, R1_SR, R1_DH, inter);
+            const int col = i_of + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = t_of + mrow(r);
+                if (t0 + t < p.L) {
+                    const float val = intra[r] + expf(sLc[t]) * inter[r];
+                    yp[(rowbase + (t0 + t) * p.H) * R1_DH + col] = IO<TO>::st(val);
+                }
+            }
+        }
+        __syncthreads();   // sVT (unscaled) and the old state halves are consumed
+        // S <- exp(Lc_T) S + V^T diag(w) K  with w_s = exp(Lc_T - Lc_s) (1 - f_s)
+        {
+            const float lcT = sLc[R1_T - 1];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int e = tid + R1_THREADS * u;   // over DH x T
+                const int i = e >> 6, s = e & 63;
+                bf16_t& x = sVT[i * R1_SR + s];
+                x = f32_to_bf16(bf16_to_f32(x) * (expf(lcT - sLc[s]) * sOmf[s]));
+            }
+            __syncthreads();
+            f32x16 dS = mma32(sVT + tb * 32 * R1_SR, R1_SR, sKT + xb * 32 * R1_SR, R1_SR, R1_T, zero16());
+            const float dec = expf(lcT);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) S[r] = fmaf(dec, S[r], dS[r]);
+            put_state();
+        }
+        __syncthreads();   // tiles of this sub-chunk consumed before the next staging
     }
 }
 
 namespace {
 
 struct R1Geo {
-    int nch;
+    int nsc;
     size_t off_ds, off_lct, off_sin, bytes;
 };
 
 R1Geo r1_geometry(int64_t B, int64_t L, int64_t H) {
     R1Geo g{};
-    g.nch = static_cast<int>((L + R1_T - 1) / R1_T);
+    g.nsc = static_cast<int>((L + R1_RS - 1) / R1_RS);
     const size_t nseq = static_cast<size_t>(B) * H;
     size_t off = WS_HDR_BYTES;
     auto take = [&](size_t n) { size_t o = off; off = round_up(off + n, 256); return o; };
-    g.off_ds = take(nseq * g.nch * R1_DH * R1_DH * sizeof(float));
-    g.off_lct = take(nseq * g.nch * sizeof(float));
-    g.off_sin = take(nseq * g.nch * R1_DH * R1_DH * sizeof(float));
+    g.off_ds = take(nseq * g.nsc * R1_DH * R1_DH * sizeof(float));
+    g.off_lct = take(nseq * g.nsc * sizeof(float));
+    g.off_sin = take(nseq * g.nsc * R1_DH * R1_DH * sizeof(float));
     g.bytes = off;
     return g;
 }
 
 template <typename TF, typename TI, typename TO>
 int run_rank1(const Rank1Params& prm, int n_seq, hipStream_t st) {
-    const dim3 grid(prm.nch, n_seq);
+    const dim3 grid(prm.nsc, n_seq);
     hipLaunchKernelGGL((rank1_summary_kernel<TF, TI>), grid, dim3(R1_THREADS), 0, st, prm);
     int rc = check_launch("rank1_summary_kernel");
     if (rc) return rc;
@@ -282,13 +451,14 @@ extern "C" int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const v
     if (!workspace || workspace_bytes < g.bytes)
         return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", g.bytes, workspace_bytes);
     if (batch * heads > 65535) return set_error(MOGT_E_INVALID, "batch * heads > 65535");
+    if (length > (int64_t(1) << 40)) return set_error(MOGT_E_INVALID, "length too large");
     char* base = static_cast<char*>(workspace);
     Rank1Params prm{};
     prm.f = f; prm.k = k; prm.v = v; prm.q = q; prm.y = y;
     prm.dS = reinterpret_cast<float*>(base + g.off_ds);
     prm.lcT = reinterpret_cast<float*>(base + g.off_lct);
     prm.Sin = reinterpret_cast<float*>(base + g.off_sin);
-    prm.L = length; prm.H = static_cast<int>(heads); prm.nch = g.nch;
+    prm.L = length; prm.H = static_cast<int>(heads); prm.nsc = g.nsc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n_seq = static_cast<int>(batch * heads);
     const bool fb = f_dtype == MOGT_BF16, ib = kvq_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
