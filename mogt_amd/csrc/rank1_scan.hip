@@ -4,10 +4,11 @@
 // rank-1 write V_t = (1 - f_t) v_t k_t^T, read out through q_t.  S_t (d x d per
 // step) is never written to memory.
 //
-// Chunked form.  Inside a block of steps with Lc_t = sum_{u<=t} log f_u (block
-// local) and S_in the state before the block:
-//   y_t   = exp(Lc_t) S_in q_t + sum_{s<=t} exp(Lc_t - Lc_s) (1 - f_s) (q_t . k_s) v_s
-//   S_out = exp(Lc_T) S_in + V^T diag(w) K,   w_s = exp(Lc_T - Lc_s) (1 - f_s)
+// Chunked form.  Inside a block of steps with Lc_t = sum_{u<=t} log2 f_u (block
+// local; decays are 2^(Lc_t - Lc_s), one v_exp_f32 each) and S_in the state
+// before the block:
+//   y_t   = 2^Lc_t S_in q_t + sum_{s<=t} 2^(Lc_t - Lc_s) (1 - f_s) (q_t . k_s) v_s
+//   S_out = 2^Lc_T S_in + V^T diag(w) K,   w_s = 2^(Lc_T - Lc_s) (1 - f_s)
 // Three launches over super-chunks of RS = 256 steps:
 //   K_A  per super-chunk: dS = V^T diag(w) K over its 256 steps (one bf16 MFMA
 //        chain, K = 256) and its total log-decay.
@@ -15,8 +16,8 @@
 //        compose element-wise with a scalar decay, so this is a plain scan.
 //   K_C  per super-chunk: four 64-step sub-chunks in order, the 64 x 64 state
 //        carried in MFMA accumulators; per sub-chunk the masked, decayed
-//        (Q K^T) V plus exp(Lc) Q S^T (state split into bf16 hi + lo parts for
-//        fp32-level accuracy), then S <- exp(Lc_T) S + V^T diag(w) K.  The next
+//        (Q K^T) V plus 2^Lc Q S^T (state split into bf16 hi + lo parts for
+//        fp32-level accuracy), then S <- 2^Lc_T S + V^T diag(w) K.  The next
 //        sub-chunk's q, k, v are loaded into registers while this one computes.
 // K_A reads k and v with ordinary (cache-allocating) loads, so K_C usually finds
 // them in the Infinity Cache.  Layouts: f [B, L, H]; q, k, v, y [B, L, H, DH].
@@ -34,7 +35,7 @@ constexpr int R1_RS = R1_T * R1_SUB;
 constexpr int R1_THREADS = 256;   // 4 waves
 constexpr int R1_PAD = 8;         // LDS row padding (bf16): rows of 144 B
 constexpr int R1_SR = R1_DH + R1_PAD;
-constexpr float R1_LOG_MIN = -80.0f;
+constexpr float R1_LOG2_MIN = -120.0f;   // clamp of log2 f (f = 0 -> 2^-120 per step)
 
 struct Rank1Params {
     const void* f;
@@ -194,12 +195,12 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p
 
     // block-wide inclusive log-decay cumsum over the 256 steps (one per thread)
     const float fv = fval<TF>(fraw, t0 + tid, p.L);
-    float lc = wave_incl_scan(fmaxf(logf(fv), R1_LOG_MIN));
+    float lc = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
     if (lane == 63) sWave[w] = lc;
     __syncthreads();
     for (int i = 0; i < w; ++i) lc += sWave[i];
     const float lcT = sWave[0] + sWave[1] + sWave[2] + sWave[3];
-    sW[tid] = expf(lcT - lc) * (1.0f - fv);
+    sW[tid] = exp2f(lcT - lc) * (1.0f - fv);
 
     const int ib = w >> 1, jb = w & 1;   // this wave's 32x32 tile of dS[i][j]
     f32x16 acc = zero16();
@@ -236,28 +237,29 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p
 }
 
 // ---------------------------------------------------------------------------
-// K_B: carries.  One thread per state element; the super-chunk summaries are
-// loaded in batches of 8 ahead of the dependent multiply-adds.
+// K_B: carries.  One thread per state element; the summaries of up to 32
+// super-chunks are loaded at once, ahead of the dependent multiply-adds.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rank1_carry_kernel(Rank1Params p) {
     const int seq = blockIdx.y;
     const int e = blockIdx.x * 256 + threadIdx.x;   // < DH*DH
     const int64_t base = static_cast<int64_t>(seq) * p.nsc;
     constexpr int64_t SZ = R1_DH * R1_DH;
+    constexpr int NB = 32;
     float S = 0.0f;
-    for (int c0 = 0; c0 < p.nsc; c0 += 8) {
-        float d[8], dec[8];
+    for (int c0 = 0; c0 < p.nsc; c0 += NB) {
+        float d[NB], dec[NB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const bool ok = c0 + i < p.nsc;
-            d[i] = ok ? p.dS[(base + c0 + i) * SZ + e] : 0.0f;
-            dec[i] = ok ? p.lcT[base + c0 + i] : 0.0f;
+        for (int i = 0; i < NB; ++i) {
+            const int c = min(c0 + i, p.nsc - 1);   // in-bounds, unconditional
+            d[i] = p.dS[(base + c) * SZ + e];
+            dec[i] = p.lcT[base + c];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NB; ++i) {
             if (c0 + i < p.nsc) {
                 p.Sin[(base + c0 + i) * SZ + e] = S;
-                S = fmaf(expf(dec[i]), S, d[i]);
+                S = fmaf(exp2f(dec[i]), S, d[i]);
             }
         }
     }
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
         put_cols(vt, sVT);
         if (w == 0) {
             const float fv = fval<TF>(fraw, t0 + lane, p.L);
-            sLc[lane] = wave_incl_scan(fmaxf(logf(fv), R1_LOG_MIN));
+            sLc[lane] = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
             sOmf[lane] = 1.0f - fv;
         }
         __syncthreads();
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = t_of + mrow(r);
-                const float pv = (s <= t) ? acc[r] * expf(sLc[t] - lcs) * omf : 0.0f;
+                const float pv = (s <= t) ? acc[r] * exp2f(sLc[t] - lcs) * omf : 0.0f;
                 sP[t * R1_SR + s] = f32_to_bf16(pv);
             }
         }
@@ -364,7 +366,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
             for (int r = 0; r < 16; ++r) {
                 const int t = t_of + mrow(r);
                 if (t0 + t < p.L) {
-                    const float val = intra[r] + expf(sLc[t]) * inter[r];
+                    const float val = intra[r] + exp2f(sLc[t]) * inter[r];
                     yp[(rowbase + (t0 + t) * p.H) * R1_DH + col] = IO<TO>::st(val);
                 }
             }
@@ -378,11 +380,11 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
                 const int e = tid + R1_THREADS * u;   // over DH x T
                 const int i = e >> 6, s = e & 63;
                 bf16_t& x = sVT[i * R1_SR + s];
-                x = f32_to_bf16(bf16_to_f32(x) * (expf(lcT - sLc[s]) * sOmf[s]));
+                x = f32_to_bf16(bf16_to_f32(x) * (exp2f(lcT - sLc[s]) * sOmf[s]));
             }
             __syncthreads();
             f32x16 dS = mma32(sVT + tb * 32 * R1_SR, R1_SR, sKT + xb * 32 * R1_SR, R1_SR, R1_T, zero16());
-            const float dec = expf(lcT);
+            const float dec = exp2f(lcT);
 #pragma unroll
             for (int r = 0; r < 16; ++r) S[r] = fmaf(dec, S[r], dS[r]);
             put_state();
