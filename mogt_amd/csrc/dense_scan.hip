@@ -3,332 +3,242 @@
 // Semantics: affine_scan_sequential (affine_scan.py:14-62), fp32 state, H_0 = 0,
 // optional prefix products P_t = U_t ... U_1; the chunk/carry decomposition of
 // affine_scan_block_reference (affine_scan.py:175-278) and the reference's
-// hybrid path (triton_scan.py:232-311), re-designed so no L x R x C
-// intermediate is written and the carry is applied in registers:
+// hybrid path (triton_scan.py:232-311), re-designed so that no L x R x C
+// intermediate is written and every contraction runs on fp32 MFMA.
 //
-//   K1 chunk pass    one wave per (chunk, column block, sequence).  Lane l owns
-//                    one column of the augmented state [P | H] (P columns
-//                    0..R-1, then up to 64-R columns of H) and runs the chunk's
-//                    recurrence serially with U_t read as wave-uniform values;
-//                    writes the chunk summary (P_T, H_T) -- or, for the local
-//                    scan API, every step's local prefix.
-//   K2 carry pass    one work-group per group of GS consecutive chunk summaries:
-//                    folds its group with the whole work-group (column-owner
-//                    threads, broadcast row reads from LDS), chains the groups
-//                    with the decoupled look-back of common.h, then writes the
-//                    exclusive carry (state before the chunk) of every chunk.
-//   K3 output pass   K1's recurrence restarted from the chunk's carry; writes
-//                    H_t (and P_t) once.
-//
-// Composition of affine elements (the reference's affine_combine,
-// affine_scan.py:4-11): (P_a, H_a) o (P_b, H_b) = (P_a P_b, P_a H_b + H_a).
+// One kernel (dense_chunk_kernel) runs the recurrence X_t = U_t X_{t-1} +
+// [0 | V_t] on the augmented state X = [P | H] over chunks of T steps, one wave
+// per (chunk, column block, sequence), with X held in MFMA accumulators (see
+// the kernel comment).  Its modes give every pass of the scan:
+//   SUMMARY  X_0 = [I | 0]; writes the chunk's (P_T, H_T).
+//   LOCAL    the same, plus every step's local (P_t, H_t) (the block-local scan).
+//   EXCL     X_0 = the chunk's carry (or [I | 0]); writes the state *before*
+//            every step, i.e. exclusive prefixes.
+//   OUTPUT   X_0 = the chunk's carry; writes H_t (and P_t) after every step.
+// The carries are themselves an affine scan: (P_T, H_T) of consecutive chunks
+// compose exactly like (U_t, V_t) -- the reference's affine_combine
+// (affine_scan.py:4-11), (P_a, H_a) o (P_b, H_b) = (P_a P_b, P_a H_b + H_a).
+// So the summaries, laid out like U and V, are scanned by the same kernel,
+// recursively: summaries of summaries until one chunk remains, then EXCL passes
+// back down produce every level's carries, and the OUTPUT pass of level 0
+// writes H once.  Each pass is independent per chunk (no inter-chunk waits).
 #include "common.h"
 
 namespace mogt {
 
-struct DenseParams {
-    const float* U;     // [B, L, R, R] fp32
-    const void* V;      // [B, L, R, C] (fp32 or bf16); null for the transport-only scan
-    void* H;            // K3: [B, L, R, C] output; K1 local mode: H_prefix (fp32)
-    void* P;            // K3: [B, L, R, R] prefix output or null; K1 local: U_prefix
-    float* Psum;        // [B, nb, R, R]
-    float* Hsum;        // [B, nb, R, C]
-    float* Pcar;        // [B, nb, R, R]   state before each chunk (exclusive carry)
-    float* Hcar;        // [B, nb, R, C]
-    int64_t L;
-    int R, C, T, nb, Cb, n_cblk;
-    int GS, n_grp;      // K2 grouping
-    uint32_t* hdr;
-    uint32_t* flags;    // [B * n_cblk][n_grp]
-    uint64_t* pay;      // 4 planes of [B * n_cblk][n_grp][R*(R+Cb)] words
-    int64_t plane;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum ChunkMode { CM_SUMMARY = 0, CM_LOCAL = 1, CM_EXCL = 2, CM_OUTPUT = 3 };
+
+struct ChunkParams {
+    const float* U;      // [B, L, R, R] fp32 (level 0) or chunk products of the level below
+    const void* V;       // [B, L, R, C] (fp32 / bf16; level >= 1: fp32); null if C == 0
+    const float* carP;   // [B, nb, R, R] chunk carries (EXCL / OUTPUT); null = identity
+    const float* carH;   // [B, nb, R, C]                                ; null = zero
+    void* outP;          // per-step P: LOCAL fp32 / EXCL fp32 / OUTPUT TO (may be null)
+    void* outH;          // per-step H: LOCAL fp32 / EXCL fp32 / OUTPUT TO
+    float* sumP;         // [B, nb, R, R] chunk products (SUMMARY / LOCAL)
+    float* sumH;         // [B, nb, R, C]
+    int64_t L;           // steps of this level
+    int R, C, T, nb;
+    int withP;           // carry / write the P columns (column block 0 only)
 };
 
-enum ChunkMode { CM_SUMMARY = 0, CM_LOCAL = 1, CM_OUTPUT = 2 };
-
-// One wave: runs the recurrence of chunk `k` of sequence `b`, column block `cb`.
-// EXACT: R == RMAX at compile time (unguarded loops, wide scalar loads of U_t).
-template <int RMAX, bool EXACT, typename TV, typename TO, int MODE, bool PREFIX>
-__global__ __launch_bounds__(64) void dense_chunk_kernel(DenseParams p, const float* __restrict__ Ug,
-                                                         const TV* __restrict__ Vb, TO* __restrict__ Ho) {
+// Chunk pass on fp32 MFMA (v_mfma_f32_16x16x4_f32), one wave per (chunk k,
+// column block cb, sequence b).  X = [P | H] is padded to 16-row tiles; tile
+// (rt, ct) is 4 accumulator registers, lane (g = lane/16, n = lane%16) holding
+// X[16 rt + 4 g + i][16 ct + n], i = 0..3.  Per output tile, X_t = U_t X_{t-1}
+// + [0 | V_t] is RT x 4 MFMAs over the contraction index j = 16 kt + 4 g + kk
+// (K-step kk): with that assignment the B operand of K-step kk is accumulator
+// register kk of the previous step in the same lane, so the state never moves
+// between steps, and the A operand U_t[16 rt + m][16 kt + 4 g + kk] is four
+// consecutive floats of one row of U_t per lane (one 16-byte load when R is a
+// multiple of 4).  The operands of the next D steps are always in flight.
+// Rows and columns past R / C read a clamped in-bounds address and count as 0.
+template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE>
+__global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
+    constexpr int NT = RT + CTW;          // column tiles: RT of P, then CTW of H
+    constexpr int D = RT == 1 ? 3 : 2;    // steps of operands in flight
     const int k = blockIdx.x;
     const int cb = blockIdx.y;
     const int b = blockIdx.z;
     const int lane = threadIdx.x;
-    const int R = EXACT ? RMAX : p.R;
-    const bool isP = lane < R;
-    const int hc = cb * p.Cb + (lane - R);                   // H column of this lane
-    const bool isH = !isP && lane - R < p.Cb && hc < p.C;
-    const bool pOwner = isP && cb == 0;                       // P written by block 0 only
+    const int g = lane >> 4, n = lane & 15;
+    const int R = p.R, C = p.C;
+    const int c0 = cb * (16 * CTW);
+    const bool hasP = cb == 0 && (MODE == CM_SUMMARY || MODE == CM_LOCAL || p.withP);
+    const int nH = C <= c0 ? 0 : min(CTW, (C - c0 + 15) / 16);
     const int64_t t0 = static_cast<int64_t>(k) * p.T;
     const int64_t t1 = t0 + p.T < p.L ? t0 + p.T : p.L;
-    const int64_t seq = static_cast<int64_t>(b) * p.nb + k;  // summary / carry index
+    const int64_t seq = static_cast<int64_t>(b) * p.nb + k;
+    const int64_t RR = static_cast<int64_t>(R) * R;
+    const TV* Vg = static_cast<const TV*>(p.V);
 
-    float col[RMAX];
-    if constexpr (MODE == CM_OUTPUT) {
+    auto trow = [&](int rt, int i) { return 16 * rt + 4 * g + i; };
+    auto pcol = [&](int ct) { return 16 * ct + n; };               // ct < RT
+    auto hcol = [&](int ct) { return c0 + 16 * (ct - RT) + n; };   // ct >= RT
+    auto live = [&](int ct) { return ct < RT ? hasP : (ct - RT < nH); };
+
+    // ---- initial state ------------------------------------------------------
+    f32x4 X[RT][NT];
+    const bool fromCarry = (MODE == CM_EXCL || MODE == CM_OUTPUT) && p.carH != nullptr;
 #pragma unroll
-        for (int i = 0; i < RMAX; ++i) {
-            float x = 0.0f;
-            if (i < R) {
-                if (isP) x = p.Pcar[seq * R * R + i * R + lane];
-                else if (isH) x = p.Hcar[(seq * R + i) * p.C + hc];
-            }
-            col[i] = x;
-        }
-    } else {
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int i = 0; i < RMAX; ++i) col[i] = (isP && i == lane) ? 1.0f : 0.0f;
-    }
-
-    for (int64_t t = t0; t < t1; ++t) {
-        // U_t is wave-uniform: read through the scalar data cache.
-        const float* __restrict__ Ut = Ug + (static_cast<int64_t>(b) * p.L + t) * R * R;
-        float nw[RMAX];
+        for (int ct = 0; ct < NT; ++ct)
 #pragma unroll
-        for (int i = 0; i < RMAX; ++i) {
-            float acc = 0.0f;
-            if (i < R && isH && Vb) acc = IO<TV>::ld(Vb[((static_cast<int64_t>(b) * p.L + t) * R + i) * p.C + hc]);
-            nw[i] = acc;
-        }
-#pragma unroll
-        for (int i = 0; i < RMAX; ++i) {
-            if (i < R) {
-#pragma unroll
-                for (int j = 0; j < RMAX; ++j)
-                    if (j < R) nw[i] = fmaf(Ut[i * R + j], col[j], nw[i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < RMAX; ++i) col[i] = nw[i];
-
-        if constexpr (MODE == CM_LOCAL) {
-            float* Pl = static_cast<float*>(p.P);
-            float* Hl = static_cast<float*>(p.H);
-#pragma unroll
-            for (int i = 0; i < RMAX; ++i) {
-                if (i < R) {
-                    if (pOwner) Pl[((static_cast<int64_t>(b) * p.L + t) * R + i) * R + lane] = col[i];
-                    else if (isH) Hl[((static_cast<int64_t>(b) * p.L + t) * R + i) * p.C + hc] = col[i];
-                }
-            }
-        } else if constexpr (MODE == CM_OUTPUT) {
-#pragma unroll
-            for (int i = 0; i < RMAX; ++i) {
-                if (i < R) {
-                    if (isH) Ho[((static_cast<int64_t>(b) * p.L + t) * R + i) * p.C + hc] = IO<TO>::st(col[i]);
-                    if constexpr (PREFIX) {
-                        if (pOwner)
-                            static_cast<TO*>(p.P)[((static_cast<int64_t>(b) * p.L + t) * R + i) * R + lane] =
-                                IO<TO>::st(col[i]);
-                    }
-                }
-            }
-        }
-    }
-
-    if constexpr (MODE != CM_OUTPUT) {
-#pragma unroll
-        for (int i = 0; i < RMAX; ++i) {
-            if (i < R) {
-                if (pOwner) p.Psum[seq * R * R + i * R + lane] = col[i];
-                else if (isH) p.Hsum[(seq * R + i) * p.C + hc] = col[i];
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// K2: carries.  Affine elements live in LDS as [P | H] with row stride W = R + Wc
-// (this column block only), so a composition is one R x R by R x W product.
-// ---------------------------------------------------------------------------
-constexpr int K2_THREADS = 512;
-
-// out = a o b for [R][W] elements in LDS (out must not alias a or b).
-// Thread <-> (column c, row slice): b's column stays in registers, the rows of
-// P_a are wave-uniform (broadcast) LDS reads.
-template <int RMAX>
-__device__ void compose_lds(const float* a, const float* bm, float* out, int R, int W) {
-    constexpr int SLICES = K2_THREADS / 64;
-    const int c = threadIdx.x & 63;
-    const int sl = threadIdx.x >> 6;
-    if (c < W) {
-        float bc[RMAX];
-#pragma unroll
-        for (int kk = 0; kk < RMAX; ++kk) bc[kk] = kk < R ? bm[kk * W + c] : 0.0f;
-        for (int i = sl; i < R; i += SLICES) {
-            float acc = c >= R ? a[i * W + c] : 0.0f;   // + H_a on H columns
-#pragma unroll
-            for (int kk = 0; kk < RMAX; ++kk)
-                if (kk < R) acc = fmaf(a[i * W + kk], bc[kk], acc);
-            out[i * W + c] = acc;
-        }
-    }
-}
-
-template <int RMAX>
-__global__ __launch_bounds__(K2_THREADS) void dense_carry_kernel(DenseParams p) {
-    constexpr int EMAX = RMAX * 64;   // max R * W (R + Cb <= 64)
-    __shared__ float s_buf[4][EMAX];
-    __shared__ uint32_t s_epoch;
-    __shared__ int s_nfold, s_found;
-
-    const uint32_t epoch = ws_epoch(p.hdr, &s_epoch);
-    const int grp = blockIdx.x;
-    const int cb = blockIdx.y;
-    const int b = blockIdx.z;
-    const int R = p.R;
-    const int c0 = cb * p.Cb;
-    const int Wc = (p.C - c0) < p.Cb ? (p.C - c0) : p.Cb;    // H columns of this block
-    const int W = R + Wc;
-    const int E = R * W;
-    const int k0 = grp * p.GS;
-    const int k1 = (k0 + p.GS) < p.nb ? (k0 + p.GS) : p.nb;
-    const int tid = threadIdx.x;
-
-    float* grpc = s_buf[0];   // composite of this group's summaries
-    float* acc = s_buf[1];    // running composite / state
-    float* elt = s_buf[2];    // element being folded in
-    float* tmp = s_buf[3];
-
-    auto load_summary = [&](int k, float* dst) {
-        const int64_t seq = static_cast<int64_t>(b) * p.nb + k;
-        for (int e = tid; e < E; e += K2_THREADS) {
-            const int i = e / W, j = e - i * W;
-            dst[e] = j < R ? p.Psum[seq * R * R + i * R + j]
-                           : p.Hsum[(seq * R + i) * p.C + c0 + (j - R)];
-        }
-    };
-    auto set_identity = [&](float* dst) {
-        for (int e = tid; e < E; e += K2_THREADS) {
-            const int i = e / W, j = e - i * W;
-            dst[e] = (j == i) ? 1.0f : 0.0f;
-        }
-    };
-    auto swap = [](float*& x, float*& y) { float* t = x; x = y; y = t; };
-
-    // 1. composite of this group's chunk summaries: S_{k1-1} o ... o S_{k0}.
-    load_summary(k0, grpc);
-    __syncthreads();
-    for (int k = k0 + 1; k < k1; ++k) {
-        load_summary(k, elt);
-        __syncthreads();
-        compose_lds<RMAX>(elt, grpc, tmp, R, W);
-        __syncthreads();
-        swap(grpc, tmp);
-    }
-
-    // 2. decoupled look-back over the groups of this (sequence, column block)
-    //    chain; `acc` ends as the inclusive prefix before this group (carry-in).
-    const uint32_t tagA = make_tag(epoch, ST_AGG);
-    const uint32_t tagI = make_tag(epoch, ST_INC);
-    const int64_t chain = static_cast<int64_t>(b) * p.n_cblk + cb;
-    const int64_t EW = static_cast<int64_t>(R) * (R + p.Cb);   // words per group slot
-    uint64_t* aggW = p.pay;
-    uint64_t* incW = p.pay + p.plane;
-    uint32_t* flg = p.flags + chain * p.n_grp;
-    auto slot = [&](int g) { return (chain * p.n_grp + g) * EW; };
-
-    set_identity(acc);
-    if (grp == 0) {
-        for (int e = tid; e < E; e += K2_THREADS) st_relaxed(&incW[slot(0) + e], pack_word(grpc[e], tagI));
-        __syncthreads();
-        if (tid == 0) st_relaxed(&flg[0], make_tag(epoch, ST_INC));
-    } else {
-        for (int e = tid; e < E; e += K2_THREADS) st_relaxed(&aggW[slot(grp) + e], pack_word(grpc[e], tagA));
-        __syncthreads();
-        if (tid == 0) st_relaxed(&flg[grp], make_tag(epoch, ST_AGG));
-        int p_hi = grp - 1;
-        while (true) {
-            if (tid < 64) {
-                uint32_t spins = 0;
-                while (true) {
-                    const int pc = p_hi - tid;
-                    uint32_t st = 0;
-                    if (pc >= 0) {
-                        const uint32_t w = ld_relaxed(&flg[pc]);
-                        st = ((w >> 2) == epoch) ? (w & 3u) : 0u;
-                    }
-                    const uint64_t inc_m = __ballot(pc >= 0 && st == ST_INC);
-                    const uint64_t nr_m = __ballot(pc >= 0 && st == 0u);
-                    bool ok;
-                    int nf, found;
-                    if (inc_m) {
-                        const int j = __ffsll(static_cast<long long>(inc_m)) - 1;
-                        const uint64_t below = (j == 0) ? 0ull : ((1ull << j) - 1ull);
-                        ok = (nr_m & below) == 0ull;
-                        nf = j;
-                        found = 1;
+            for (int i = 0; i < 4; ++i) {
+                const int r = trow(rt, i);
+                float x = 0.0f;
+                if (ct < RT) {
+                    if (fromCarry && p.carP) {
+                        if (hasP && r < R && pcol(ct) < R) x = p.carP[seq * RR + r * R + pcol(ct)];
                     } else {
-                        ok = nr_m == 0ull;
-                        nf = 64;
-                        found = 0;
+                        x = (r == pcol(ct) && r < R) ? 1.0f : 0.0f;
                     }
-                    if (!ok && ++spins > MAX_SPIN) {
-                        if (tid == 0) note_timeout(p.hdr);
-                        ok = true;
-                        if (!inc_m) { nf = p_hi + 1 < 64 ? p_hi + 1 : 64; found = 0; }
-                        if (p_hi - nf < 0) { nf = p_hi; found = 1; }
-                    }
-                    if (ok) {
-                        if (tid == 0) { s_nfold = nf; s_found = found; }
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
+                } else if (fromCarry && ct - RT < nH && r < R && hcol(ct) < C) {
+                    x = p.carH[(seq * R + r) * C + hcol(ct)];
+                }
+                X[rt][ct][i] = x;
+            }
+
+    // ---- operands of one step: A (rows of U_t) and C (V_t) tiles ----------
+    struct Ops {
+        f32x4 A[RT][RT];
+        f32x4 Cv[RT][CTW];
+    };
+    auto load_ops = [&](int64_t t, Ops& o) {
+        const float* Ut = p.U + (static_cast<int64_t>(b) * p.L + t) * RR;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int kt = 0; kt < RT; ++kt) {
+                const int r = min(16 * rt + n, R - 1);
+                if constexpr (U4) {
+                    const int c = min(16 * kt + 4 * g, R - 4);
+                    o.A[rt][kt] = *reinterpret_cast<const f32x4*>(Ut + r * R + c);
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) o.A[rt][kt][kk] = Ut[r * R + min(16 * kt + 4 * g + kk, R - 1)];
                 }
             }
-            __syncthreads();
-            const int nf = s_nfold;
-            const int found = s_found;
-            // acc <- acc o agg_{p_hi} o agg_{p_hi-1} o ... (newest first)
-            for (int q = 0; q < nf; ++q) {
-                const int64_t base = slot(p_hi - q);
-                for (int e = tid; e < E; e += K2_THREADS) elt[e] = wait_word(&aggW[base + e], tagA, p.hdr);
-                __syncthreads();
-                compose_lds<RMAX>(acc, elt, tmp, R, W);
-                __syncthreads();
-                swap(acc, tmp);
-            }
-            if (found) {
-                const int64_t base = slot(p_hi - nf);
-                for (int e = tid; e < E; e += K2_THREADS) elt[e] = wait_word(&incW[base + e], tagI, p.hdr);
-                __syncthreads();
-                compose_lds<RMAX>(acc, elt, tmp, R, W);
-                __syncthreads();
-                swap(acc, tmp);
-                break;
-            }
-            p_hi -= nf;
-            __syncthreads();
+        if (Vg) {
+            const TV* Vt = Vg + (static_cast<int64_t>(b) * p.L + t) * R * static_cast<int64_t>(C);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int h = 0; h < CTW; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = min(trow(rt, i), R - 1);
+                        const int c = min(c0 + 16 * h + n, C - 1);
+                        // raw value (bf16: its bit pattern), converted when masked
+                        const TV raw = Vt[static_cast<int64_t>(r) * C + c];
+                        if constexpr (sizeof(TV) == 4) o.Cv[rt][h][i] = raw;
+                        else o.Cv[rt][h][i] = __uint_as_float(static_cast<uint32_t>(raw));
+                    }
         }
-        // publish this group's inclusive prefix: grpc o acc
-        compose_lds<RMAX>(grpc, acc, tmp, R, W);
-        __syncthreads();
-        for (int e = tid; e < E; e += K2_THREADS) st_relaxed(&incW[slot(grp) + e], pack_word(tmp[e], tagI));
-        __syncthreads();
-        if (tid == 0) st_relaxed(&flg[grp], make_tag(epoch, ST_INC));
+    };
+    // Convert and zero the padding of a loaded operand set (values past R / C).
+    auto mask_ops = [&](Ops& o) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+            for (int kt = 0; kt < RT; ++kt)
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    if (16 * rt + n >= R || 16 * kt + 4 * g + kk >= R) o.A[rt][kt][kk] = 0.0f;
+#pragma unroll
+            for (int h = 0; h < CTW; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = o.Cv[rt][h][i];
+                    if constexpr (sizeof(TV) == 2) v = __uint_as_float(__float_as_uint(v) << 16);
+                    o.Cv[rt][h][i] = (!Vg || trow(rt, i) >= R || c0 + 16 * h + n >= C) ? 0.0f : v;
+                }
+        }
+    };
+    auto step = [&](const Ops& o) {
+        f32x4 Xn[RT][NT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) {
+                if (!live(ct)) { Xn[rt][ct] = X[rt][ct]; continue; }
+                f32x4 acc = ct < RT ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : o.Cv[rt][ct - RT];
+#pragma unroll
+                for (int kt = 0; kt < RT; ++kt)
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(o.A[rt][kt][kk], X[kt][ct][kk], acc, 0, 0, 0);
+                Xn[rt][ct] = acc;
+            }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct) X[rt][ct] = Xn[rt][ct];
+    };
+    // Per-step output of the state X (LOCAL, EXCL: fp32; OUTPUT: TO).
+    auto store_state = [&](int64_t t) {
+        if constexpr (MODE == CM_SUMMARY) return;
+        const int64_t row = static_cast<int64_t>(b) * p.L + t;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = trow(rt, i);
+                    if (r >= R || !live(ct)) continue;
+                    const float x = X[rt][ct][i];
+                    if (ct < RT) {
+                        if (pcol(ct) >= R || !p.outP) continue;
+                        const int64_t at = (row * R + r) * R + pcol(ct);
+                        if constexpr (MODE == CM_OUTPUT) static_cast<TO*>(p.outP)[at] = IO<TO>::st(x);
+                        else static_cast<float*>(p.outP)[at] = x;
+                    } else {
+                        if (hcol(ct) >= C) continue;
+                        const int64_t at = (row * R + r) * C + hcol(ct);
+                        if constexpr (MODE == CM_OUTPUT) static_cast<TO*>(p.outH)[at] = IO<TO>::st(x);
+                        else static_cast<float*>(p.outH)[at] = x;
+                    }
+                }
+    };
+
+    // ---- the recurrence, operands D steps ahead ---------------------------
+    Ops buf[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) load_ops(t0 + i < t1 ? t0 + i : t1 - 1, buf[i]);
+    for (int64_t t = t0; t < t1; t += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const int64_t ti = t + i;
+            if (ti >= t1) break;
+            mask_ops(buf[i]);
+            if constexpr (MODE == CM_EXCL) store_state(ti);
+            step(buf[i]);
+            if constexpr (MODE == CM_LOCAL || MODE == CM_OUTPUT) store_state(ti);
+            // refill this slot (always issued; clamped to the chunk's last step)
+            load_ops(ti + D < t1 ? ti + D : t1 - 1, buf[i]);
+        }
     }
 
-    // 3. exclusive carry of every chunk of the group: state before chunk k.
-    for (int k = k0; k < k1; ++k) {
-        const int64_t seq = static_cast<int64_t>(b) * p.nb + k;
-        for (int e = tid; e < E; e += K2_THREADS) {
-            const int i = e / W, j = e - i * W;
-            if (j < R) {
-                if (cb == 0) p.Pcar[seq * R * R + i * R + j] = acc[e];
-            } else {
-                p.Hcar[(seq * R + i) * p.C + c0 + (j - R)] = acc[e];
-            }
-        }
-        if (k + 1 < k1) {
-            load_summary(k, elt);
-            __syncthreads();
-            compose_lds<RMAX>(elt, acc, tmp, R, W);
-            __syncthreads();
-            swap(acc, tmp);
-        }
+    if constexpr (MODE == CM_SUMMARY || MODE == CM_LOCAL) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = trow(rt, i);
+                    if (r >= R || !live(ct)) continue;
+                    if (ct < RT) {
+                        if (pcol(ct) < R) p.sumP[seq * RR + r * R + pcol(ct)] = X[rt][ct][i];
+                    } else if (hcol(ct) < C) {
+                        p.sumH[(seq * R + r) * C + hcol(ct)] = X[rt][ct][i];
+                    }
+                }
     }
-
-    ws_finish(p.hdr, p.flags, static_cast<int64_t>(gridDim.y) * gridDim.z * p.n_grp, epoch);
 }
 
 // ---------------------------------------------------------------------------
@@ -336,100 +246,138 @@ __global__ __launch_bounds__(K2_THREADS) void dense_carry_kernel(DenseParams p) 
 // ---------------------------------------------------------------------------
 namespace {
 
-struct DenseGeo {
-    int T, nb, Cb, n_cblk, GS, n_grp, rmax;
-    size_t off_psum, off_hsum, off_pcar, off_hcar, off_flags, off_pay, bytes;
-    int64_t plane;
-};
+// Steps per chunk: 32 at level 0 (long serial runs over the big operands),
+// 8 above it (the summary levels are small, so parallelism matters more than
+// the number of levels).
+constexpr int kChunk0 = 32;
+constexpr int kChunkUp = 8;
+inline int chunk_len(int level) { return level == 0 ? kChunk0 : kChunkUp; }
 
-int rmax_for(int R) {
-    if (R <= 4) return 4;
-    if (R <= 8) return 8;
-    if (R <= 16) return 16;
-    if (R <= 32) return 32;
-    return 0;
+int col_tiles(int64_t C) { return C <= 16 ? 1 : C <= 32 ? 2 : C <= 48 ? 3 : 4; }
+int col_blocks(int64_t C, int ctw) {
+    return C == 0 ? 1 : static_cast<int>((C + 16 * ctw - 1) / (16 * ctw));
 }
 
-DenseGeo dense_geometry(int64_t B, int64_t L, int R, int64_t C, int T) {
+template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE>
+int launch_ct(const ChunkParams& c, int64_t B, hipStream_t st) {
+    hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, U4, TV, TO, MODE>),
+                       dim3(c.nb, col_blocks(c.C, CTW), static_cast<unsigned>(B)), dim3(64), 0, st, c);
+    return check_launch("dense_chunk_kernel");
+}
+
+template <int RT, bool U4, typename TV, typename TO, int MODE>
+int launch_c(const ChunkParams& c, int64_t B, hipStream_t st) {
+    switch (col_tiles(c.C)) {
+        case 1: return launch_ct<RT, 1, U4, TV, TO, MODE>(c, B, st);
+        case 2: return launch_ct<RT, 2, U4, TV, TO, MODE>(c, B, st);
+        case 3: return launch_ct<RT, 3, U4, TV, TO, MODE>(c, B, st);
+        default: return launch_ct<RT, 4, U4, TV, TO, MODE>(c, B, st);
+    }
+}
+
+// One pass over a level.  U4: R % 4 == 0 and 16-byte aligned rows of U (level
+// >= 1 products live in the 256-byte aligned workspace).
+template <typename TV, typename TO, int MODE>
+int launch_pass(const ChunkParams& c, int64_t B, hipStream_t st) {
+    const bool u4 = c.R % 4 == 0 && reinterpret_cast<uintptr_t>(c.U) % 16 == 0;
+    if (c.R <= 16) return u4 ? launch_c<1, true, TV, TO, MODE>(c, B, st) : launch_c<1, false, TV, TO, MODE>(c, B, st);
+    return u4 ? launch_c<2, true, TV, TO, MODE>(c, B, st) : launch_c<2, false, TV, TO, MODE>(c, B, st);
+}
+
+// Workspace: per level l >= 0 with n_l = ceil(n_{l-1} / T) chunks (n_{-1} = L),
+// the chunk products (sumP, sumH) and the chunk carries (carP, carH), fp32.
+struct Level {
+    int64_t n;                        // chunks of this level (= steps of the next)
+    size_t sumP, sumH, carP, carH;    // byte offsets
+};
+struct DenseGeo {
+    int depth;
+    Level lv[24];
+    size_t bytes;
+};
+
+DenseGeo dense_geometry(int64_t B, int64_t L, int64_t R, int64_t C) {
     DenseGeo g{};
-    g.T = T;
-    g.nb = static_cast<int>((L + T - 1) / T);
-    g.rmax = rmax_for(R);
-    const int room = 64 - R;                       // H columns per wave
-    g.Cb = C == 0 ? 0 : static_cast<int>(C < room ? C : room);
-    g.n_cblk = C == 0 ? 1 : static_cast<int>((C + g.Cb - 1) / g.Cb);
-    g.GS = g.nb <= 64 ? 1 : (g.nb + 63) / 64;
-    g.n_grp = (g.nb + g.GS - 1) / g.GS;
     size_t off = WS_HDR_BYTES;
-    auto take = [&](size_t n) { size_t o = off; off = round_up(off + n, 256); return o; };
-    const size_t nb = static_cast<size_t>(B) * g.nb;
-    g.off_psum = take(nb * R * R * sizeof(float));
-    g.off_hsum = take(nb * R * static_cast<size_t>(C) * sizeof(float));
-    g.off_pcar = take(nb * R * R * sizeof(float));
-    g.off_hcar = take(nb * R * static_cast<size_t>(C) * sizeof(float));
-    const size_t chains = static_cast<size_t>(B) * g.n_cblk;
-    g.off_flags = take(chains * g.n_grp * sizeof(uint32_t));
-    g.plane = static_cast<int64_t>(chains) * g.n_grp * R * (R + g.Cb);
-    g.off_pay = take(2 * static_cast<size_t>(g.plane) * sizeof(uint64_t));
+    auto take = [&](size_t nbytes) { size_t o = off; off = round_up(off + nbytes, 256); return o; };
+    int64_t steps = L;
+    while (steps > 1 && g.depth < 24) {
+        const int T = chunk_len(g.depth);
+        Level& v = g.lv[g.depth++];
+        v.n = (steps + T - 1) / T;
+        const size_t m = static_cast<size_t>(B) * v.n;
+        v.sumP = take(m * R * R * sizeof(float));
+        v.sumH = take(m * R * static_cast<size_t>(C) * sizeof(float));
+        v.carP = take(m * R * R * sizeof(float));
+        v.carH = take(m * R * static_cast<size_t>(C) * sizeof(float));
+        steps = v.n;
+    }
     g.bytes = off;
     return g;
 }
 
-// Chunk length: short chunks give parallelism along L; the serial work per
-// step is R*(R+64) FMAs per lane.
-int default_chunk(int64_t B, int64_t L, int R) {
-    (void)B;
-    (void)R;
-    return L >= 4096 ? 32 : 16;
-}
-
-template <int RMAX, typename TV, typename TO, int MODE, bool PREFIX>
-int launch_chunk(const DenseParams& prm, int64_t B, hipStream_t st) {
-    if (prm.R == RMAX) {
-        hipLaunchKernelGGL((dense_chunk_kernel<RMAX, true, TV, TO, MODE, PREFIX>),
-                           dim3(prm.nb, prm.n_cblk, static_cast<unsigned>(B)), dim3(64), 0, st, prm,
-                           prm.U, static_cast<const TV*>(prm.V), static_cast<TO*>(prm.H));
-        return check_launch("dense_chunk_kernel");
+// Exclusive scan of a level's (U, V) sequence of `len` steps into (outP, outH):
+// the state before every step, starting from [I | 0].  Recursive over chunk
+// products; lv indexes the workspace level holding this sequence's chunks.
+template <typename TV>
+int excl_scan(const float* U, const void* V, int64_t len, float* outP, float* outH, int64_t B,
+              int64_t R, int64_t C, bool withP, char* ws, const DenseGeo& geo, int lv,
+              hipStream_t st) {
+    ChunkParams c{};
+    c.U = U; c.V = C > 0 ? V : nullptr;
+    c.L = len; c.R = static_cast<int>(R); c.C = static_cast<int>(C); c.T = chunk_len(lv);
+    c.nb = static_cast<int>((len + c.T - 1) / c.T);
+    c.withP = withP;
+    c.outP = withP ? outP : nullptr;
+    c.outH = outH;
+    if (c.nb > 1) {
+        const Level& v = geo.lv[lv];
+        ChunkParams s = c;
+        s.sumP = reinterpret_cast<float*>(ws + v.sumP);
+        s.sumH = reinterpret_cast<float*>(ws + v.sumH);
+        int rc = launch_pass<TV, float, CM_SUMMARY>(s, B, st);
+        if (rc) return rc;
+        // carries of this level's chunks: exclusive scan of the chunk products
+        rc = excl_scan<float>(s.sumP, s.sumH, c.nb, reinterpret_cast<float*>(ws + v.carP),
+                              reinterpret_cast<float*>(ws + v.carH), B, R, C, withP, ws, geo, lv + 1, st);
+        if (rc) return rc;
+        c.carP = withP ? reinterpret_cast<float*>(ws + v.carP) : nullptr;
+        c.carH = reinterpret_cast<float*>(ws + v.carH);
     }
-    hipLaunchKernelGGL((dense_chunk_kernel<RMAX, false, TV, TO, MODE, PREFIX>),
-                       dim3(prm.nb, prm.n_cblk, static_cast<unsigned>(B)), dim3(64), 0, st, prm,
-                       prm.U, static_cast<const TV*>(prm.V), static_cast<TO*>(prm.H));
-    return check_launch("dense_chunk_kernel");
-}
-
-template <int RMAX>
-int launch_carry(const DenseParams& prm, int64_t B, hipStream_t st) {
-    hipLaunchKernelGGL((dense_carry_kernel<RMAX>), dim3(prm.n_grp, prm.n_cblk, static_cast<unsigned>(B)),
-                       dim3(K2_THREADS), 0, st, prm);
-    return check_launch("dense_carry_kernel");
-}
-
-template <int RMAX, typename TV, typename TO>
-int run_dense_t(DenseParams prm, int64_t B, bool prefix, hipStream_t st) {
-    int rc = launch_chunk<RMAX, TV, TO, CM_SUMMARY, false>(prm, B, st);
-    if (rc) return rc;
-    rc = launch_carry<RMAX>(prm, B, st);
-    if (rc) return rc;
-    if (prefix) return launch_chunk<RMAX, TV, TO, CM_OUTPUT, true>(prm, B, st);
-    return launch_chunk<RMAX, TV, TO, CM_OUTPUT, false>(prm, B, st);
+    return launch_pass<TV, float, CM_EXCL>(c, B, st);
 }
 
 template <typename TV, typename TO>
-int run_dense_r(const DenseParams& prm, int64_t B, bool prefix, int rmax, hipStream_t st) {
-    switch (rmax) {
-        case 4: return run_dense_t<4, TV, TO>(prm, B, prefix, st);
-        case 8: return run_dense_t<8, TV, TO>(prm, B, prefix, st);
-        case 16: return run_dense_t<16, TV, TO>(prm, B, prefix, st);
-        case 32: return run_dense_t<32, TV, TO>(prm, B, prefix, st);
-        default: return set_error(MOGT_E_INVALID, "R must be <= 32");
+int run_levels(const float* U, const void* V, void* H, void* P, int64_t B, int64_t L, int64_t R,
+               int64_t C, char* ws, const DenseGeo& geo, hipStream_t st) {
+    const bool withP = P != nullptr;
+    ChunkParams c{};
+    c.U = U; c.V = C > 0 ? V : nullptr;
+    c.L = L; c.R = static_cast<int>(R); c.C = static_cast<int>(C); c.T = chunk_len(0);
+    c.nb = static_cast<int>((L + c.T - 1) / c.T);
+    c.withP = withP;
+    c.outP = P; c.outH = H;
+    if (c.nb > 1) {
+        const Level& v = geo.lv[0];
+        ChunkParams s = c;
+        s.sumP = reinterpret_cast<float*>(ws + v.sumP);
+        s.sumH = reinterpret_cast<float*>(ws + v.sumH);
+        int rc = launch_pass<TV, TO, CM_SUMMARY>(s, B, st);
+        if (rc) return rc;
+        rc = excl_scan<float>(s.sumP, s.sumH, c.nb, reinterpret_cast<float*>(ws + v.carP),
+                              reinterpret_cast<float*>(ws + v.carH), B, R, C, withP, ws, geo, 1, st);
+        if (rc) return rc;
+        c.carP = withP ? reinterpret_cast<float*>(ws + v.carP) : nullptr;
+        c.carH = reinterpret_cast<float*>(ws + v.carH);
     }
+    return launch_pass<TV, TO, CM_OUTPUT>(c, B, st);
 }
 
 int check_dense_shapes(int64_t B, int64_t L, int64_t R, int64_t C) {
     if (B < 0 || L < 0 || R <= 0 || C < 0)
         return set_error(MOGT_E_INVALID, "U must be [B, L, R, R] and V must be [B, L, R, C]");
     if (R > 32) return set_error(MOGT_E_INVALID, "R = %lld not supported (R <= 32)", (long long)R);
-    if (C > (1 << 24)) return set_error(MOGT_E_INVALID, "C too large");
+    if (C > (1 << 22)) return set_error(MOGT_E_INVALID, "C too large");
     return MOGT_OK;
 }
 
@@ -442,36 +390,17 @@ int run_dense(const float* U, const void* V, void* H, void* P, int64_t B, int64_
     if (out_dtype != MOGT_F32 && out_dtype != MOGT_BF16) return set_error(MOGT_E_INVALID, "unsupported output dtype");
     if (B == 0 || L == 0) return MOGT_OK;
     if (!U || (C > 0 && (!V || !H)) || (C == 0 && !P)) return set_error(MOGT_E_INVALID, "null tensor pointer");
-    const int T = default_chunk(B, L, static_cast<int>(R));
-    const DenseGeo g = dense_geometry(B, L, static_cast<int>(R), C, T);
+    if (B > 65535 || (L + kChunk0 - 1) / kChunk0 > 0x7fffffffLL)
+        return set_error(MOGT_E_INVALID, "problem too large for one launch");
+    const DenseGeo g = dense_geometry(B, L, R, C);
     if (!ws || ws_bytes < g.bytes)
         return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", g.bytes, ws_bytes);
-    if (static_cast<int64_t>(g.nb) > 0x7fffffffLL || B > 65535)
-        return set_error(MOGT_E_INVALID, "problem too large for one launch");
     char* base = static_cast<char*>(ws);
-    DenseParams prm{};
-    prm.U = U; prm.V = C > 0 ? V : nullptr; prm.H = H; prm.P = P;
-    prm.Psum = reinterpret_cast<float*>(base + g.off_psum);
-    prm.Hsum = reinterpret_cast<float*>(base + g.off_hsum);
-    prm.Pcar = reinterpret_cast<float*>(base + g.off_pcar);
-    prm.Hcar = reinterpret_cast<float*>(base + g.off_hcar);
-    prm.L = L; prm.R = static_cast<int>(R); prm.C = static_cast<int>(C); prm.T = T; prm.nb = g.nb;
-    prm.Cb = g.Cb; prm.n_cblk = g.n_cblk; prm.GS = g.GS; prm.n_grp = g.n_grp;
-    prm.hdr = reinterpret_cast<uint32_t*>(base);
-    prm.flags = reinterpret_cast<uint32_t*>(base + g.off_flags);
-    prm.pay = reinterpret_cast<uint64_t*>(base + g.off_pay);
-    prm.plane = g.plane;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool prefix = P != nullptr;
-    if (v_dtype == MOGT_F32 && out_dtype == MOGT_F32) return run_dense_r<float, float>(prm, B, prefix, g.rmax, st);
-    if (v_dtype == MOGT_F32 && out_dtype == MOGT_BF16) return run_dense_r<float, bf16_t>(prm, B, prefix, g.rmax, st);
-    if (v_dtype == MOGT_BF16 && out_dtype == MOGT_F32) return run_dense_r<bf16_t, float>(prm, B, prefix, g.rmax, st);
-    return run_dense_r<bf16_t, bf16_t>(prm, B, prefix, g.rmax, st);
-}
-
-template <int RMAX, typename TV>
-int launch_local(const DenseParams& prm, int64_t B, hipStream_t st) {
-    return launch_chunk<RMAX, TV, float, CM_LOCAL, false>(prm, B, st);
+    if (v_dtype == MOGT_F32 && out_dtype == MOGT_F32) return run_levels<float, float>(U, V, H, P, B, L, R, C, base, g, st);
+    if (v_dtype == MOGT_F32 && out_dtype == MOGT_BF16) return run_levels<float, bf16_t>(U, V, H, P, B, L, R, C, base, g, st);
+    if (v_dtype == MOGT_BF16 && out_dtype == MOGT_F32) return run_levels<bf16_t, float>(U, V, H, P, B, L, R, C, base, g, st);
+    return run_levels<bf16_t, bf16_t>(U, V, H, P, B, L, R, C, base, g, st);
 }
 
 }  // namespace
@@ -482,8 +411,7 @@ using namespace mogt;
 extern "C" size_t mogt_affine_scan_workspace_bytes(int64_t batch, int64_t length, int64_t rank,
                                                    int64_t channels) {
     if (batch <= 0 || length <= 0 || rank <= 0 || rank > 32 || channels < 0) return WS_HDR_BYTES;
-    const int T = default_chunk(batch, length, static_cast<int>(rank));
-    return dense_geometry(batch, length, static_cast<int>(rank), channels, T).bytes;
+    return dense_geometry(batch, length, rank, channels).bytes;
 }
 
 extern "C" int mogt_affine_scan_fwd(const void* U, const void* V, void* H, void* U_prefix, int64_t batch,
@@ -520,24 +448,16 @@ extern "C" int mogt_affine_local_scan(const void* U, const void* V, void* U_pref
     const int64_t nb = (length + block_size - 1) / block_size;
     if (nb > 0x7fffffffLL || block_size > 0x7fffffffLL || batch > 65535)
         return set_error(MOGT_E_INVALID, "problem too large for one launch");
-    const DenseGeo g = dense_geometry(batch, length, static_cast<int>(rank), channels,
-                                      static_cast<int>(block_size));
-    DenseParams prm{};
-    prm.U = static_cast<const float*>(U);
-    prm.V = channels > 0 ? V : nullptr;
-    prm.H = H_prefix; prm.P = U_prefix;
-    prm.Psum = static_cast<float*>(U_summary);
-    prm.Hsum = static_cast<float*>(H_summary);
-    prm.L = length; prm.R = static_cast<int>(rank); prm.C = static_cast<int>(channels);
-    prm.T = static_cast<int>(block_size); prm.nb = static_cast<int>(nb);
-    prm.Cb = g.Cb; prm.n_cblk = g.n_cblk;
+    ChunkParams c{};
+    c.U = static_cast<const float*>(U);
+    c.V = channels > 0 ? V : nullptr;
+    c.outP = U_prefix; c.outH = H_prefix;
+    c.sumP = static_cast<float*>(U_summary);
+    c.sumH = static_cast<float*>(H_summary);
+    c.L = length; c.R = static_cast<int>(rank); c.C = static_cast<int>(channels);
+    c.T = static_cast<int>(block_size); c.nb = static_cast<int>(nb);
+    c.withP = 1;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const bool bf = v_dtype == MOGT_BF16;
-    switch (g.rmax) {
-        case 4: return bf ? launch_local<4, bf16_t>(prm, batch, st) : launch_local<4, float>(prm, batch, st);
-        case 8: return bf ? launch_local<8, bf16_t>(prm, batch, st) : launch_local<8, float>(prm, batch, st);
-        case 16: return bf ? launch_local<16, bf16_t>(prm, batch, st) : launch_local<16, float>(prm, batch, st);
-        case 32: return bf ? launch_local<32, bf16_t>(prm, batch, st) : launch_local<32, float>(prm, batch, st);
-        default: return set_error(MOGT_E_INVALID, "R must be <= 32");
-    }
+    return v_dtype == MOGT_BF16 ? launch_pass<bf16_t, float, CM_LOCAL>(c, batch, st)
+                                : launch_pass<float, float, CM_LOCAL>(c, batch, st);
 }
