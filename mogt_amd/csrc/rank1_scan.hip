@@ -27,6 +27,7 @@ namespace mogt {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int R1_DH = 64;         // head dimension
 constexpr int R1_T = 64;          // sub-chunk length
@@ -84,11 +85,12 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
     return x;
 }
 
-// One 64-step x 64-wide tile of q, k or v held in registers: thread e covers
-// row (e + 256 u) / 8, segment (e + 256 u) % 8 of 8 consecutive elements, so
-// 8 consecutive lanes read one 128-byte row (u = 0, 1).  Rows past L are read
-// from row L - 1 (every load is unconditional, so no wait is forced between
-// them) and zeroed when the tile is staged into LDS.
+// One 64-step x 64-wide tile of q, k or v held in registers.  Thread e covers
+// the row pair (2m, 2m + 1), m = e / 8, and segment sg = e % 8 of 8 consecutive
+// elements in both rows, so 8 consecutive lanes read one 128-byte row and a
+// transposed store writes both rows' elements of one column as one 4-byte
+// word.  Rows past L are read from row L - 1 (every load is unconditional, so
+// no wait is forced between them) and zeroed when the tile is staged into LDS.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename TI>
@@ -98,65 +100,80 @@ struct Tile8 {
     bool ok[2];
 };
 
+__device__ __forceinline__ int tile_m() { return static_cast<int>(threadIdx.x) >> 3; }
+__device__ __forceinline__ int tile_sg() { return static_cast<int>(threadIdx.x) & 7; }
+
 template <typename TI>
 __device__ __forceinline__ Tile8<TI> load_tile(const TI* __restrict__ src, int64_t rowbase, int64_t t0,
                                                int64_t L, int H) {
     Tile8<TI> r;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int e = threadIdx.x + R1_THREADS * u;
-        const int t = e >> 3, sg = e & 7;
+        const int t = 2 * tile_m() + u;
         r.ok[u] = t0 + t < L;
         const int64_t row = r.ok[u] ? t0 + t : L - 1;
-        const u32x4* ptr = reinterpret_cast<const u32x4*>(src + (rowbase + row * H) * R1_DH + sg * 8);
+        const u32x4* ptr = reinterpret_cast<const u32x4*>(src + (rowbase + row * H) * R1_DH + tile_sg() * 8);
 #pragma unroll
         for (int j = 0; j < Tile8<TI>::NW; ++j) r.x[u][j] = ptr[j];
     }
     return r;
 }
 
-// The 8 elements of segment u as bf16 (zero past L).
+// The 8 elements of row 2m + u as fp32 (zero past L).
 template <typename TI>
-__device__ __forceinline__ bf16x8 seg_bf16(const Tile8<TI>& r, int u) {
-    bf16x8 o;
+__device__ __forceinline__ void seg_f32(const Tile8<TI>& r, int u, float (&o)[8]) {
     if constexpr (sizeof(TI) == 2) {
-        o = __builtin_bit_cast(bf16x8, r.x[u][0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i] = __uint_as_float(r.x[u][0][i] << 16);
+            o[2 * i + 1] = __uint_as_float(r.x[u][0][i] & 0xffff0000u);
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[4 * j + i] = static_cast<__bf16>(__uint_as_float(r.x[u][j][i]));
+            for (int i = 0; i < 4; ++i) o[4 * j + i] = __uint_as_float(r.x[u][j][i]);
     }
     if (!r.ok[u]) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = static_cast<__bf16>(0.0f);
+        for (int i = 0; i < 8; ++i) o[i] = 0.0f;
     }
-    return o;
 }
 
-// Tile into LDS: row-major [t][d] (row stride R1_SR) and/or transposed [d][t].
+// Two fp32 values as one word of two bf16 (round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Tile into LDS row-major [t][d] (row stride R1_SR).
 template <typename TI>
 __device__ __forceinline__ void put_rows(const Tile8<TI>& r, bf16_t* dst) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int e = threadIdx.x + R1_THREADS * u;
-        const int t = e >> 3, sg = e & 7;
-        *reinterpret_cast<bf16x8*>(dst + t * R1_SR + sg * 8) = seg_bf16(r, u);
+        const int t = 2 * tile_m() + u;
+        u32x4 w;
+        if constexpr (sizeof(TI) == 2) {
+            w = r.x[u][0];
+            if (!r.ok[u]) w = u32x4{0u, 0u, 0u, 0u};
+        } else {
+            float o[8];
+            seg_f32(r, u, o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = pack_bf16(o[2 * i], o[2 * i + 1]);
+        }
+        *reinterpret_cast<u32x4*>(dst + t * R1_SR + tile_sg() * 8) = w;
     }
 }
+// Tile into LDS transposed [d][t], rows 2m and 2m + 1 scaled by s0 and s1.
 template <typename TI>
-__device__ __forceinline__ void put_cols(const Tile8<TI>& r, bf16_t* dst) {
+__device__ __forceinline__ void put_cols(const Tile8<TI>& r, bf16_t* dst, float s0 = 1.0f, float s1 = 1.0f) {
+    float a[8], b[8];
+    seg_f32(r, 0, a);
+    seg_f32(r, 1, b);
+    const int m = tile_m(), sg = tile_sg();
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int e = threadIdx.x + R1_THREADS * u;
-        const int t = e >> 3, sg = e & 7;
-        const bf16x8 o = seg_bf16(r, u);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const __bf16 b = o[i];
-            dst[(sg * 8 + i) * R1_SR + t] = *reinterpret_cast<const bf16_t*>(&b);
-        }
-    }
+    for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<uint32_t*>(dst + (sg * 8 + i) * R1_SR + 2 * m) = pack_bf16(a[i] * s0, b[i] * s1);
 }
 
 // Raw f of step t (row L - 1 past the end; see fval).
@@ -170,6 +187,10 @@ template <typename TF>
 __device__ __forceinline__ float fval(TF raw, int64_t t, int64_t L) {
     return t < L ? IO<TF>::ld(raw) : 1.0f;
 }
+
+// 2^x on the hardware exponential (v_exp_f32); every argument here is <= 0,
+// and results below 2^-126 only weight terms already below bf16 resolution.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------
 // K_A: dS = V^T diag(w) K over one 256-step super-chunk.
@@ -200,28 +221,15 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p
     __syncthreads();
     for (int i = 0; i < w; ++i) lc += sWave[i];
     const float lcT = sWave[0] + sWave[1] + sWave[2] + sWave[3];
-    sW[tid] = exp2f(lcT - lc) * (1.0f - fv);
+    sW[tid] = exp2_hw(lcT - lc) * (1.0f - fv);
 
     const int ib = w >> 1, jb = w & 1;   // this wave's 32x32 tile of dS[i][j]
+    const int m = tile_m();
     f32x16 acc = zero16();
     for (int sub = 0; sub < R1_SUB; ++sub) {
         __syncthreads();   // previous sub-block's tiles consumed; sW visible
         put_cols(kt, sKT);
-        {
-            // V^T scaled by w_s (rounded to bf16 for the MFMA)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int e = tid + R1_THREADS * u;
-                const int t = e >> 3, sg = e & 7;
-                const float ws = sW[sub * R1_T + t];
-                const bf16x8 vs = seg_bf16(vt, u);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const __bf16 bv = static_cast<__bf16>(static_cast<float>(vs[i]) * ws);
-                    sVT[(sg * 8 + i) * R1_SR + t] = *reinterpret_cast<const bf16_t*>(&bv);
-                }
-            }
-        }
+        put_cols(vt, sVT, sW[sub * R1_T + 2 * m], sW[sub * R1_T + 2 * m + 1]);   // V^T diag(w)
         if (sub + 1 < R1_SUB) {   // prefetch the next sub-block while this one multiplies
             kt = load_tile<TI>(kp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
             vt = load_tile<TI>(vp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
@@ -267,28 +275,45 @@ __global__ __launch_bounds__(256) void rank1_carry_kernel(Rank1Params p) {
 
 // ---------------------------------------------------------------------------
 // K_C: outputs of one super-chunk, four sub-chunks in order.
+//
+// Wave w = (a, c) = (w / 2, w % 2) owns the 32 x 32 quadrant (rows 32a, columns
+// 32c) of every 64 x 64 product: of P[t][s] (a >= c only), of y[t][i], and of
+// the transposed state S^T[j][i], kept in MFMA accumulators.  Holding S^T
+// puts four consecutive j of one row S[i][.] in each lane's register group,
+// so the bf16 hi / lo halves of S go to LDS as 8-byte words.  Per sub-chunk:
+//   every wave scans the 64 log-decays itself (lane = step) and stages its
+//   share of q, k (rows), k^T diag(w) and v^T into LDS      | barrier
+//   P = (Q K^T) o 2^(Lc_t - Lc_s) (1 - f_s), s <= t          | barrier
+//   y = P V + 2^Lc_t Q S^T (S as bf16 hi + lo)               | barrier
+//   S^T <- 2^Lc_T S^T + K^T diag(w) V; S halves to LDS       | barrier
+// The next sub-chunk's q, k, v, f are loaded while the current one computes.
+// y is written through a buffer descriptor whose range ends at the sequence's
+// last row, so rows past L are dropped by the hardware.
 // ---------------------------------------------------------------------------
 template <typename TF, typename TI, typename TO>
 __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p) {
     __shared__ __attribute__((aligned(16))) bf16_t sQ[R1_T * R1_SR];
     __shared__ __attribute__((aligned(16))) bf16_t sK[R1_T * R1_SR];
     __shared__ __attribute__((aligned(16))) bf16_t sVT[R1_DH * R1_SR];
-    __shared__ __attribute__((aligned(16))) bf16_t sKT[R1_DH * R1_SR];
+    __shared__ __attribute__((aligned(16))) bf16_t sKTw[R1_DH * R1_SR];
     __shared__ __attribute__((aligned(16))) bf16_t sP[R1_T * R1_SR];
     __shared__ __attribute__((aligned(16))) bf16_t sShi[R1_DH * R1_SR];
     __shared__ __attribute__((aligned(16))) bf16_t sSlo[R1_DH * R1_SR];
-    __shared__ float sLc[R1_T], sOmf[R1_T];
+    __shared__ __attribute__((aligned(16))) float sLc[R1_T];
+    __shared__ __attribute__((aligned(16))) float sE[R1_T];
+    __shared__ float sOmf[R1_T];
     const int sc = blockIdx.x;
     const int seq = blockIdx.y;
     const int b = seq / p.H, h = seq - (seq / p.H) * p.H;
     const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + h;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int tb = w >> 1, xb = w & 1;   // this wave's 32-row block and 32-column block
+    const int qa = w >> 1, qc = w & 1;   // this wave's quadrant: rows 32 qa, columns 32 qc
+    const int m = tile_m();
     const TI* qp = static_cast<const TI*>(p.q);
     const TI* kp = static_cast<const TI*>(p.k);
     const TI* vp = static_cast<const TI*>(p.v);
     const TF* fp = static_cast<const TF*>(p.f);
-    TO* yp = static_cast<TO*>(p.y);
+    const int64_t rowStrideB = static_cast<int64_t>(p.H) * R1_DH * sizeof(TO);   // bytes between steps of y
 
     const int64_t tsc = static_cast<int64_t>(sc) * R1_RS;
     TF fraw = load_f<TF>(fp, rowbase, tsc + lane, p.L, p.H);
@@ -296,22 +321,35 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
     Tile8<TI> kt = load_tile<TI>(kp, rowbase, tsc, p.L, p.H);
     Tile8<TI> vt = load_tile<TI>(vp, rowbase, tsc, p.L, p.H);
 
-    // state tile (rows tb, columns xb) of S_in in the accumulator layout
-    f32x16 S;
+    // S^T quadrant (rows j = 32 qa + mrow(r), columns i = 32 qc + lane % 32) of S_in
+    f32x16 ST;
     {
         const float* src = p.Sin + (static_cast<int64_t>(seq) * p.nsc + sc) * R1_DH * R1_DH;
-        const int col = xb * 32 + (lane & 31);
+        const int i = qc * 32 + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) S[r] = src[(tb * 32 + mrow(r)) * R1_DH + col];
+        for (int g4 = 0; g4 < 4; ++g4) {   // j = 32 qa + 8 g4 + 4 (lane / 32) + 0..3: one 16-byte load
+            const int j = qa * 32 + 8 * g4 + 4 * (lane >> 5);
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(src + i * R1_DH + j);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ST[4 * g4 + q] = v4[q];
+        }
     }
+    // S (= transposed accumulators) as bf16 hi + lo halves into LDS rows [i][j]
     auto put_state = [&]() {
-        const int col = xb * 32 + (lane & 31);
+        const int i = qc * 32 + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float x = S[r];
-            const bf16_t hi = f32_to_bf16(x);
-            sShi[(tb * 32 + mrow(r)) * R1_SR + col] = hi;
-            sSlo[(tb * 32 + mrow(r)) * R1_SR + col] = f32_to_bf16(x - bf16_to_f32(hi));
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int j = qa * 32 + 8 * g4 + 4 * (lane >> 5);
+            uint32_t hw[2], lw[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float x0 = ST[4 * g4 + 2 * q], x1 = ST[4 * g4 + 2 * q + 1];
+                hw[q] = pack_bf16(x0, x1);
+                const float h0 = __uint_as_float(hw[q] << 16), h1 = __uint_as_float(hw[q] & 0xffff0000u);
+                lw[q] = pack_bf16(x0 - h0, x1 - h1);
+            }
+            *reinterpret_cast<uint2*>(sShi + i * R1_SR + j) = uint2{hw[0], hw[1]};
+            *reinterpret_cast<uint2*>(sSlo + i * R1_SR + j) = uint2{lw[0], lw[1]};
         }
     };
     put_state();
@@ -321,72 +359,88 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
                          : R1_SUB;
     for (int sub = 0; sub < nsub; ++sub) {
         const int64_t t0 = tsc + static_cast<int64_t>(sub) * R1_T;
-        // stage this sub-chunk; then start loading the next one
-        put_rows(qt, sQ);
-        put_rows(kt, sK);
-        put_cols(kt, sKT);
-        put_cols(vt, sVT);
+        // log-decays of this sub-chunk, lane = step (every wave; wave 0 publishes)
+        const float fv = fval<TF>(fraw, t0 + lane, p.L);
+        const float lc = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
+        const float lcT = __shfl(lc, 63, 64);
+        const float wgt = exp2_hw(lcT - lc) * (1.0f - fv);
         if (w == 0) {
-            const float fv = fval<TF>(fraw, t0 + lane, p.L);
-            sLc[lane] = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
+            sLc[lane] = lc;
+            sE[lane] = exp2_hw(lc);
             sOmf[lane] = 1.0f - fv;
         }
+        // stage this sub-chunk
+        put_rows(qt, sQ);
+        put_rows(kt, sK);
+        put_cols(kt, sKTw, __shfl(wgt, 2 * m, 64), __shfl(wgt, 2 * m + 1, 64));
+        put_cols(vt, sVT);
         __syncthreads();
-        if (sub + 1 < nsub) {
+        if (sub + 1 < nsub) {   // next sub-chunk's operands, in flight while this one computes
             qt = load_tile<TI>(qp, rowbase, t0 + R1_T, p.L, p.H);
             kt = load_tile<TI>(kp, rowbase, t0 + R1_T, p.L, p.H);
             vt = load_tile<TI>(vp, rowbase, t0 + R1_T, p.L, p.H);
             fraw = load_f<TF>(fp, rowbase, t0 + R1_T + lane, p.L, p.H);
         }
-        // P = (Q K^T) o exp(Lc_t - Lc_s) (1 - f_s) on s <= t (tile (tb, xb); xb > tb unused)
-        if (xb <= tb) {
-            const int t_of = tb * 32, s_of = xb * 32;
-            f32x16 acc = mma32(sQ + t_of * R1_SR, R1_SR, sK + s_of * R1_SR, R1_SR, R1_DH, zero16());
-            const int s = s_of + (lane & 31);
+        const int t_of = qa * 32, c_of = qc * 32;
+        // Lc_t and 2^Lc_t of this lane's 16 rows t = t_of + mrow(r): 16-byte reads
+        float lct[16], et[16];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int t = t_of + 8 * g4 + 4 * (lane >> 5);
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(sLc + t);
+            const f32x4 e4 = *reinterpret_cast<const f32x4*>(sE + t);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                lct[4 * g4 + q] = l4[q];
+                et[4 * g4 + q] = e4[q];
+            }
+        }
+        // P quadrant (rows t_of, columns s_of = c_of), lower triangle only
+        if (qc <= qa) {
+            f32x16 acc = mma32(sQ + t_of * R1_SR, R1_SR, sK + c_of * R1_SR, R1_SR, R1_DH, zero16());
+            const int s = c_of + (lane & 31);
             const float lcs = sLc[s], omf = sOmf[s];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = t_of + mrow(r);
-                const float pv = (s <= t) ? acc[r] * exp2f(sLc[t] - lcs) * omf : 0.0f;
+                const float pv = (qc < qa || s <= t) ? acc[r] * exp2_hw(lct[r] - lcs) * omf : 0.0f;
                 sP[t * R1_SR + s] = f32_to_bf16(pv);
             }
         }
         __syncthreads();
-        // y tile (rows tb, columns xb): intra-chunk P V + decayed inter-chunk Q S^T
+        // y quadrant (rows t_of, columns i = c_of): intra P V + decayed inter Q S^T
         {
-            const int t_of = tb * 32, i_of = xb * 32;
             f32x16 intra = zero16();
-            for (int sb = 0; sb <= tb; ++sb)
-                intra = mma32(sP + t_of * R1_SR + sb * 32, R1_SR, sVT + i_of * R1_SR + sb * 32, R1_SR,
-                              32, intra);
-            f32x16 inter = mma32(sQ + t_of * R1_SR, R1_SR, sShi + i_of * R1_SR, R1_SR, R1_DH, zero16());
-            inter = mma32(sQ + t_of * R1_SR, R1_SR, sSlo + i_of * R1_SR, R1_SR, R1_DH, inter);
-            const int col = i_of + (lane & 31);
+            for (int sb = 0; sb <= qa; ++sb)
+                intra = mma32(sP + t_of * R1_SR + sb * 32, R1_SR, sVT + c_of * R1_SR + sb * 32, R1_SR, 32,
+                              intra);
+            f32x16 inter = mma32(sQ + t_of * R1_SR, R1_SR, sShi + c_of * R1_SR, R1_SR, R1_DH, zero16());
+            inter = mma32(sQ + t_of * R1_SR, R1_SR, sSlo + c_of * R1_SR, R1_SR, R1_DH, inter);
+            // rows of this sub-chunk at or past L fall outside the range and are dropped
+            const int64_t left = p.L - t0;   // >= 1
+            const int64_t span = (left - 1) * rowStrideB + static_cast<int64_t>(R1_DH) * sizeof(TO);
+            const auto ry = __builtin_amdgcn_make_buffer_rsrc(
+                static_cast<TO*>(p.y) + (rowbase + t0 * p.H) * R1_DH, 0,
+                static_cast<int>(span < 0x7fffffff ? span : 0x7fffffff), 0x00020000);
+            const int colB = (c_of + (lane & 31)) * static_cast<int>(sizeof(TO));
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = t_of + mrow(r);
-                if (t0 + t < p.L) {
-                    const float val = intra[r] + exp2f(sLc[t]) * inter[r];
-                    yp[(rowbase + (t0 + t) * p.H) * R1_DH + col] = IO<TO>::st(val);
-                }
+                const float val = intra[r] + et[r] * inter[r];
+                const int off = t * static_cast<int>(rowStrideB) + colB;
+                if constexpr (sizeof(TO) == 4)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), ry, off, 0, 0);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(val), ry, off, 0, 0);
             }
         }
-        __syncthreads();   // sVT (unscaled) and the old state halves are consumed
-        // S <- exp(Lc_T) S + V^T diag(w) K  with w_s = exp(Lc_T - Lc_s) (1 - f_s)
+        __syncthreads();   // sQ, sP and the old state halves are consumed
+        // S^T <- 2^Lc_T S^T + K^T diag(w) V
         {
-            const float lcT = sLc[R1_T - 1];
+            const f32x16 dST = mma32(sKTw + t_of * R1_SR, R1_SR, sVT + c_of * R1_SR, R1_SR, R1_T, zero16());
+            const float dec = exp2_hw(lcT);
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int e = tid + R1_THREADS * u;   // over DH x T
-                const int i = e >> 6, s = e & 63;
-                bf16_t& x = sVT[i * R1_SR + s];
-                x = f32_to_bf16(bf16_to_f32(x) * (exp2f(lcT - sLc[s]) * sOmf[s]));
-            }
-            __syncthreads();
-            f32x16 dS = mma32(sVT + tb * 32 * R1_SR, R1_SR, sKT + xb * 32 * R1_SR, R1_SR, R1_T, zero16());
-            const float dec = exp2f(lcT);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) S[r] = fmaf(dec, S[r], dS[r]);
+            for (int r = 0; r < 16; ++r) ST[r] = fmaf(dec, ST[r], dST[r]);
             put_state();
         }
         __syncthreads();   // tiles of this sub-chunk consumed before the next staging

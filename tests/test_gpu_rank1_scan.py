@@ -59,3 +59,19 @@ def test_equals_dense_scan_with_scalar_transport(gpu):
                                         out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert rel_err(to_np(y[0, :, 0]), to_np(y_dense).astype(np.float64)) <= 5e-3
+
+
+@pytest.mark.parametrize("L,H", [(77, 1), (700, 2)])
+def test_fp32_inputs(gpu, L, H):
+    """fp32 f, k, v, q (rounded to bf16 inside the products): against the oracle
+    on the unrounded inputs, fp32 output."""
+    announce(f"rank1 fp32 inputs L={L} H={H}")
+    import mogt_amd
+
+    f, k, v, q = synthetic.rank1_inputs(1, L, H, 64, seed=11 + L)
+    ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).float() for x in (f, k, v, q))
+    ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
+    y = mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float32
+    assert rel_err(to_np(y), ref) <= 1e-2
