@@ -178,15 +178,36 @@ def _cayley_transport_gpu(torch, n_seq, L, d, seed):
         U[:, s0:s1] = torch.linalg.solve(eye - W, eye + W) * gate
     v = torch.randn(n_seq, L, d, 1, generator=gen, device=dev)
     k = torch.nn.functional.normalize(torch.randn(n_seq, L, 1, d, generator=gen, device=dev), dim=-1)
-    return U, (v * k).contiguous()
+    return U, (v * k).contiguous(), v[..., 0].contiguous(), k[..., 0, :].contiguous()
 
 
-def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets=2):
+def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets=2, vk=False):
     """Dense U [B,L,R,R] fp32, V [B,L,R,C] fp32 -> H fp32 via the C ABI
-    (three launches: chunk summaries, carries, output)."""
+    (chunk summaries, carries, output).  vk: B_t = v_t k_t^T from v [B,L,R] and
+    k [B,L,C] formed in registers (mogt_affine_scan_vk_fwd)."""
     dev = torch.device("cuda:0")
+    if vk:
+        U0, _, v0, k0 = _cayley_transport_gpu(torch, B, L, R, seed=11)
+        bufs = [(U0.clone(), v0.clone(), k0.clone(), torch.empty(B, L, R, C, device=dev)) for _ in range(sets)]
+        del U0, v0, k0
+        ws = ops.workspace(lib.mogt_affine_scan_workspace_bytes(B, L, R, C), dev)
+        stream = torch.cuda.current_stream(dev)
+        sh = stream.cuda_stream
+
+        def launch_vk(i):
+            u, vv, kk, h = bufs[i % sets]
+            rc = lib.mogt_affine_scan_vk_fwd(u.data_ptr(), vv.data_ptr(), kk.data_ptr(), h.data_ptr(), None,
+                                             B, L, R, C, 0, 0, ws.data_ptr(), ws.numel(), sh)
+            if rc:
+                raise RuntimeError(lib.mogt_last_error().decode())
+
+        ms = EventTimer(torch, stream).time(launch_vk, steps, warmup)
+        total = B * L * (R * R + R + C + R * C) * 4
+        flops = B * L * (2 * R * R * C + 2 * R * C)   # U_t H_{t-1} + v_t k_t^T
+        return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9,
+                "tflops": flops / (ms * 1e-3) / 1e12}
     if cayley:
-        U0, V0 = _cayley_transport_gpu(torch, B, L, R, seed=11)
+        U0, V0, _, _ = _cayley_transport_gpu(torch, B, L, R, seed=11)
     else:
         gen = torch.Generator(device="cuda").manual_seed(5)
         U0 = torch.eye(R, device=dev) + 0.05 * torch.randn(B, L, R, R, generator=gen, device=dev)
@@ -418,6 +439,13 @@ def main():
             "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
             "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
             "note": "BASELINE configs[3]: U=gate*Cayley(W) [8,L,32,32], V=v k^T [8,L,32,32] fp32"}
+        r = measure_dense(torch, lib, ops, 8, 16384, 32, 32, max(3, args.steps // 10), 1, sets=2, vk=True)
+        extras["dense_cayley_cfg4_vk_h8_d32_L16384"] = {
+            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
+            "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
+                    "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
         r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
         extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
             r, ffn_hidden=3072, vocab=32000,

@@ -108,6 +108,18 @@ int mogt_affine_scan_fwd(const void* U, const void* V, void* H, void* U_prefix,
                          int v_dtype, int out_dtype,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same scan with a rank-1 write V_t = v_t k_t^T, formed in registers
+ * (never materialised): the `dense_scan(A, v, k)` form of the matrix scan,
+ * i.e. configs[3]'s B_t = v_t k_t^T fed to
+ * triton_affine_scan_hybrid (triton_scan.py:429-477) without building the
+ * [B, L, R, C] tensor.  v: [B, L, R], k: [B, L, C], both vk_dtype (fp32 or
+ * bf16); each element of V_t is the fp32 product v_i * k_j, as a
+ * materialised fp32 V.  Workspace: mogt_affine_scan_workspace_bytes.        */
+int mogt_affine_scan_vk_fwd(const void* U, const void* v, const void* k, void* H, void* U_prefix,
+                            int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                            int vk_dtype, int out_dtype,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* Transport-only prefix product Y_t = U_t Y_{t-1}, Y_0 = I.
  * Replaces triton_fused_scan / _fused_scan_kernel (triton_scan.py:13-51,
  * :151-175), which hard-codes R = 16; here any R <= 32.  U fp32, Y out_dtype. */

@@ -52,6 +52,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
          _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_affine_scan_vk_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+         _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
     "mogt_fused_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "mogt_fused_scan_fwd": (
         _c_int,

@@ -37,7 +37,9 @@ constexpr int kDenseChunk = 32;
 
 struct ChunkParams {
     const float* U;      // [B, L, R, R] fp32 (level 0) or chunk products of the level below
-    const void* V;       // [B, L, R, C] (fp32 / bf16; level >= 1: fp32); null if C == 0
+    const void* V;       // [B, L, R, C] (fp32 / bf16; level >= 1: fp32); null if C == 0;
+                         // VK passes: the vectors v [B, L, R]
+    const void* K;       // VK passes: the vectors k [B, L, C] of V_t = v_t k_t^T
     const float* carP;   // [B, nb, R, R] chunk carries (EXCL / OUTPUT); null = identity
     const float* carH;   // [B, nb, R, C]                                ; null = zero
     void* outP;          // per-step P: LOCAL fp32 / EXCL fp32 / OUTPUT TO (may be null)
@@ -73,7 +75,7 @@ constexpr int64_t kDenseNarrowWaves = 256;
 // of rows.  Otherwise V is read and H written one element at a time.
 // All global accesses of the step loop go through buffer descriptors, whose
 // range check zero-fills padding (see the addressing comment in the body).
-template <int RT, int CTW, bool WITHP, bool U4, bool W16, typename TV, typename TO, int MODE>
+template <int RT, int CTW, bool WITHP, bool U4, bool W16, typename TV, typename TO, int MODE, bool VK>
 __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
     constexpr bool FIXED = MODE != CM_LOCAL;   // trip count kDenseChunk
     constexpr int NT = RT + CTW;               // column tiles: RT of P, then CTW of H
@@ -144,13 +146,15 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
     constexpr int ROWS = 16 * RT;
     constexpr int VE = 16 / static_cast<int>(sizeof(TV));     // V elements per 16-byte piece
     constexpr int OE = 16 / static_cast<int>(sizeof(TO));     // output elements per piece
-    constexpr int NV = W16 ? (ROWS * VW / VE + 63) / 64 : 1;
+    constexpr bool VBLOCK = W16 && !VK;                       // V_t block through LDS
+    constexpr int NV = VBLOCK ? (ROWS * VW / VE + 63) / 64 : 1;
     constexpr bool STORES = MODE != CM_SUMMARY;
     constexpr bool STAGE_OUT = W16 && STORES;
     constexpr int NO = STAGE_OUT ? (ROWS * VW / OE + 63) / 64 : 1;
     constexpr int ES = MODE == CM_OUTPUT ? static_cast<int>(sizeof(TO)) : 4;   // stored element bytes
     const uint32_t uBytes = static_cast<uint32_t>(RR * 4);
-    const uint32_t vBytes = static_cast<uint32_t>(R * C * static_cast<int>(sizeof(TV)));
+    const uint32_t vBytes = static_cast<uint32_t>((VK ? R : R * C) * static_cast<int>(sizeof(TV)));
+    const uint32_t kBytes = static_cast<uint32_t>(C * static_cast<int>(sizeof(TV)));
     const uint32_t hBytes = static_cast<uint32_t>(R * C * ES);
     const uint32_t pBytes = static_cast<uint32_t>(RR * ES);
 
@@ -165,25 +169,34 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                 const int r = 16 * rt + n, c = 16 * kt + 4 * g + kk;
                 offA[rt][kt][kk] = (r < R && c < R) ? (r * R + c) * 4 : kOOB;
             }
-    // V: 16-byte pieces of the ROWS x VW block (W16) or one element per tile register
-    int offV[W16 ? NV : RT][W16 ? 1 : CTW][W16 ? 1 : 4];
+    // V: 16-byte pieces of the ROWS x VW block (VBLOCK) or one element per tile
+    // register; VK: element i of v per tile row group and one element of k per
+    // column tile (offK)
+    int offV[VBLOCK ? NV : RT][VBLOCK || VK ? 1 : CTW][VBLOCK ? 1 : 4];
+    int offK[VK ? CTW : 1];
 #pragma unroll
-    for (int j = 0; j < (W16 ? NV : RT); ++j)
+    for (int j = 0; j < (VBLOCK ? NV : RT); ++j)
 #pragma unroll
-        for (int h = 0; h < (W16 ? 1 : CTW); ++h)
+        for (int h = 0; h < (VBLOCK || VK ? 1 : CTW); ++h)
 #pragma unroll
-            for (int i = 0; i < (W16 ? 1 : 4); ++i) {
+            for (int i = 0; i < (VBLOCK ? 1 : 4); ++i) {
                 int r, c;
-                if constexpr (W16) {
+                if constexpr (VBLOCK) {
                     const int e = (lane + 64 * j) * VE;
                     r = e < ROWS * VW ? e / VW : R;
                     c = c0 + e % VW;
                 } else {
                     r = trow(j, i);
-                    c = c0 + 16 * h + n;
+                    c = VK ? 0 : c0 + 16 * h + n;
                 }
-                offV[j][h][i] = (r < R && c < C) ? (r * C + c) * static_cast<int>(sizeof(TV)) : kOOB;
+                const int e = VK ? r : r * C + c;
+                offV[j][h][i] = (r < R && c < C) ? e * static_cast<int>(sizeof(TV)) : kOOB;
             }
+#pragma unroll
+    for (int h = 0; h < (VK ? CTW : 1); ++h) {
+        const int c = c0 + 16 * h + n;
+        offK[h] = (VK && c < C) ? c * static_cast<int>(sizeof(TV)) : kOOB;
+    }
     // H stores: 16-byte pieces (STAGE_OUT) or one element per tile register
     int offH[STAGE_OUT ? NO : RT][STAGE_OUT ? 1 : CTW][STAGE_OUT ? 1 : 4];
 #pragma unroll
@@ -215,7 +228,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                 offP[rt][ct][i] = (hasP && r < R && c < R) ? (r * R + c) * ES : kOOB;
             }
 
-    __shared__ __align__(16) float s_v[W16 ? ROWS : 1][W16 ? VS : 4];
+    __shared__ __align__(16) float s_v[VBLOCK ? ROWS : 1][VBLOCK ? VS : 4];
     __shared__ __align__(16) float s_o[STAGE_OUT ? ROWS : 1][STAGE_OUT ? VS : 4];
     // Orders this wave's LDS writes before its reads of other lanes' data and
     // vice versa (LDS executes one wave's accesses in issue order; a wave-scope
@@ -227,6 +240,8 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
         f32x4 A[RT][RT];
         f32x4 Cv[RT][CTW];
         u32x4 raw[NV];
+        f32x4 vv[VK ? RT : 1];   // VK: v rows of the tile row groups
+        float kk[VK ? CTW : 1];  // VK: k columns of the column tiles
     };
     const int64_t seqStep = static_cast<int64_t>(b) * p.L;
     auto load_ops = [&](int64_t t, bool valid, Ops& o) {
@@ -243,9 +258,21 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                         o.A[rt][kt][kk] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, offA[rt][kt][kk], 0, 0));
                 }
             }
-        if (!W16 && !Vg) return;   // C == 0: no V (W16 implies V)
-        const auto rv = rsrc(Vg + (seqStep + t) * R * static_cast<int64_t>(C), valid ? vBytes : 0u);
-        if constexpr (W16) {
+        if (!VBLOCK && !Vg) return;   // C == 0: no V (VBLOCK implies V)
+        const auto rv = rsrc(static_cast<const char*>(p.V) + (seqStep + t) * vBytes, valid ? vBytes : 0u);
+        auto ld1 = [](__amdgpu_buffer_rsrc_t r, int off) {   // one element as fp32 bits (bf16: raw)
+            if constexpr (sizeof(TV) == 4) return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+            else return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+        };
+        if constexpr (VK) {
+            const auto rk = rsrc(static_cast<const char*>(p.K) + (seqStep + t) * kBytes, valid ? kBytes : 0u);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o.vv[rt][i] = ld1(rv, offV[rt][0][i]);
+#pragma unroll
+            for (int h = 0; h < CTW; ++h) o.kk[h] = ld1(rk, offK[h]);
+        } else if constexpr (VBLOCK) {
 #pragma unroll
             for (int j = 0; j < NV; ++j) o.raw[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, offV[j][0][0], 0, 0));
         } else {
@@ -254,18 +281,24 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
 #pragma unroll
                 for (int h = 0; h < CTW; ++h)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if constexpr (sizeof(TV) == 4)
-                            o.Cv[rt][h][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, offV[rt][h][i], 0, 0));
-                        else   // raw bf16 bits, widened in convert_ops
-                            o.Cv[rt][h][i] = __uint_as_float(static_cast<uint32_t>(
-                                __builtin_amdgcn_raw_buffer_load_b16(rv, offV[rt][h][i], 0, 0)));
-                    }
+                    for (int i = 0; i < 4; ++i) o.Cv[rt][h][i] = ld1(rv, offV[rt][h][i]);   // bf16: raw bits
         }
     };
     // Bring a loaded operand set into the accumulator layout (fp32).
     auto convert_ops = [&](Ops& o) {
-        if constexpr (W16) {
+        auto widen = [](float x) {   // bf16 raw bits -> fp32
+            if constexpr (sizeof(TV) == 2) return __uint_as_float(__float_as_uint(x) << 16);
+            else return x;
+        };
+        if constexpr (VK) {
+            // V_t = v_t k_t^T, one fp32 product per element (as a materialised V)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int h = 0; h < CTW; ++h)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o.Cv[rt][h][i] = widen(o.vv[rt][i]) * widen(o.kk[h]);
+        } else if constexpr (VBLOCK) {
             // 16-byte pieces -> LDS (fp32) -> accumulator layout
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
@@ -299,7 +332,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
 #pragma unroll
                 for (int h = 0; h < CTW; ++h)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) o.Cv[rt][h][i] = __uint_as_float(__float_as_uint(o.Cv[rt][h][i]) << 16);
+                    for (int i = 0; i < 4; ++i) o.Cv[rt][h][i] = widen(o.Cv[rt][h][i]);
         }
     };
     // K-step-major order: consecutive MFMAs belong to different tiles, so none
@@ -310,7 +343,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < NT; ++ct)
-                acc[rt][ct] = (ct < RT || (!W16 && !Vg)) ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : o.Cv[rt][ct - RT];
+                acc[rt][ct] = (ct < RT || (!VBLOCK && !Vg)) ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : o.Cv[rt][ct - RT];
 #pragma unroll
         for (int kt = 0; kt < RT; ++kt)
 #pragma unroll
@@ -450,57 +483,70 @@ inline int dense_col_blocks(int64_t C, int ctw) {
     return C == 0 ? 1 : static_cast<int>((C + 16 * ctw - 1) / (16 * ctw));
 }
 
-template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE>
+template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE, bool VK>
 int dense_launch_ct(const ChunkParams& c, int64_t B, hipStream_t st) {
     const dim3 grid(c.nb, dense_col_blocks(c.C, CTW), static_cast<unsigned>(B));
     auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-    // W16: whole 16-byte pieces of both element types (C % 8 == 0).
-    const bool w16 = c.V && c.C % 8 == 0 && c.C >= 8 && al16(c.V) && (!c.outH || al16(c.outH));
+    // W16: whole 16-byte pieces of both element types (C % 8 == 0): V blocks
+    // (not VK) and staged H stores (not SUMMARY).
+    const bool w16 = c.V && (VK || al16(c.V)) && c.C % 8 == 0 && c.C >= 8 && (!c.outH || al16(c.outH));
     constexpr bool alwaysP = MODE == CM_SUMMARY || MODE == CM_LOCAL;
+    constexpr bool anyW16 = !(VK && MODE == CM_SUMMARY);   // VK summaries use neither path
     const bool wp = alwaysP || c.withP;
-    if (wp && w16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, true, TV, TO, MODE>), grid, dim3(64), 0, st, c);
-    else if (wp) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, false, TV, TO, MODE>), grid, dim3(64), 0, st, c);
+    if (wp && w16 && anyW16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, anyW16, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
+    else if (wp) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, false, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
     else if constexpr (!alwaysP) {
-        if (w16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, true, TV, TO, MODE>), grid, dim3(64), 0, st, c);
-        else hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, false, TV, TO, MODE>), grid, dim3(64), 0, st, c);
+        if (w16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, true, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
+        else hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, false, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
     }
     return check_launch("dense_chunk_kernel");
 }
 
-template <int RT, bool U4, typename TV, typename TO, int MODE>
+template <int RT, bool U4, typename TV, typename TO, int MODE, bool VK>
 int dense_launch_c(const ChunkParams& c, int64_t B, hipStream_t st) {
     const int ctw = dense_col_tiles(c.C);
     if (ctw > 1 && B * c.nb * dense_col_blocks(c.C, ctw) < kDenseNarrowWaves)
-        return dense_launch_ct<RT, 1, U4, TV, TO, MODE>(c, B, st);
+        return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK>(c, B, st);
     switch (ctw) {
-        case 1: return dense_launch_ct<RT, 1, U4, TV, TO, MODE>(c, B, st);
-        case 2: return dense_launch_ct<RT, 2, U4, TV, TO, MODE>(c, B, st);
-        case 3: return dense_launch_ct<RT, 3, U4, TV, TO, MODE>(c, B, st);
-        default: return dense_launch_ct<RT, 4, U4, TV, TO, MODE>(c, B, st);
+        case 1: return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK>(c, B, st);
+        case 2: return dense_launch_ct<RT, 2, U4, TV, TO, MODE, VK>(c, B, st);
+        case 3: return dense_launch_ct<RT, 3, U4, TV, TO, MODE, VK>(c, B, st);
+        default: return dense_launch_ct<RT, 4, U4, TV, TO, MODE, VK>(c, B, st);
     }
 }
 
 // One pass over a level.  U4: R % 4 == 0 and 16-byte aligned rows of U (level
 // >= 1 products live in the 256-byte aligned workspace).  The FIXED passes
-// require c.T == kDenseChunk.
-template <typename TV, typename TO, int MODE>
+// require c.T == kDenseChunk.  VK: V_t = v_t k_t^T from c.V = v, c.K = k.
+template <typename TV, typename TO, int MODE, bool VK = false>
 int dense_launch_pass(const ChunkParams& c, int64_t B, hipStream_t st) {
     if (MODE != CM_LOCAL && c.T != kDenseChunk)
         return set_error(MOGT_E_INVALID, "dense pass: chunk length %d, expected %d", c.T, kDenseChunk);
     const bool u4 = c.R % 4 == 0 && reinterpret_cast<uintptr_t>(c.U) % 16 == 0;
-    if (c.R <= 16) return u4 ? dense_launch_c<1, true, TV, TO, MODE>(c, B, st) : dense_launch_c<1, false, TV, TO, MODE>(c, B, st);
-    return u4 ? dense_launch_c<2, true, TV, TO, MODE>(c, B, st) : dense_launch_c<2, false, TV, TO, MODE>(c, B, st);
+    if (c.R <= 16) return u4 ? dense_launch_c<1, true, TV, TO, MODE, VK>(c, B, st) : dense_launch_c<1, false, TV, TO, MODE, VK>(c, B, st);
+    return u4 ? dense_launch_c<2, true, TV, TO, MODE, VK>(c, B, st) : dense_launch_c<2, false, TV, TO, MODE, VK>(c, B, st);
 }
 
 // Instantiated once each in dense_pass_*.hip (parallel compilation).
-extern template int dense_launch_pass<float, float, CM_SUMMARY>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<bf16_t, float, CM_SUMMARY>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<float, float, CM_EXCL>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<float, float, CM_LOCAL>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<bf16_t, float, CM_LOCAL>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<float, float, CM_OUTPUT>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<float, bf16_t, CM_OUTPUT>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<bf16_t, float, CM_OUTPUT>(const ChunkParams&, int64_t, hipStream_t);
-extern template int dense_launch_pass<bf16_t, bf16_t, CM_OUTPUT>(const ChunkParams&, int64_t, hipStream_t);
+#define MOGT_DENSE_PASSES(X)                 \
+    X(float, float, CM_SUMMARY, false)       \
+    X(bf16_t, float, CM_SUMMARY, false)      \
+    X(float, float, CM_EXCL, false)          \
+    X(float, float, CM_LOCAL, false)         \
+    X(bf16_t, float, CM_LOCAL, false)        \
+    X(float, float, CM_OUTPUT, false)        \
+    X(float, bf16_t, CM_OUTPUT, false)       \
+    X(bf16_t, float, CM_OUTPUT, false)       \
+    X(bf16_t, bf16_t, CM_OUTPUT, false)      \
+    X(float, float, CM_SUMMARY, true)        \
+    X(bf16_t, float, CM_SUMMARY, true)       \
+    X(float, float, CM_OUTPUT, true)         \
+    X(float, bf16_t, CM_OUTPUT, true)        \
+    X(bf16_t, float, CM_OUTPUT, true)        \
+    X(bf16_t, bf16_t, CM_OUTPUT, true)
+#define MOGT_DENSE_EXTERN(TV, TO, M, VK) \
+    extern template int dense_launch_pass<TV, TO, M, VK>(const ChunkParams&, int64_t, hipStream_t);
+MOGT_DENSE_PASSES(MOGT_DENSE_EXTERN)
+#undef MOGT_DENSE_EXTERN
 
 }  // namespace mogt

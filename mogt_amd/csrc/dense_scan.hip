@@ -83,12 +83,13 @@ int excl_scan(const float* U, const void* V, int64_t len, float* outP, float* ou
     return dense_launch_pass<TV, float, CM_EXCL>(c, B, st);
 }
 
-template <typename TV, typename TO>
-int run_levels(const float* U, const void* V, void* H, void* P, int64_t B, int64_t L, int64_t R,
-               int64_t C, char* ws, const DenseGeo& geo, hipStream_t st) {
+// Level 0 (VK: V_t = v_t k_t^T from V = v, K = k), then the carries, then H.
+template <typename TV, typename TO, bool VK>
+int run_levels(const float* U, const void* V, const void* K, void* H, void* P, int64_t B, int64_t L,
+               int64_t R, int64_t C, char* ws, const DenseGeo& geo, hipStream_t st) {
     const bool withP = P != nullptr;
     ChunkParams c{};
-    c.U = U; c.V = C > 0 ? V : nullptr;
+    c.U = U; c.V = C > 0 ? V : nullptr; c.K = VK ? K : nullptr;
     c.L = L; c.R = static_cast<int>(R); c.C = static_cast<int>(C); c.T = kDenseChunk;
     c.nb = static_cast<int>((L + c.T - 1) / c.T);
     c.withP = withP;
@@ -98,7 +99,7 @@ int run_levels(const float* U, const void* V, void* H, void* P, int64_t B, int64
         ChunkParams s = c;
         s.sumP = reinterpret_cast<float*>(ws + v.sumP);
         s.sumH = reinterpret_cast<float*>(ws + v.sumH);
-        int rc = dense_launch_pass<TV, float, CM_SUMMARY>(s, B, st);
+        int rc = dense_launch_pass<TV, float, CM_SUMMARY, VK>(s, B, st);
         if (rc) return rc;
         rc = excl_scan<float>(s.sumP, s.sumH, c.nb, reinterpret_cast<float*>(ws + v.carP),
                               reinterpret_cast<float*>(ws + v.carH), B, R, C, withP, ws, geo, 1, st);
@@ -106,7 +107,7 @@ int run_levels(const float* U, const void* V, void* H, void* P, int64_t B, int64
         c.carP = withP ? reinterpret_cast<float*>(ws + v.carP) : nullptr;
         c.carH = reinterpret_cast<float*>(ws + v.carH);
     }
-    return dense_launch_pass<TV, TO, CM_OUTPUT>(c, B, st);
+    return dense_launch_pass<TV, TO, CM_OUTPUT, VK>(c, B, st);
 }
 
 int check_dense_shapes(int64_t B, int64_t L, int64_t R, int64_t C) {
@@ -117,8 +118,9 @@ int check_dense_shapes(int64_t B, int64_t L, int64_t R, int64_t C) {
     return MOGT_OK;
 }
 
-int run_dense(const float* U, const void* V, void* H, void* P, int64_t B, int64_t L, int64_t R,
-              int64_t C, int v_dtype, int out_dtype, void* ws, size_t ws_bytes, void* stream) {
+// K != nullptr: the rank-1 form, V holds v [B, L, R] and K holds k [B, L, C].
+int run_dense(const float* U, const void* V, const void* K, void* H, void* P, int64_t B, int64_t L,
+              int64_t R, int64_t C, int v_dtype, int out_dtype, void* ws, size_t ws_bytes, void* stream) {
     clear_error();
     int rc = check_dense_shapes(B, L, R, C);
     if (rc) return rc;
@@ -133,10 +135,17 @@ int run_dense(const float* U, const void* V, void* H, void* P, int64_t B, int64_
         return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", g.bytes, ws_bytes);
     char* base = static_cast<char*>(ws);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (v_dtype == MOGT_F32 && out_dtype == MOGT_F32) return run_levels<float, float>(U, V, H, P, B, L, R, C, base, g, st);
-    if (v_dtype == MOGT_F32 && out_dtype == MOGT_BF16) return run_levels<float, bf16_t>(U, V, H, P, B, L, R, C, base, g, st);
-    if (v_dtype == MOGT_BF16 && out_dtype == MOGT_F32) return run_levels<bf16_t, float>(U, V, H, P, B, L, R, C, base, g, st);
-    return run_levels<bf16_t, bf16_t>(U, V, H, P, B, L, R, C, base, g, st);
+    const bool vf = v_dtype == MOGT_F32, of = out_dtype == MOGT_F32;
+    if (K) {
+        if (vf && of) return run_levels<float, float, true>(U, V, K, H, P, B, L, R, C, base, g, st);
+        if (vf) return run_levels<float, bf16_t, true>(U, V, K, H, P, B, L, R, C, base, g, st);
+        if (of) return run_levels<bf16_t, float, true>(U, V, K, H, P, B, L, R, C, base, g, st);
+        return run_levels<bf16_t, bf16_t, true>(U, V, K, H, P, B, L, R, C, base, g, st);
+    }
+    if (vf && of) return run_levels<float, float, false>(U, V, K, H, P, B, L, R, C, base, g, st);
+    if (vf) return run_levels<float, bf16_t, false>(U, V, K, H, P, B, L, R, C, base, g, st);
+    if (of) return run_levels<bf16_t, float, false>(U, V, K, H, P, B, L, R, C, base, g, st);
+    return run_levels<bf16_t, bf16_t, false>(U, V, K, H, P, B, L, R, C, base, g, st);
 }
 
 }  // namespace
@@ -154,8 +163,20 @@ extern "C" int mogt_affine_scan_fwd(const void* U, const void* V, void* H, void*
                                     int64_t length, int64_t rank, int64_t channels, int v_dtype,
                                     int out_dtype, void* workspace, size_t workspace_bytes,
                                     void* stream) {
-    return run_dense(static_cast<const float*>(U), V, H, U_prefix, batch, length, rank, channels,
+    return run_dense(static_cast<const float*>(U), V, nullptr, H, U_prefix, batch, length, rank, channels,
                      v_dtype, out_dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mogt_affine_scan_vk_fwd(const void* U, const void* v, const void* k, void* H, void* U_prefix,
+                                       int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                       int vk_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    if (channels > 0 && (!v || !k)) {
+        clear_error();
+        return set_error(MOGT_E_INVALID, "null tensor pointer");
+    }
+    return run_dense(static_cast<const float*>(U), v, channels > 0 ? k : nullptr, H, U_prefix, batch, length,
+                     rank, channels, vk_dtype, out_dtype, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t mogt_fused_scan_workspace_bytes(int64_t batch, int64_t length, int64_t rank) {
@@ -165,7 +186,7 @@ extern "C" size_t mogt_fused_scan_workspace_bytes(int64_t batch, int64_t length,
 extern "C" int mogt_fused_scan_fwd(const void* U, void* Y, int64_t batch, int64_t length, int64_t rank,
                                    int out_dtype, void* workspace, size_t workspace_bytes,
                                    void* stream) {
-    return run_dense(static_cast<const float*>(U), nullptr, nullptr, Y, batch, length, rank, 0,
+    return run_dense(static_cast<const float*>(U), nullptr, nullptr, nullptr, Y, batch, length, rank, 0,
                      MOGT_F32, out_dtype, workspace, workspace_bytes, stream);
 }
 

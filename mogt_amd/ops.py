@@ -295,6 +295,66 @@ def affine_scan(U: torch.Tensor, V: torch.Tensor, *, output_dtype: torch.dtype |
     return torch.ops.mogt.affine_scan(U, V, output_dtype)
 
 
+# ---------------------------------------------------------------------------
+# dense_scan: the matrix scan with B_t given densely or as a rank-1 write v k^T
+# ---------------------------------------------------------------------------
+def check_vk_shapes(U: torch.Tensor, v: torch.Tensor, k: torch.Tensor) -> tuple[int, int, int, int]:
+    if U.ndim != 4 or v.ndim != 3 or k.ndim != 3:
+        raise ValueError("U must be [B, L, R, R], v [B, L, R] and k [B, L, C]")
+    B, L, R, R2 = U.shape
+    if R != R2 or tuple(v.shape) != (B, L, R) or tuple(k.shape[:2]) != (B, L):
+        raise ValueError("U must be [B, L, R, R], v [B, L, R] and k [B, L, C]")
+    if R > 32:
+        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= 32)")
+    return B, L, R, k.shape[-1]
+
+
+@torch.library.custom_op("mogt::affine_scan_vk", mutates_args=())
+def _affine_scan_vk_op(U: torch.Tensor, v: torch.Tensor, k: torch.Tensor,
+                       out_dtype: torch.dtype) -> torch.Tensor:
+    B, L, R, C = check_vk_shapes(U, v, k)
+    U = U.contiguous()
+    if U.dtype != torch.float32:
+        U = U.to(torch.float32)
+    if v.dtype not in _DTYPE_CODE or k.dtype != v.dtype:
+        wide = torch.float32 if v.dtype not in _DTYPE_CODE else v.dtype
+        v, k = v.to(wide), k.to(wide)
+    v, k = v.contiguous(), k.contiguous()
+    H = torch.empty((B, L, R, C), dtype=out_dtype, device=U.device)
+    lib = _lib.load()
+    ws = workspace(lib.mogt_affine_scan_workspace_bytes(B, L, R, C), U.device)
+    rc = lib.mogt_affine_scan_vk_fwd(U.data_ptr(), v.data_ptr(), k.data_ptr(), H.data_ptr(), None,
+                                     B, L, R, C, dtype_code(v.dtype, "dense_scan"),
+                                     dtype_code(out_dtype, "dense_scan"), ws.data_ptr(), ws.numel(),
+                                     _stream_handle(U.device))
+    _lib.check(rc, "mogt_affine_scan_vk_fwd")
+    return H
+
+
+@_affine_scan_vk_op.register_fake
+def _(U, v, k, out_dtype):
+    return U.new_empty((*v.shape, k.shape[-1]), dtype=out_dtype)
+
+
+def dense_scan(A: torch.Tensor, Bm: torch.Tensor | None = None, *, v: torch.Tensor | None = None,
+               k: torch.Tensor | None = None, output_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``S_t = A_t S_{t-1} + B_t``, ``S_0 = 0`` (fp32 state) with either a dense
+    ``Bm [B, L, R, C]`` or a rank-1 write ``B_t = v_t k_t^T`` from ``v [B, L, R]``
+    and ``k [B, L, C]``, which is formed in registers and never written to
+    memory (configs[3]'s ``B_t = v_t k_t^T``).  ``output_dtype`` defaults to the
+    dtype of ``Bm`` (or ``v``)."""
+    if (Bm is None) == (v is None and k is None) or (Bm is None and (v is None or k is None)):
+        raise ValueError("dense_scan takes either Bm or both v and k")
+    if Bm is not None:
+        return affine_scan(A, Bm, output_dtype=output_dtype)
+    require_cuda("dense_scan", A, v, k)
+    check_vk_shapes(A, v, k)
+    output_dtype = output_dtype or v.dtype
+    if output_dtype not in _DTYPE_CODE:
+        raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
+    return torch.ops.mogt.affine_scan_vk(A, v, k, output_dtype)
+
+
 @torch.library.custom_op("mogt::fused_scan", mutates_args=())
 def _fused_scan_op(U: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     Uf = U.contiguous().to(torch.float32)

@@ -68,9 +68,11 @@ def skew_generators(n: int, d: int, *, std: float = 0.05, g: np.random.Generator
     return T - np.swapaxes(T, -1, -2)
 
 
-def dense_cayley_inputs(B: int, L: int, H: int, d: int, *, seed: int = 0, chunk: int = 8192):
+def dense_cayley_inputs(B: int, L: int, H: int, d: int, *, seed: int = 0, chunk: int = 8192,
+                        return_vk: bool = False):
     """U [B*H, L, d, d] (fp32) and V = v k^T [B*H, L, d, d] in the affine-scan API
-    layout (sequence index = b*H + h)."""
+    layout (sequence index = b*H + h); with ``return_vk`` also v and k
+    [B*H, L, d] (V is their fp32 outer product)."""
     g = rng(seed)
     n = B * H * L
     U = np.empty((n, d, d), dtype=np.float32)
@@ -87,7 +89,11 @@ def dense_cayley_inputs(B: int, L: int, H: int, d: int, *, seed: int = 0, chunk:
     # [B, L, H, d, d] -> [B*H, L, d, d]
     U = U.reshape(B, L, H, d, d).transpose(0, 2, 1, 3, 4).reshape(B * H, L, d, d)
     V = V.reshape(B, L, H, d, d).transpose(0, 2, 1, 3, 4).reshape(B * H, L, d, d)
-    return np.ascontiguousarray(U), np.ascontiguousarray(V)
+    if not return_vk:
+        return np.ascontiguousarray(U), np.ascontiguousarray(V)
+    v = v.reshape(B, L, H, d).transpose(0, 2, 1, 3).reshape(B * H, L, d)
+    k = k.reshape(B, L, H, d).transpose(0, 2, 1, 3).reshape(B * H, L, d)
+    return tuple(np.ascontiguousarray(x) for x in (U, V, v, k))
 
 
 def reference_test_case(batch_size=2, seq_len=17, rank=4, channels=3):

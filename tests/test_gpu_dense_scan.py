@@ -187,6 +187,65 @@ def test_cfg4_dense_cayley_full_size(gpu):
     assert rel_err(to_np(S), ref) <= FP32_TOL
 
 
+@pytest.mark.parametrize("B,L,R,C", [(2, 1000, 16, 48), (1, 777, 7, 11), (3, 300, 32, 32), (1, 64, 5, 130)])
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_dense_scan_vk_equals_materialised(gpu, B, L, R, C, dt):
+    """B_t = v_t k_t^T formed in registers: bit-identical to the scan of the
+    materialised fp32 V = v k^T (same fp32 products, same MFMA sequence)."""
+    announce(f"dense vk B={B} L={L} R={R} C={C} {dt}")
+    import mogt_amd
+
+    g = np.random.default_rng(B * 1000 + L + R + C)
+    U = (np.eye(R, dtype=np.float32) * 0.95 + 0.03 * g.standard_normal((B, L, R, R), dtype=np.float32))
+    v = g.standard_normal((B, L, R), dtype=np.float32)
+    k = g.standard_normal((B, L, C), dtype=np.float32)
+    Ut = torch.from_numpy(U).to(gpu)
+    vt, kt = torch.from_numpy(v).to(gpu), torch.from_numpy(k).to(gpu)
+    if dt == "bf16":
+        vt, kt = vt.bfloat16(), kt.bfloat16()
+    V = vt.float()[..., :, None] * kt.float()[..., None, :]
+    for out in (torch.float32, torch.bfloat16):
+        S = mogt_amd.dense_scan(Ut, v=vt, k=kt, output_dtype=out)
+        S_ref = mogt_amd.ops.affine_scan(Ut, V.contiguous(), output_dtype=out)
+        torch.cuda.synchronize()
+        assert S.shape == (B, L, R, C) and S.dtype == out
+        assert torch.equal(S, S_ref)
+    ref = so.affine_scan_sequential(U, to_np(V))
+    S32 = mogt_amd.dense_scan(Ut, v=vt, k=kt, output_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(S32), ref) <= FP32_TOL
+
+
+def test_cfg4_dense_cayley_vk_full_size(gpu):
+    """configs[3] with B_t = v_t k_t^T never materialised: bit-identical to the
+    materialised-V scan (itself checked against the oracle above)."""
+    announce("cfg4 dense cayley vk full size")
+    import mogt_amd
+
+    U, V, v, k = synthetic.dense_cayley_inputs(1, 16384, 8, 32, seed=0, return_vk=True)
+    Ut = torch.from_numpy(U).to(gpu)
+    S_vk = mogt_amd.dense_scan(Ut, v=torch.from_numpy(v).to(gpu), k=torch.from_numpy(k).to(gpu))
+    S = mogt_amd.dense_scan(Ut, torch.from_numpy(V).to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(S_vk, S)
+
+
+def test_dense_scan_argument_errors(gpu):
+    import mogt_amd
+
+    U = torch.zeros(1, 4, 3, 3, device=gpu)
+    v = torch.zeros(1, 4, 3, device=gpu)
+    k = torch.zeros(1, 4, 5, device=gpu)
+    with pytest.raises(ValueError):
+        mogt_amd.dense_scan(U)
+    with pytest.raises(ValueError):
+        mogt_amd.dense_scan(U, torch.zeros(1, 4, 3, 5, device=gpu), v=v, k=k)
+    with pytest.raises(ValueError):
+        mogt_amd.dense_scan(U, v=v)
+    with pytest.raises(ValueError):
+        mogt_amd.dense_scan(U, v=torch.zeros(1, 4, 2, device=gpu), k=k)
+
+
 def test_zz_dense_no_lookback_wait_gave_up(gpu):
     from mogt_amd import ops
 
