@@ -27,10 +27,11 @@ bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 // lanes of one vector must share a gate, so the vector must divide the channel
 // count), 512-step chunks; short problems fall back to shorter chunks.
 DiagTile coupled_tile(int64_t B, int64_t L, int64_t R, int64_t C, int align_elems) {
-    static const DiagTile v4[] = {{4, 16, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
-    static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
-    static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
-    if (C % 4 == 0 && align_elems % 4 == 0) return pick_tile(B, L, R * C, v4, 3);
+    static const TileChoice v4[] = {{{4, 16, 8, 16}, 512}, {{4, 16, 8, 8}, 128}, {{2, 32, 8, 16}, 128},
+                                    {{1, 64, 8, 16}, 0}};
+    static const TileChoice v2[] = {{{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
+    static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
+    if (C % 4 == 0 && align_elems % 4 == 0) return pick_tile(B, L, R * C, v4, 4);
     if (C % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, R * C, v2, 3);
     return pick_tile(B, L, R * C, v1, 3);
 }

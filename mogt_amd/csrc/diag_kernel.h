@@ -398,10 +398,17 @@ inline int64_t diag_groups(int64_t B, int64_t L, int64_t D, const DiagTile& t) {
 // work-groups; else the last (shortest).  Measured at D = 768, L = 8192: 192
 // long chunks (fewer than the 256 CUs) beat 768 short ones, because short
 // chunks put more chunks of one chain in flight and lengthen the look-back.
-inline DiagTile pick_tile(int64_t B, int64_t L, int64_t D, const DiagTile* list, int n) {
+// Default tile: the first of `list` whose launch has at least its minimum
+// number of work-groups (else the last).  Lists and thresholds come from
+// MI355X sweeps at D = 768, L = 8K / 16K / 32K.
+struct TileChoice {
+    DiagTile tile;
+    int64_t min_groups;
+};
+inline DiagTile pick_tile(int64_t B, int64_t L, int64_t D, const TileChoice* list, int n) {
     for (int i = 0; i < n - 1; ++i)
-        if (diag_groups(B, L, D, list[i]) >= 128) return list[i];
-    return list[n - 1];
+        if (diag_groups(B, L, D, list[i].tile) >= list[i].min_groups) return list[i].tile;
+    return list[n - 1].tile;
 }
 
 // Shape checks shared by every entry point; fills prm (except tensor pointers).
@@ -440,9 +447,9 @@ int diag_launch(const DiagParams& prm, hipStream_t stream) {
 // row, steps per lane, waves per work-group), per input family.  Every tile
 // keeps rows of at least 256 contiguous bytes (narrower rows cost HBM
 // efficiency) and at most 64 stash registers per lane.
-#define MOGT_DIAG_F32_TILES(X) X(2, 32, 16, 16) X(1, 64, 32, 16) X(2, 32, 8, 16) X(1, 64, 16, 16) X(1, 64, 8, 16) X(2, 64, 16, 16)
-#define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 16) X(4, 64, 8, 16) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
-#define MOGT_COUPLED_TILES(X) X(2, 32, 16, 16) X(4, 16, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_DIAG_F32_TILES(X) X(2, 32, 32, 8) X(2, 32, 16, 16) X(2, 32, 16, 8) X(2, 32, 32, 4) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 8) X(4, 16, 16, 16) X(4, 16, 8, 8) X(4, 32, 16, 8) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_COUPLED_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(4, 16, 16, 16) X(4, 32, 8, 16) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 
 // Per-family launchers (diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
 int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,

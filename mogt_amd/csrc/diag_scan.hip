@@ -26,16 +26,17 @@ bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 // shorter chunks so the grid still covers the GPU.
 DiagTile default_tile(int64_t B, int64_t L, int64_t D, bool bf16_in, int align_elems) {
     if (bf16_in) {
-        static const DiagTile v4[] = {{4, 16, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
-        static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
-        static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
+        static const TileChoice v4[] = {{{4, 16, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
+        static const TileChoice v2[] = {{{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
+        static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
         if (D % 4 == 0 && align_elems % 4 == 0) return pick_tile(B, L, D, v4, 3);
         if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 3);
         return pick_tile(B, L, D, v1, 3);
     }
-    static const DiagTile v2[] = {{2, 32, 16, 16}, {2, 32, 8, 16}, {1, 64, 8, 16}};
-    static const DiagTile v1[] = {{1, 64, 32, 16}, {1, 64, 16, 16}, {1, 64, 8, 16}};
-    if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 3);
+    static const TileChoice v2[] = {{{2, 32, 32, 8}, 128}, {{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128},
+                                    {{1, 64, 8, 16}, 0}};
+    static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
+    if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 4);
     return pick_tile(B, L, D, v1, 3);
 }
 

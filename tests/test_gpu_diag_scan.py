@@ -20,10 +20,10 @@ BF16_TOL = 2e-2
 
 # every compiled tile (vec, lanes per row, steps per lane, waves); the CPU test
 # test_capi.py::test_gpu_tile_lists_match_library keeps these in step
-TILES_F32 = [(2, 32, 16, 16), (1, 64, 32, 16), (2, 32, 8, 16), (1, 64, 16, 16), (1, 64, 8, 16),
-             (2, 64, 16, 16)]
-TILES_BF16 = [(4, 16, 16, 16), (4, 64, 8, 16), (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16),
-              (1, 64, 16, 16), (1, 64, 8, 16)]
+TILES_F32 = [(2, 32, 32, 8), (2, 32, 16, 16), (2, 32, 16, 8), (2, 32, 32, 4), (2, 32, 8, 16),
+             (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
+TILES_BF16 = [(4, 16, 16, 8), (4, 16, 16, 16), (4, 16, 8, 8), (4, 32, 16, 8), (2, 32, 16, 8),
+              (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
 
 
 def _run_cfg(a, b, out_dtype, cfg, prefix=False):
