@@ -134,6 +134,30 @@ def measure_diag(torch, lib, ops, L, dtype, out_dtype, steps, warmup, tile=None,
     return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
 
 
+def measure_diag_rev(torch, lib, ops, L, steps, warmup, D=768, B=1, sets=3):
+    """Reverse-time diagonal scan (the backward's G_t = dH_t + a_{t+1} G_{t+1}),
+    fp32 a, dH in, G out, via mogt_diag_scan_rev_fwd."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    bufs = [(torch.sigmoid(torch.randn(B, L, D, generator=gen, device=dev) + 3.0),
+             torch.randn(B, L, D, generator=gen, device=dev), torch.empty(B, L, D, device=dev))
+            for _ in range(sets)]
+    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, 0), dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def launch(i):
+        a, g, out = bufs[i % sets]
+        rc = lib.mogt_diag_scan_rev_fwd(a.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, D,
+                                        ws.data_ptr(), ws.numel(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    total = B * L * D * 12
+    return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
+
+
 def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
     """Model-shaped coupled per-rank gate scan (config 2'): z fp32 [1,L,16],
     v bf16 [1,L,768] -> h fp32 [1,L,768]."""
@@ -415,6 +439,11 @@ def main():
                              args.warmup)
             extras[f"diag_bf16_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                                          "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+        r = measure_diag_rev(torch, lib, ops, 32768, args.steps, args.warmup)
+        extras["diag_rev_fp32_L32768"] = {
+            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+            "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
         r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
         extras["coupled_rank_scan_r16c48_L32768"] = {
             "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),

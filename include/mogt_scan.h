@@ -74,6 +74,17 @@ int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix
                            void* workspace, size_t workspace_bytes, void* stream);
 int mogt_diag_scan_tiles(int family, int* out, int max_tiles);
 
+/* Reverse-time diagonal scan h_t = a_{t+1} * h_{t+1} + b_t, h_L = 0 (a_L
+ * unused), fp32 a, b, h [B, L, D]: with b = dH it is the gradient
+ * G_t = dH_t + a_{t+1} G_{t+1} of the diagonal scan, the R = C = 1 case of
+ * affine_scan_sequential_backward (affine_scan.py:65-124) and of the reverse
+ * scan of _triton_affine_scan_hybrid_backward (triton_scan.py:359-426); then
+ * db = G and da_t = G_t h_{t-1}.  Workspace:
+ * mogt_diag_scan_workspace_bytes(batch, length, features, MOGT_F32).        */
+int mogt_diag_scan_rev_fwd(const void* a, const void* b, void* h,
+                           int64_t batch, int64_t length, int64_t features,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Coupled write-forget per-rank scan of the MOGT mixer with identity
  * connection (model_mogt.py:166-203 with connection_impl="identity",

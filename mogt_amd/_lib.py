@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
          _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_diag_scan_rev_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p]),
     "mogt_diag_scan_workspace_bytes_cfg": (
         _c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int]),
     "mogt_diag_scan_fwd_cfg": (

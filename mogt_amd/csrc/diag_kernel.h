@@ -47,7 +47,10 @@
 
 namespace mogt {
 
-enum DiagMode { MODE_DIAG = 0, MODE_COUPLED = 1 };
+// MODE_DIAG_REV: the backward recurrence of MODE_DIAG, run in reverse time
+// with the decay shifted by one step: h_t = a_{t+1} h_{t+1} + b_t (a_L := 0),
+// i.e. G_t = dH_t + a_{t+1} G_{t+1} of affine_scan.py:65-124 for R = C = 1.
+enum DiagMode { MODE_DIAG = 0, MODE_COUPLED = 1, MODE_DIAG_REV = 2 };
 
 struct DiagParams {
     const void* a;      // [B, L, D] (DIAG)            | gate logits z [B, L, R] (COUPLED)
@@ -79,6 +82,8 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int NR = NT / FW;       // look-back window (predecessors read per round)
     static_assert(64 % FWL == 0 && FWL >= 16, "a row spans 16, 32 or 64 lanes");
     constexpr bool COUPLED = MODE == MODE_COUPLED;
+    constexpr bool REV = MODE == MODE_DIAG_REV;
+    static_assert(!(PREFIX && REV), "prefix output is a forward option");
     constexpr bool BF16_IN = std::is_same<TIn, bf16_t>::value;
     // Stash (32-bit registers per step and lane): DIAG fp32 a[VEC], b[VEC];
     // DIAG bf16 raw a and b words (two values per word); COUPLED the gate logit
@@ -113,6 +118,11 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     const int64_t t0 = tw + q * S;             // first step of this lane
     const int64_t row0 = static_cast<int64_t>(bi) * p.L;
     const int Di = static_cast<int>(p.D);      // row stride (checked on the host)
+    // Memory row of logical step t: row0 + t, or row0 + L - 1 - t in reverse
+    // time (REV), where rows are walked with a negative stride.
+    const int64_t rbase = REV ? row0 + p.L - 1 : row0;
+    const int Ds = REV ? -Di : Di;             // signed row stride
+    const bool first = REV && t0 == 0;         // REV: this lane holds step 0 (a_L := 0)
 
     // The launch epoch is read by every lane before the data loads are issued:
     // memory counters retire in order, so waiting for it never waits for data.
@@ -133,7 +143,10 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         nv = !fvalid || r <= 0 ? 0 : (r >= S ? S : static_cast<int>(r));
         const int lastrel = static_cast<int>(p.L - 1 - tw);   // last row of the problem, from tw
         const int flc = fvalid ? flane : 0;
-        const int64_t wbase = (row0 + tw) * p.D + fbase;
+        const int64_t wbase = (rbase + (REV ? -tw : tw)) * p.D + fbase;
+        // REV reads a one row later in memory (a_{t+1}), except for logical
+        // step 0, whose a_L does not exist: it reads row L - 1 and uses a = 0
+        // (step_a); clamped rows past the end map to step 0 too when L = 1
         const TIn* pa = static_cast<const TIn*>(p.a) + wbase;
         const TIn* pb = static_cast<const TIn*>(p.b) + wbase;
         const TZ* pz = nullptr;
@@ -145,7 +158,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int rel = min(q * S + s, lastrel);
-            const int off = rel * Di + flc;
+            const int off = rel * Ds + flc;
             load_raw<sizeof(TIn) * VEC>(pb + off, rb[s]);
             if constexpr (COUPLED) {
                 uint32_t zw[1];
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 ra[s][0] = __uint_as_float(zw[0]);
             } else {
                 uint32_t aw[NA];
-                load_raw<sizeof(TIn) * VEC>(pa + off, aw);
+                load_raw<sizeof(TIn) * VEC>(pa + off + ((REV && tw + rel != 0) ? Di : 0), aw);
 #pragma unroll
                 for (int j = 0; j < NA; ++j) ra[s][j] = __uint_as_float(aw[j]);
             }
@@ -195,6 +208,9 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     };
     // Element accessors (fp32 values of a and b for step s, feature v).
     auto step_a = [&](int s, int v) -> float {
+        if constexpr (REV) {
+            if (s == 0 && first) return 0.0f;
+        }
         if constexpr (COUPLED) return ra[s][0];
         else if constexpr (BF16_IN) return s < nv ? bf16_at(__float_as_uint(ra[s][v >> 1]), v) : 1.0f;
         else return s < nv ? ra[s][v] : 1.0f;
@@ -321,7 +337,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
             hh[v] = fmaf(cwA, s_inH[flane + v], s_cwH[vw][flane + v]);
             Ap[v] = cwA * s_inA[flane + v];
         }
-        const int64_t wbase = (row0 + tw) * p.D + fbase;
+        const int64_t wbase = (rbase + (REV ? -tw : tw)) * p.D + fbase;
         TOut* ph = static_cast<TOut*>(p.h) + wbase;
         TOut* pp = PREFIX ? static_cast<TOut*>(p.aprefix) + wbase : nullptr;
 #pragma unroll
@@ -335,7 +351,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 o[v] = hh[v];
             }
             if (s < nv) {
-                const int off = (q * S + s) * Di + flane;
+                const int off = (q * S + s) * Ds + flane;
                 store_stream<TOut, VEC>(ph + off, o);
                 if constexpr (PREFIX) {
 #pragma unroll
@@ -457,5 +473,6 @@ int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool
 int diag_run_bf16in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,
                     hipStream_t stream);
 bool diag_tile_compiled(int family, const DiagTile& t);   // family: 0 f32, 1 bf16, 2 coupled
+int diag_run_rev(const DiagParams& prm, const DiagTile& t, hipStream_t stream);   // diag_rev.hip
 
 }  // namespace mogt

@@ -40,9 +40,10 @@ DiagTile default_tile(int64_t B, int64_t L, int64_t D, bool bf16_in, int align_e
     return pick_tile(B, L, D, v1, 3);
 }
 
+// rev: the reverse-time recurrence h_t = a_{t+1} h_{t+1} + b_t (fp32 only).
 int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, int64_t L,
              int64_t D, int in_dtype, int out_dtype, const DiagTile& t, void* ws, size_t ws_bytes,
-             void* stream) {
+             void* stream, bool rev = false) {
     clear_error();
     if (B < 0 || L < 0 || D < 0) return set_error(MOGT_E_INVALID, "negative size");
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
@@ -68,6 +69,7 @@ int run_scan(const void* a, const void* b, void* h, void* aprefix, int64_t B, in
     prm.damping = 1.0f;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool pre = aprefix != nullptr;
+    if (rev) return diag_run_rev(prm, t, st);
     return family == 1 ? diag_run_bf16in(prm, t, out_dtype, pre, st)
                        : diag_run_f32in(prm, t, out_dtype, pre, st);
 }
@@ -134,6 +136,15 @@ extern "C" int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a
     const DiagTile t = default_tile(batch, length, features, in_dtype == MOGT_BF16, al);
     return run_scan(a, b, h, a_prefix, batch, length, features, in_dtype, out_dtype, t, workspace,
                     workspace_bytes, stream);
+}
+
+extern "C" int mogt_diag_scan_rev_fwd(const void* a, const void* b, void* h, int64_t batch,
+                                      int64_t length, int64_t features, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    const int al = common_alignment(a, b, h, nullptr, MOGT_F32, MOGT_F32);
+    const DiagTile t = default_tile(batch, length, features, false, al);
+    return run_scan(a, b, h, nullptr, batch, length, features, MOGT_F32, MOGT_F32, t, workspace,
+                    workspace_bytes, stream, true);
 }
 
 extern "C" int mogt_diag_scan_tiles(int family, int* out, int max_tiles) {

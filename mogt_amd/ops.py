@@ -137,6 +137,58 @@ def _(a, b, out_dtype):
     return a.new_empty(a.shape, dtype=out_dtype), a.new_empty(a.shape, dtype=out_dtype)
 
 
+@torch.library.custom_op("mogt::diag_scan_rev", mutates_args=())
+def _diag_scan_rev_op(a: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """G_t = g_t + a_{t+1} G_{t+1} (G_L = 0) in fp32: the reverse-time scan of
+    the diagonal scan's backward."""
+    lib = _lib.load()
+    a = a.to(torch.float32).contiguous()
+    g = g.to(torch.float32).contiguous()
+    B, L, D = a.shape
+    out = torch.empty(a.shape, dtype=torch.float32, device=a.device)
+    ws = workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, _lib.MOGT_F32), a.device)
+    rc = lib.mogt_diag_scan_rev_fwd(a.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, D,
+                                    ws.data_ptr(), ws.numel(), _stream_handle(a.device))
+    _lib.check(rc, "mogt_diag_scan_rev_fwd")
+    return out
+
+
+@_diag_scan_rev_op.register_fake
+def _(a, g):
+    return a.new_empty(a.shape, dtype=torch.float32)
+
+
+def _shift_prev(h: torch.Tensor) -> torch.Tensor:
+    """h_{t-1} with h_{-1} = 0 along dim 1."""
+    out = torch.zeros_like(h)
+    out[:, 1:] = h[:, :-1]
+    return out
+
+
+def _diag_scan_setup(ctx, inputs, output):
+    a, b, _ = inputs
+    ctx.save_for_backward(a, b)
+
+
+def _diag_scan_backward(ctx, grad_h):
+    """Reverse scan on the GPU (affine_scan.py:65-124 for R = C = 1): G = dH +
+    a_{t+1} G_{t+1}; db = G; da_t = G_t h_{t-1}, with h recomputed in fp32 as
+    the reference's backward does (triton_scan.py:370-378)."""
+    a, b = ctx.saved_tensors
+    need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    G = torch.ops.mogt.diag_scan_rev(a, grad_h)
+    da = db = None
+    if need_a:
+        h = torch.ops.mogt.diag_scan(a.float().contiguous(), b.float().contiguous(), torch.float32)
+        da = (G * _shift_prev(h)).to(a.dtype)
+    if need_b:
+        db = G.to(b.dtype)
+    return da, db, None
+
+
+torch.library.register_autograd("mogt::diag_scan", _diag_scan_backward, setup_context=_diag_scan_setup)
+
+
 def diag_scan(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype | None = None,
               return_prefix: bool = False):
     """h_t = a_t * h_{t-1} + b_t (h_0 = 0) over ``[B, L, D]`` on the GPU.
@@ -181,6 +233,44 @@ def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: 
 @_coupled_rank_scan_op.register_fake
 def _(z, v, rank, damping, out_dtype):
     return v.new_empty(v.shape, dtype=out_dtype)
+
+
+def _coupled_setup(ctx, inputs, output):
+    z, v, rank, damping, _ = inputs
+    ctx.save_for_backward(z, v)
+    ctx.rank = rank
+    ctx.damping = damping
+
+
+def _coupled_backward(ctx, grad_h):
+    """Backward of the fused gate + scan.  With g = sigmoid(z), a = damping (1-g)
+    (per rank, over its c channels) and v' = v * g:  G = dH + a_{t+1} G_{t+1}
+    (GPU reverse scan), dv = G * g, and per rank
+    dg = sum_c G * v - damping * sum_c G * h_{t-1}, dz = dg * g (1 - g), with h
+    recomputed in fp32 (the reference recomputes too, triton_scan.py:370-378).
+    The bf16 rounding of v * g (model_mogt.py:180) passes gradients through
+    unchanged, as a dtype cast does under autograd."""
+    z, v = ctx.saved_tensors
+    r, damping = ctx.rank, ctx.damping
+    B, L, D = v.shape
+    c = D // r
+    g = torch.sigmoid(z.float())                                   # [B, L, r]
+    a_full = (damping * (1.0 - g)).unsqueeze(-1).expand(B, L, r, c).reshape(B, L, D)
+    G = torch.ops.mogt.diag_scan_rev(a_full, grad_h)               # fp32 [B, L, D]
+    Gr = G.view(B, L, r, c)
+    dz = dv = None
+    if ctx.needs_input_grad[1]:
+        g_io = g.to(v.dtype).float()                               # the gate as multiplied into v
+        dv = (Gr * g_io.unsqueeze(-1)).reshape(B, L, D).to(v.dtype)
+    if ctx.needs_input_grad[0]:
+        h = torch.ops.mogt.coupled_rank_scan(z, v, r, damping, torch.float32)
+        hp = _shift_prev(h).view(B, L, r, c)
+        dg = (Gr * v.float().view(B, L, r, c)).sum(-1) - damping * (Gr * hp).sum(-1)
+        dz = (dg * g * (1.0 - g)).to(z.dtype)
+    return dz, dv, None, None, None
+
+
+torch.library.register_autograd("mogt::coupled_rank_scan", _coupled_backward, setup_context=_coupled_setup)
 
 
 def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,

@@ -1,0 +1,132 @@
+"""GPU backward of the diagonal and coupled scans (the reverse-time HIP scan
+behind ``torch.library.register_autograd``) against the float64 oracle.
+
+The diagonal case is checked against ``affine_scan_sequential_backward``
+(affine_scan.py:65-124 restated) in the folded R = C = 1 mapping, including a
+full-size L = 32768 run; the coupled mixer scan against ``torch.autograd`` of a
+float64 CPU restatement of the same recurrence (model_mogt.py:166-182 with the
+identity connection), the reference's own way of checking its backward
+(sanity_affine_scan.py:102-135).  Bars: fp32 <= 1e-4, bf16 inputs <= 2e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, rel_err, to_np
+from mogt_amd import synthetic
+from oracle import scan_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _fold(x):
+    """[B, L, D] -> [B*D, L, 1, 1] (the reference's per-feature mapping)."""
+    B, L, D = x.shape
+    return np.ascontiguousarray(np.transpose(x, (0, 2, 1)).reshape(B * D, L, 1, 1))
+
+
+def _unfold(x, B, D):
+    BD, L = x.shape[:2]
+    return np.transpose(x.reshape(B, D, L), (0, 2, 1))
+
+
+def _diag_oracle_grads(a, b, w):
+    B, L, D = a.shape
+    gU, gV = so.affine_scan_sequential_backward(_fold(a.astype(np.float64)), _fold(b.astype(np.float64)),
+                                                _fold(w.astype(np.float64)))
+    return _unfold(gU, B, D), _unfold(gV, B, D)
+
+
+@pytest.mark.parametrize("B,L,D", [(2, 300, 64), (1, 1, 8), (1, 2049, 768), (3, 77, 10)])
+def test_diag_scan_backward_fp32(gpu, B, L, D):
+    announce(f"diag backward fp32 B={B} L={L} D={D}")
+    import mogt_amd
+
+    a, b = synthetic.diag_inputs(B, L, D, seed=L + D)
+    w = np.random.default_rng(L).standard_normal((B, L, D)).astype(np.float32)
+    at = torch.from_numpy(a).to(gpu).requires_grad_()
+    bt = torch.from_numpy(b).to(gpu).requires_grad_()
+    h = mogt_amd.diag_scan(at, bt)
+    (h * torch.from_numpy(w).to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    da_ref, db_ref = _diag_oracle_grads(a, b, w)
+    assert rel_err(to_np(bt.grad), db_ref) <= FP32_TOL
+    assert rel_err(to_np(at.grad), da_ref) <= FP32_TOL
+
+
+def test_diag_scan_backward_bf16(gpu):
+    announce("diag backward bf16 B=1 L=1000 D=256")
+    import mogt_amd
+
+    a, b = synthetic.diag_inputs(1, 1000, 256, seed=5)
+    w = np.random.default_rng(6).standard_normal((1, 1000, 256)).astype(np.float32)
+    at = torch.from_numpy(a).to(gpu).bfloat16().requires_grad_()
+    bt = torch.from_numpy(b).to(gpu).bfloat16().requires_grad_()
+    h = mogt_amd.diag_scan(at, bt, out_dtype=torch.float32)
+    (h * torch.from_numpy(w).to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    assert at.grad.dtype == torch.bfloat16 and bt.grad.dtype == torch.bfloat16
+    da_ref, db_ref = _diag_oracle_grads(to_np(at.detach()), to_np(bt.detach()), w)
+    assert rel_err(to_np(bt.grad), db_ref) <= BF16_TOL
+    assert rel_err(to_np(at.grad), da_ref) <= BF16_TOL
+
+
+def test_diag_scan_backward_full_size(gpu):
+    """configs[1] shape (B=1, D=768, L=32768), fp32."""
+    announce("diag backward full size")
+    import mogt_amd
+
+    a, b = synthetic.cfg2_inputs(32768, seed=9)
+    w = np.random.default_rng(10).standard_normal(a.shape).astype(np.float32)
+    at = torch.from_numpy(a).to(gpu).requires_grad_()
+    bt = torch.from_numpy(b).to(gpu).requires_grad_()
+    h = mogt_amd.diag_scan(at, bt)
+    (h * torch.from_numpy(w).to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    da_ref, db_ref = _diag_oracle_grads(a, b, w)
+    assert rel_err(to_np(bt.grad), db_ref) <= FP32_TOL
+    assert rel_err(to_np(at.grad), da_ref) <= FP32_TOL
+
+
+def _coupled_ref(z, v, r, damping):
+    """float64 CPU restatement with autograd: g = sigmoid(z), a = damping (1 - g)
+    per rank, h_t = a_t h_{t-1} + v_t g_t (model_mogt.py:166-182, identity U)."""
+    B, L, D = v.shape
+    c = D // r
+    g = torch.sigmoid(z)
+    a = damping * (1.0 - g)
+    vv = v.view(B, L, r, c) * g.unsqueeze(-1)
+    h = torch.zeros(B, r, c, dtype=v.dtype)
+    out = []
+    for t in range(L):
+        h = a[:, t, :, None] * h + vv[:, t]
+        out.append(h)
+    return torch.stack(out, 1).reshape(B, L, D)
+
+
+@pytest.mark.parametrize("L,r,c,vdt", [(200, 4, 6, "fp32"), (513, 16, 48, "fp32"), (300, 16, 48, "bf16")])
+def test_coupled_scan_backward(gpu, L, r, c, vdt):
+    announce(f"coupled backward L={L} r={r} c={c} v={vdt}")
+    import mogt_amd
+
+    z, v = synthetic.coupled_inputs(1, L, r, c, seed=L + r)
+    w = np.random.default_rng(L).standard_normal((1, L, r * c)).astype(np.float32)
+    zt = torch.from_numpy(z).to(gpu).requires_grad_()
+    vt = torch.from_numpy(v).to(gpu)
+    if vdt == "bf16":
+        vt = vt.bfloat16()
+    vt.requires_grad_()
+    h = mogt_amd.coupled_rank_scan(zt, vt, damping=0.999)
+    (h * torch.from_numpy(w).to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+
+    z64 = torch.from_numpy(z).double().requires_grad_()
+    v64 = torch.from_numpy(to_np(vt.detach())).double().requires_grad_()
+    (_coupled_ref(z64, v64, r, 0.999) * torch.from_numpy(w).double()).sum().backward()
+    tol = FP32_TOL if vdt == "fp32" else BF16_TOL
+    assert vt.grad.dtype == vt.dtype
+    assert rel_err(to_np(vt.grad), v64.grad.numpy()) <= tol
+    assert rel_err(to_np(zt.grad), z64.grad.numpy()) <= tol
