@@ -158,6 +158,38 @@ def measure_diag_rev(torch, lib, ops, L, steps, warmup, D=768, B=1, sets=3):
     return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
 
 
+def measure_connection_map(torch, lib, ops, impl, n, r, steps, warmup):
+    """Batched transport maps of skew generators (model_mogt.py:79-102):
+    the HIP kernel via the C ABI, and torch's routine on the same inputs."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    T = torch.randn(n, r, r, generator=gen, device=dev) * 0.1
+    A = (T - T.transpose(-1, -2)).contiguous()
+    U = torch.empty_like(A)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    from mogt_amd import _lib as mlib
+
+    code = mlib.MOGT_CONN_EXP if impl == "matrix_exp" else mlib.MOGT_CONN_CAYLEY
+
+    def launch(i):
+        rc = lib.mogt_connection_map_fwd(A.data_ptr(), U.data_ptr(), n, r, 1.0, 1.0, code, 0, sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    eye = torch.eye(r, device=dev)
+
+    def launch_torch(i):
+        if impl == "matrix_exp":
+            torch.matrix_exp(A)
+        else:
+            torch.linalg.solve(eye - 0.5 * A, eye + 0.5 * A)
+
+    ms_torch = EventTimer(torch, stream).time(launch_torch, max(3, steps // 10), 2)
+    return {"ms": ms, "ms_torch": ms_torch}
+
+
 def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
     """Model-shaped coupled per-rank gate scan (config 2'): z fp32 [1,L,16],
     v bf16 [1,L,768] -> h fp32 [1,L,768]."""
@@ -475,6 +507,12 @@ def main():
             "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
             "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
                     "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
+        for impl in ("matrix_exp", "cayley"):
+            r = measure_connection_map(torch, lib, ops, impl, 32768, 16, args.steps, args.warmup)
+            extras[f"connection_map_{impl}_r16_n32768"] = {
+                "us": round(r["ms"] * 1e3, 2), "torch_us": round(r["ms_torch"] * 1e3, 2),
+                "note": "U = f(A) for 32768 skew 16x16 generators (one MOGT layer at L = 32768); "
+                        "torch_us: torch.matrix_exp / torch.linalg.solve on the same GPU inputs"}
         r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
         extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
             r, ffn_hidden=3072, vocab=32000,

@@ -183,6 +183,20 @@ int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float
 int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
                       void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Connection map of the transport, U = damping * f(scale * A) for a batch of
+ * skew-symmetric r x r generators A (fp32 [count, r, r], r <= 32), replacing
+ * MOGTBlock._build_transport (model_mogt.py:79-102):
+ *   impl MOGT_CONN_EXP:    f = matrix exponential (torch.matrix_exp, :83-85)
+ *   impl MOGT_CONN_CAYLEY: f(S) = (I - S/2)^{-1} (I + S/2)
+ *                          (torch.linalg.solve(I - A/2, I + A/2), :86-90)
+ * The reference passes A / r, i.e. scale = 1 / r.  U: [count, r, r] in
+ * out_dtype.  A must be skew-symmetric (the kernels rely on A^T = -A).      */
+#define MOGT_CONN_EXP 0
+#define MOGT_CONN_CAYLEY 1
+int mogt_connection_map_fwd(const void* A, void* U, int64_t count, int64_t rank, float scale,
+                            float damping, int impl, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

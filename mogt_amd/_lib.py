@@ -14,6 +14,8 @@ from . import _build
 
 MOGT_F32 = 0
 MOGT_BF16 = 1
+MOGT_CONN_EXP = 0
+MOGT_CONN_CAYLEY = 1
 ABI_VERSION = 2
 
 _c_void_p = ctypes.c_void_p
@@ -76,6 +78,8 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
          _c_int, _c_int, _c_void_p]),
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_connection_map_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
     "mogt_rank1_coupled_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "mogt_rank1_coupled_scan_fwd": (
         _c_int,

@@ -132,14 +132,12 @@ class MOGTBlock(nn.Module):
         """model_mogt.py:79-102."""
         A_fp32 = (A / self.r).to(torch.float32)
         impl = self._resolve_connection_impl()
-        if impl == "matrix_exp":
-            with torch.autograd.profiler.record_function("mogt.matrix_exp"):
-                U_fp32 = torch.matrix_exp(A_fp32)
-        elif impl == "cayley":
-            with torch.autograd.profiler.record_function("mogt.cayley_solve"):
-                eye = self._identity_r.view(1, 1, self.r, self.r)
-                half_A = 0.5 * A_fp32
-                U_fp32 = torch.linalg.solve(eye - half_A, eye + half_A)
+        if impl in ("matrix_exp", "cayley"):
+            # HIP connection-map kernel (A is skew: A_raw - A_raw^T); damping and
+            # the output cast are applied below exactly as in the reference
+            name = "mogt.matrix_exp" if impl == "matrix_exp" else "mogt.cayley_solve"
+            with torch.autograd.profiler.record_function(name):
+                U_fp32 = ops.connection_map(A_fp32, impl)
         elif impl == "identity":
             U_fp32 = self._identity_r.view(1, 1, self.r, self.r).expand(
                 A.shape[0], A.shape[1], self.r, self.r)

@@ -601,6 +601,79 @@ def silu_mul(y: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# connection map of the transport: U = damping * f(scale * A), A skew
+# ---------------------------------------------------------------------------
+_CONN_IMPL = {"matrix_exp": _lib.MOGT_CONN_EXP, "cayley": _lib.MOGT_CONN_CAYLEY}
+
+
+def _connection_map_reference(A: torch.Tensor, impl: int, scale: float, damping: float) -> torch.Tensor:
+    """The same map with torch's library routines (model_mogt.py:79-102); used
+    to differentiate the HIP forward."""
+    X = A.to(torch.float32) * scale
+    if impl == _lib.MOGT_CONN_EXP:
+        U = torch.matrix_exp(X)
+    else:
+        eye = torch.eye(A.shape[-1], dtype=X.dtype, device=X.device)
+        U = torch.linalg.solve(eye - 0.5 * X, eye + 0.5 * X)
+    return U * damping
+
+
+@torch.library.custom_op("mogt::connection_map", mutates_args=())
+def _connection_map_op(A: torch.Tensor, impl: int, scale: float, damping: float,
+                       out_dtype: torch.dtype) -> torch.Tensor:
+    lib = _lib.load()
+    A32 = A.to(torch.float32).contiguous()
+    r = A.shape[-1]
+    n = A32.numel() // (r * r) if r else 0
+    U = torch.empty(A.shape, dtype=out_dtype, device=A.device)
+    rc = lib.mogt_connection_map_fwd(A32.data_ptr(), U.data_ptr(), n, r, float(scale), float(damping),
+                                     int(impl), dtype_code(out_dtype, "connection_map"),
+                                     _stream_handle(A.device))
+    _lib.check(rc, "mogt_connection_map_fwd")
+    return U
+
+
+@_connection_map_op.register_fake
+def _(A, impl, scale, damping, out_dtype):
+    return A.new_empty(A.shape, dtype=out_dtype)
+
+
+def _connection_map_setup(ctx, inputs, output):
+    A, impl, scale, damping, _ = inputs
+    ctx.save_for_backward(A)
+    ctx.args = (impl, scale, damping)
+
+
+def _connection_map_backward(ctx, grad_u):
+    (A,) = ctx.saved_tensors
+    with torch.enable_grad():
+        Ad = A.detach().requires_grad_()
+        U = _connection_map_reference(Ad, *ctx.args)
+        (gA,) = torch.autograd.grad(U, Ad, grad_u.to(U.dtype))
+    return gA.to(A.dtype), None, None, None, None
+
+
+torch.library.register_autograd("mogt::connection_map", _connection_map_backward,
+                                setup_context=_connection_map_setup)
+
+
+def connection_map(A: torch.Tensor, impl: str, *, scale: float = 1.0, damping: float = 1.0,
+                   out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``U = damping * f(scale * A)`` for skew-symmetric ``A [..., r, r]`` (r <= 32)
+    with ``f`` = ``matrix_exp`` or ``cayley`` (``(I - S/2)^{-1} (I + S/2)``),
+    the transport maps of model_mogt.py:79-102, on the HIP kernels; gradients
+    come from torch's routines on the same inputs."""
+    require_cuda("connection_map", A)
+    if impl not in _CONN_IMPL:
+        raise ValueError(f"Unsupported connection_impl: {impl}")
+    if A.ndim < 2 or A.shape[-1] != A.shape[-2]:
+        raise ValueError("A must be [..., r, r]")
+    if A.shape[-1] > 32:
+        raise ValueError(f"r = {A.shape[-1]} not supported by the MI355X connection map (r <= 32)")
+    return torch.ops.mogt.connection_map(A, _CONN_IMPL[impl], float(scale), float(damping), out_dtype)
+
+
+# ---------------------------------------------------------------------------
 # rank-1 coupled write-forget scan with readout
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("mogt::rank1_coupled_scan", mutates_args=())
