@@ -74,14 +74,21 @@ __device__ __forceinline__ f32x16 zero16() {
     return z;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (shuffle-up scan).
+// Inclusive prefix sum over the 64 lanes of a wave on DPP lane moves (no LDS
+// round trips): shifts by 1, 2, 4, 8 inside each row of 16 lanes (lanes
+// shifted past the row start add 0), then each row adds the total of the rows
+// before it through row_bcast:15 (rows 1, 3) and row_bcast:31 (rows 2, 3).
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, BOUND_ZERO));
+}
 __device__ __forceinline__ float wave_incl_scan(float x) {
-    const int l = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(x, off, 64);
-        if (l >= off) x += y;
-    }
+    x += dpp_f32<0x111, 0xf, true>(x);   // row_shr:1
+    x += dpp_f32<0x112, 0xf, true>(x);   // row_shr:2
+    x += dpp_f32<0x114, 0xf, true>(x);   // row_shr:4
+    x += dpp_f32<0x118, 0xf, true>(x);   // row_shr:8
+    x += dpp_f32<0x142, 0xa, false>(x);  // row_bcast:15 into rows 1 and 3
+    x += dpp_f32<0x143, 0xc, false>(x);  // row_bcast:31 into rows 2 and 3
     return x;
 }
 
