@@ -33,6 +33,13 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
 ]
 
+# Per-file extras.  The rank-1 kernels rescale MFMA accumulators between
+# chains; keeping accumulators in ordinary VGPRs avoids a copy to and from the
+# accumulation registers around every such rescale.
+FILE_FLAGS = {
+    "rank1_scan.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -46,7 +53,7 @@ def lib_path() -> Path:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -51,14 +51,27 @@ struct Rank1Params {
     int H, nsc;
 };
 
-// 32x32 fp32 tile += A[32 x K] B[K x 32]; A rows in `a` (row stride sa, k contiguous),
-// B columns in `b` (column stride sb, k contiguous), both bf16 in LDS.
-__device__ __forceinline__ f32x16 mma32(const bf16_t* a, int sa, const bf16_t* b, int sb, int K,
+// Transposed tiles (rows d, 64 steps t per row, written by put_cols) hold
+// 16-byte chunk c of row d at chunk position c ^ (d / 8 % 8).  The transposed
+// 4-byte stores, whose lanes write rows 8 apart, then fall into distinct
+// banks, and an MFMA operand read (8 consecutive rows, one chunk each) stays
+// conflict-free through the row padding.
+__device__ __forceinline__ int tsw(int row) { return (row >> 3) & 7; }
+
+// 32x32 fp32 tile += A[32 x K] B[K x 32].  A is rows ar.. of tile `a` from
+// column ac, B the columns held as rows br.. of tile `b` from column bc (k
+// contiguous in both); SWA / SWB mark transposed (chunk-swizzled) tiles.
+template <bool SWA, bool SWB>
+__device__ __forceinline__ f32x16 mma32(const bf16_t* a, int ar, int ac, const bf16_t* b, int br, int bc, int K,
                                         f32x16 acc) {
-    const int l = threadIdx.x & 63;
+    const int l = threadIdx.x & 63, hb = l >> 5;
+    const int ra = ar + (l & 31), rb = br + (l & 31);
+    const int xa = SWA ? tsw(ra) : 0, xb = SWB ? tsw(rb) : 0;
+#pragma unroll
     for (int k0 = 0; k0 < K; k0 += 16) {
-        const bf16x8 av = *reinterpret_cast<const bf16x8*>(a + (l & 31) * sa + k0 + 8 * (l >> 5));
-        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(b + (l & 31) * sb + k0 + 8 * (l >> 5));
+        const int ca = (((ac + k0) >> 3) + hb) ^ xa, cb = (((bc + k0) >> 3) + hb) ^ xb;
+        const bf16x8 av = *reinterpret_cast<const bf16x8*>(a + ra * R1_SR + 8 * ca);
+        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(b + rb * R1_SR + 8 * cb);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
     }
     return acc;
@@ -96,37 +109,49 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
 // the row pair (2m, 2m + 1), m = e / 8, and segment sg = e % 8 of 8 consecutive
 // elements in both rows, so 8 consecutive lanes read one 128-byte row and a
 // transposed store writes both rows' elements of one column as one 4-byte
-// word.  Rows past L are read from row L - 1 (every load is unconditional, so
-// no wait is forced between them) and zeroed when the tile is staged into LDS.
+// word.  Tiles are read through a buffer descriptor whose range ends with the
+// sequence's row L - 1, so rows past L read as zeros; the per-lane offsets are
+// constant and the loads carry no address arithmetic.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 template <typename TI>
 struct Tile8 {
     static constexpr int NW = sizeof(TI) == 2 ? 1 : 2;   // 16-byte words per segment
     u32x4 x[2][NW];
-    bool ok[2];
 };
 
 __device__ __forceinline__ int tile_m() { return static_cast<int>(threadIdx.x) >> 3; }
 __device__ __forceinline__ int tile_sg() { return static_cast<int>(threadIdx.x) & 7; }
 
+// Descriptor over the rows t0 .. L - 1 of one (batch, head) sequence of a
+// [B, L, H, n] tensor with n elements of T per row (t0 < L).
+template <typename T>
+__device__ __forceinline__ auto seq_rsrc(const T* base, int64_t rowbase, int64_t t0, int64_t L, int H, int n) {
+    const int64_t strideB = static_cast<int64_t>(H) * n * sizeof(T);
+    const int64_t span = (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + t0 * H) * n, 0,
+                                             static_cast<int>(span < 0x7fffffff ? span : 0x7fffffff), 0x00020000);
+}
+
 template <typename TI>
 __device__ __forceinline__ Tile8<TI> load_tile(const TI* __restrict__ src, int64_t rowbase, int64_t t0,
                                                int64_t L, int H) {
+    const auto rs = seq_rsrc(src, rowbase, t0, L, H, R1_DH);
+    const int strideB = H * R1_DH * static_cast<int>(sizeof(TI));
     Tile8<TI> r;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int t = 2 * tile_m() + u;
-        r.ok[u] = t0 + t < L;
-        const int64_t row = r.ok[u] ? t0 + t : L - 1;
-        const u32x4* ptr = reinterpret_cast<const u32x4*>(src + (rowbase + row * H) * R1_DH + tile_sg() * 8);
+        const int off = (2 * tile_m() + u) * strideB + tile_sg() * 8 * static_cast<int>(sizeof(TI));
 #pragma unroll
-        for (int j = 0; j < Tile8<TI>::NW; ++j) r.x[u][j] = ptr[j];
+        for (int j = 0; j < Tile8<TI>::NW; ++j)
+            r.x[u][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * j, 0, 0));
     }
     return r;
 }
 
-// The 8 elements of row 2m + u as fp32 (zero past L).
+// The 8 elements of row 2m + u as fp32.
 template <typename TI>
 __device__ __forceinline__ void seg_f32(const Tile8<TI>& r, int u, float (&o)[8]) {
     if constexpr (sizeof(TI) == 2) {
@@ -141,15 +166,12 @@ __device__ __forceinline__ void seg_f32(const Tile8<TI>& r, int u, float (&o)[8]
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[4 * j + i] = __uint_as_float(r.x[u][j][i]);
     }
-    if (!r.ok[u]) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = 0.0f;
-    }
 }
 
-// Two fp32 values as one word of two bf16 (round to nearest even).
+// Two fp32 values as one word of two bf16 (round to nearest even): one
+// v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
 }
 
 // Tile into LDS row-major [t][d] (row stride R1_SR).
@@ -161,7 +183,6 @@ __device__ __forceinline__ void put_rows(const Tile8<TI>& r, bf16_t* dst) {
         u32x4 w;
         if constexpr (sizeof(TI) == 2) {
             w = r.x[u][0];
-            if (!r.ok[u]) w = u32x4{0u, 0u, 0u, 0u};
         } else {
             float o[8];
             seg_f32(r, u, o);
@@ -171,16 +192,31 @@ __device__ __forceinline__ void put_rows(const Tile8<TI>& r, bf16_t* dst) {
         *reinterpret_cast<u32x4*>(dst + t * R1_SR + tile_sg() * 8) = w;
     }
 }
-// Tile into LDS transposed [d][t], rows 2m and 2m + 1 scaled by s0 and s1.
-template <typename TI>
+// Tile into LDS transposed [d][t] with the chunk swizzle of tsw();
+// with SCALE, rows 2m and 2m + 1 are multiplied by s0 and s1.  Row d = 8 sg + i
+// of the transposed tile gets the word (t = 2m, 2m + 1) in chunk (m / 4) ^ sg.
+template <bool SCALE, typename TI>
 __device__ __forceinline__ void put_cols(const Tile8<TI>& r, bf16_t* dst, float s0 = 1.0f, float s1 = 1.0f) {
-    float a[8], b[8];
-    seg_f32(r, 0, a);
-    seg_f32(r, 1, b);
     const int m = tile_m(), sg = tile_sg();
+    bf16_t* base = dst + 8 * sg * R1_SR + 8 * ((m >> 2) ^ sg) + 2 * (m & 3);
+    uint32_t wd[8];
+    if constexpr (sizeof(TI) == 2 && !SCALE) {
+        // bf16 halves regrouped by byte permutes: element 2i is the low half of
+        // word i, element 2i + 1 the high half
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint32_t*>(dst + (sg * 8 + i) * R1_SR + 2 * m) = pack_bf16(a[i] * s0, b[i] * s1);
+        for (int i = 0; i < 4; ++i) {
+            wd[2 * i] = __builtin_amdgcn_perm(r.x[1][0][i], r.x[0][0][i], 0x05040100u);
+            wd[2 * i + 1] = __builtin_amdgcn_perm(r.x[1][0][i], r.x[0][0][i], 0x07060302u);
+        }
+    } else {
+        float a[8], b[8];
+        seg_f32(r, 0, a);
+        seg_f32(r, 1, b);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wd[i] = SCALE ? pack_bf16(a[i] * s0, b[i] * s1) : pack_bf16(a[i], b[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint32_t*>(base + i * R1_SR) = wd[i];
 }
 
 // Raw f of step t (row L - 1 past the end; see fval).
@@ -235,14 +271,14 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p
     f32x16 acc = zero16();
     for (int sub = 0; sub < R1_SUB; ++sub) {
         __syncthreads();   // previous sub-block's tiles consumed; sW visible
-        put_cols(kt, sKT);
-        put_cols(vt, sVT, sW[sub * R1_T + 2 * m], sW[sub * R1_T + 2 * m + 1]);   // V^T diag(w)
+        put_cols<false>(kt, sKT);
+        put_cols<true>(vt, sVT, sW[sub * R1_T + 2 * m], sW[sub * R1_T + 2 * m + 1]);   // V^T diag(w)
         if (sub + 1 < R1_SUB) {   // prefetch the next sub-block while this one multiplies
             kt = load_tile<TI>(kp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
             vt = load_tile<TI>(vp, rowbase, t0 + (sub + 1) * R1_T, p.L, p.H);
         }
         __syncthreads();
-        acc = mma32(sVT + ib * 32 * R1_SR, R1_SR, sKT + jb * 32 * R1_SR, R1_SR, R1_T, acc);
+        acc = mma32<true, true>(sVT, ib * 32, 0, sKT, jb * 32, 0, R1_T, acc);
     }
     float* out = p.dS + (static_cast<int64_t>(seq) * p.nsc + sc) * R1_DH * R1_DH;
     const int col = jb * 32 + (lane & 31);
@@ -379,8 +415,8 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
         // stage this sub-chunk
         put_rows(qt, sQ);
         put_rows(kt, sK);
-        put_cols(kt, sKTw, __shfl(wgt, 2 * m, 64), __shfl(wgt, 2 * m + 1, 64));
-        put_cols(vt, sVT);
+        put_cols<true>(kt, sKTw, __shfl(wgt, 2 * m, 64), __shfl(wgt, 2 * m + 1, 64));
+        put_cols<false>(vt, sVT);
         __syncthreads();
         if (sub + 1 < nsub) {   // next sub-chunk's operands, in flight while this one computes
             qt = load_tile<TI>(qp, rowbase, t0 + R1_T, p.L, p.H);
@@ -404,7 +440,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
         }
         // P quadrant (rows t_of, columns s_of = c_of), lower triangle only
         if (qc <= qa) {
-            f32x16 acc = mma32(sQ + t_of * R1_SR, R1_SR, sK + c_of * R1_SR, R1_SR, R1_DH, zero16());
+            f32x16 acc = mma32<false, false>(sQ, t_of, 0, sK, c_of, 0, R1_DH, zero16());
             const int s = c_of + (lane & 31);
             const float lcs = sLc[s], omf = sOmf[s];
 #pragma unroll
@@ -417,12 +453,13 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
         __syncthreads();
         // y quadrant (rows t_of, columns i = c_of): intra P V + decayed inter Q S^T
         {
-            f32x16 intra = zero16();
+            // decayed inter term first, then the intra products accumulate onto it
+            f32x16 acc = mma32<false, false>(sQ, t_of, 0, sShi, c_of, 0, R1_DH, zero16());
+            acc = mma32<false, false>(sQ, t_of, 0, sSlo, c_of, 0, R1_DH, acc);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] *= et[r];
             for (int sb = 0; sb <= qa; ++sb)
-                intra = mma32(sP + t_of * R1_SR + sb * 32, R1_SR, sVT + c_of * R1_SR + sb * 32, R1_SR, 32,
-                              intra);
-            f32x16 inter = mma32(sQ + t_of * R1_SR, R1_SR, sShi + c_of * R1_SR, R1_SR, R1_DH, zero16());
-            inter = mma32(sQ + t_of * R1_SR, R1_SR, sSlo + c_of * R1_SR, R1_SR, R1_DH, inter);
+                acc = mma32<false, true>(sP, t_of, sb * 32, sVT, c_of, sb * 32, 32, acc);
             // rows of this sub-chunk at or past L fall outside the range and are dropped
             const int64_t left = p.L - t0;   // >= 1
             const int64_t span = (left - 1) * rowStrideB + static_cast<int64_t>(R1_DH) * sizeof(TO);
@@ -433,7 +470,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int t = t_of + mrow(r);
-                const float val = intra[r] + et[r] * inter[r];
+                const float val = acc[r];
                 const int off = t * static_cast<int>(rowStrideB) + colB;
                 if constexpr (sizeof(TO) == 4)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), ry, off, 0, 0);
@@ -444,10 +481,10 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
         __syncthreads();   // sQ, sP and the old state halves are consumed
         // S^T <- 2^Lc_T S^T + K^T diag(w) V
         {
-            const f32x16 dST = mma32(sKTw + t_of * R1_SR, R1_SR, sVT + c_of * R1_SR, R1_SR, R1_T, zero16());
             const float dec = exp2_hw(lcT);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ST[r] = fmaf(dec, ST[r], dST[r]);
+            for (int r = 0; r < 16; ++r) ST[r] *= dec;
+            ST = mma32<true, true>(sKTw, t_of, 0, sVT, c_of, 0, R1_T, ST);
             put_state();
         }
         __syncthreads();   // tiles of this sub-chunk consumed before the next staging
