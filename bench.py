@@ -190,6 +190,89 @@ def measure_connection_map(torch, lib, ops, impl, n, r, steps, warmup):
     return {"ms": ms, "ms_torch": ms_torch}
 
 
+def _reference_chunked_ce_torch(torch, hidden, weight, labels, chunk):
+    """The reference's chunked tied-head CE (chunked_lm_loss.py:7-72) restated
+    with torch ops -- forward and backward -- for a same-GPU timing comparison:
+    per chunk an fp32 GEMM and F.cross_entropy, then softmax, one-hot update,
+    scale and the two gradient GEMMs."""
+    import torch.nn.functional as F
+
+    T, D = hidden.shape[0] * hidden.shape[1], hidden.shape[2]
+    hf = hidden.reshape(T, D)
+    lf = labels.reshape(T)
+    wf = weight.float()
+    loss = hidden.new_zeros((), dtype=torch.float32)
+    with torch.no_grad():
+        for s in range(0, T, chunk):
+            e = min(s + chunk, T)
+            loss = loss + F.cross_entropy(hf[s:e].float().matmul(wf.t()), lf[s:e], reduction="sum")
+        gh = torch.empty_like(hf)
+        gw = torch.zeros_like(weight, dtype=torch.float32)
+        scale = 1.0 / T
+        for s in range(0, T, chunk):
+            e = min(s + chunk, T)
+            hc = hf[s:e]
+            probs = torch.softmax(hc.float().matmul(wf.t()), dim=-1)
+            probs[torch.arange(e - s, device=hidden.device), lf[s:e]] -= 1.0
+            probs = probs * scale
+            gh[s:e] = probs.matmul(wf).to(hidden.dtype)
+            gw = gw + probs.t().matmul(hc.float())
+    return loss / T, gh, gw
+
+
+def measure_lm_ce(torch, lib, steps, warmup, rows=4096, vocab=32000, L=32768, D=768, chunk=4096):
+    """Chunked tied-head CE (chunked_lm_loss.py): the HIP cross-entropy rows on
+    one [rows, vocab] fp32 logits block (forward reads it once; backward reads
+    it and writes the gradient), and chunked_linear_cross_entropy forward +
+    backward at B=1, L, D, vocab against the reference's torch ops."""
+    from mogt_amd.chunked_lm_loss import chunked_linear_cross_entropy
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    x = torch.randn(rows, vocab, generator=gen, device=dev) * 4.0
+    g = torch.empty_like(x)
+    lab = torch.randint(0, vocab, (rows,), generator=gen, device=dev)
+    loss = torch.empty(rows, device=dev)
+    lse = torch.empty(rows, device=dev)
+    scale = torch.ones(1, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def fwd(i):
+        rc = lib.mogt_lm_ce_fwd(x.data_ptr(), vocab, 0, lab.data_ptr(), rows, vocab, -100, loss.data_ptr(),
+                                lse.data_ptr(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    def bwd(i):
+        rc = lib.mogt_lm_ce_bwd(x.data_ptr(), vocab, 0, lab.data_ptr(), lse.data_ptr(), rows, vocab, -100,
+                                scale.data_ptr(), g.data_ptr(), vocab, 0, sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    timer = EventTimer(torch, stream)
+    ms_f = timer.time(fwd, steps, warmup)
+    ms_b = timer.time(bwd, steps, warmup)
+    blk = rows * vocab * 4
+
+    h = (torch.randn(1, L, D, generator=gen, device=dev) * 0.5).bfloat16().requires_grad_()
+    w = (torch.randn(vocab, D, generator=gen, device=dev) * 0.02).requires_grad_()
+    labels = torch.randint(0, vocab, (1, L), generator=gen, device=dev)
+
+    def ours(i):
+        h.grad = None
+        w.grad = None
+        chunked_linear_cross_entropy(h, w, labels, chunk_size=chunk).backward()
+
+    def ref(i):
+        _reference_chunked_ce_torch(torch, h.detach(), w.detach(), labels, chunk)
+
+    ms_e2e = timer.time(ours, 3, 1)
+    ms_ref = timer.time(ref, 3, 1)
+    return {"fwd_ms": ms_f, "bwd_ms": ms_b, "fwd_gbs": blk / ms_f / 1e6, "bwd_gbs": 2 * blk / ms_b / 1e6,
+            "e2e_ms": ms_e2e, "ref_ms": ms_ref}
+
+
 def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
     """Model-shaped coupled per-rank gate scan (config 2'): z fp32 [1,L,16],
     v bf16 [1,L,768] -> h fp32 [1,L,768]."""
@@ -513,6 +596,19 @@ def main():
                 "us": round(r["ms"] * 1e3, 2), "torch_us": round(r["ms_torch"] * 1e3, 2),
                 "note": "U = f(A) for 32768 skew 16x16 generators (one MOGT layer at L = 32768); "
                         "torch_us: torch.matrix_exp / torch.linalg.solve on the same GPU inputs"}
+        r = measure_lm_ce(torch, lib, args.steps, args.warmup)
+        extras["lm_ce_rows_4096x32000_fp32"] = {
+            "fwd_us": round(r["fwd_ms"] * 1e3, 2), "fwd_GB/s": round(r["fwd_gbs"], 1),
+            "fwd_frac": round(r["fwd_gbs"] / HBM_PEAK_GBS, 4),
+            "bwd_us": round(r["bwd_ms"] * 1e3, 2), "bwd_GB/s": round(r["bwd_gbs"], 1),
+            "bwd_frac": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4),
+            "note": "cross-entropy rows of one logits block: forward reads it once (lse, loss), "
+                    "backward reads it and writes the softmax gradient"}
+        extras["chunked_linear_ce_L32768_d768_v32000_fwd_bwd_ms"] = {
+            "ms": round(r["e2e_ms"], 2), "reference_torch_ops_ms": round(r["ref_ms"], 2),
+            "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
+                    "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
+                    "torch ops on the same GPU"}
         r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
         extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
             r, ffn_hidden=3072, vocab=32000,

@@ -197,6 +197,29 @@ int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, in
 int mogt_connection_map_fwd(const void* A, void* U, int64_t count, int64_t rank, float scale,
                             float damping, int impl, int out_dtype, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Cross-entropy rows of the chunked tied-head loss, replacing the per-chunk
+ * F.cross_entropy of _ChunkedLinearCrossEntropy.forward and the softmax /
+ * one-hot / scale steps of its backward (chunked_lm_loss.py:29-35, 61-64).
+ * logits: [rows, vocab] with row stride `ld` elements (fp32 or bf16, the
+ * caller's GEMM output); labels: int64 [rows].
+ *
+ * mogt_lm_ce_fwd: lse_rows[r] = log sum_j exp(logits[r][j]) and
+ *   loss_rows[r] = lse_rows[r] - logits[r][labels[r]] (fp32).  A row whose
+ *   label equals ignore_index gets loss 0 (F.cross_entropy's ignore_index,
+ *   -100 by default); any other label outside [0, vocab) gets NaN.
+ * mogt_lm_ce_bwd: grad[r][j] = s * (exp(logits[r][j] - lse_rows[r]) -
+ *   [j == labels[r]]) with s = *scale (one fp32 in device memory: the
+ *   caller's grad_output / tokens, read by the kernel, so no host sync),
+ *   row stride ld_grad, fp32 or bf16; ignored rows are zero.  grad may be
+ *   the logits buffer itself (same dtype and stride).                      */
+int mogt_lm_ce_fwd(const void* logits, int64_t ld, int logits_dtype, const int64_t* labels,
+                   int64_t rows, int64_t vocab, int64_t ignore_index, float* loss_rows,
+                   float* lse_rows, void* stream);
+int mogt_lm_ce_bwd(const void* logits, int64_t ld, int logits_dtype, const int64_t* labels,
+                   const float* lse_rows, int64_t rows, int64_t vocab, int64_t ignore_index,
+                   const float* scale, void* grad, int64_t ld_grad, int grad_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -80,6 +80,12 @@ SIGNATURES: dict[str, tuple] = {
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "mogt_connection_map_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
+    "mogt_lm_ce_fwd": (
+        _c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_void_p,
+                 _c_void_p]),
+    "mogt_lm_ce_bwd": (
+        _c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p,
+                 _c_void_p, _c_i64, _c_int, _c_void_p]),
     "mogt_rank1_coupled_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "mogt_rank1_coupled_scan_fwd": (
         _c_int,

@@ -27,6 +27,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from . import ops, triton_scan
+from .chunked_lm_loss import chunked_linear_cross_entropy
 
 
 def _autocast_dtype() -> torch.dtype | None:
@@ -370,13 +371,49 @@ class MOGTForCausalLM(nn.Module):
         elif isinstance(module, nn.Embedding):
             torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
 
+    def _chunked_lm_loss(self, hidden_states, labels, loss_chunk_size: int, return_logits: bool):
+        """Chunked loss that keeps the logits (model_mogt.py:326-348): per chunk of
+        positions the LM head and a summed cross-entropy, divided by the token
+        count."""
+        vocab_size = self.lm_head.weight.size(0)
+        total_loss = hidden_states.new_zeros(())
+        total_tokens = 0
+        logits_chunks = [] if return_logits else None
+        for start in range(0, hidden_states.size(1), loss_chunk_size):
+            end = min(start + loss_chunk_size, hidden_states.size(1))
+            logits_chunk = self.lm_head(hidden_states[:, start:end, :])
+            labels_chunk = labels[:, start:end]
+            total_loss = total_loss + F.cross_entropy(logits_chunk.reshape(-1, vocab_size),
+                                                      labels_chunk.reshape(-1), reduction="sum")
+            total_tokens += labels_chunk.numel()
+            if return_logits:
+                logits_chunks.append(logits_chunk)
+        loss = total_loss / total_tokens
+        logits = torch.cat(logits_chunks, dim=1) if return_logits else None
+        return logits, loss
+
     def forward(self, input_ids, labels=None, *, return_logits=True, loss_chunk_size=0):
+        """model_mogt.py:350-380: with labels and ``loss_chunk_size > 0`` the loss
+        is chunked -- keeping the logits through the LM head, or, without
+        logits, through chunked_linear_cross_entropy (HIP cross-entropy rows)."""
         x = self.mogt(input_ids)
-        logits = self.lm_head(x)
+        logits = None
         loss = None
-        if labels is not None:
-            loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)).float(), labels.reshape(-1))
-        return (logits if return_logits else None), loss
+        loss_chunk_size = int(loss_chunk_size or 0)
+        with torch.autograd.profiler.record_function("mogt.lm_head_loss"):
+            if labels is not None and loss_chunk_size > 0:
+                if return_logits:
+                    logits, loss = self._chunked_lm_loss(x, labels, loss_chunk_size, True)
+                else:
+                    loss = chunked_linear_cross_entropy(x, self.lm_head.weight, labels,
+                                                        chunk_size=loss_chunk_size)
+            else:
+                logits = self.lm_head(x)
+                if labels is not None:
+                    loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)).float(), labels.reshape(-1))
+                if not return_logits:
+                    logits = None
+        return logits, loss
 
 
 def configure_coupled_gate(model: nn.Module, *, scan_impl: str = "triton_hybrid",

@@ -715,3 +715,77 @@ def rank1_coupled_scan(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: tor
     if k.shape[-1] != 64:
         raise ValueError(f"head dim {k.shape[-1]} not supported (64)")
     return torch.ops.mogt.rank1_coupled_scan(f, k, v, q, out_dtype or q.dtype)
+
+
+# ---------------------------------------------------------------------------
+# cross-entropy rows of the chunked tied-head loss (chunked_lm_loss.py:5-80)
+# ---------------------------------------------------------------------------
+def _check_ce_rows(logits: torch.Tensor, labels: torch.Tensor, what: str) -> None:
+    require_cuda(what, logits, labels)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError(f"{what}: logits must be [rows, vocab] with contiguous rows")
+    if labels.dim() != 1 or labels.shape[0] != logits.shape[0] or labels.dtype != torch.int64:
+        raise ValueError(f"{what}: labels must be int64 [rows]")
+    dtype_code(logits.dtype, what)
+
+
+@torch.library.custom_op("mogt::lm_ce_fwd", mutates_args=())
+def _lm_ce_fwd_op(logits: torch.Tensor, labels: torch.Tensor,
+                  ignore_index: int) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    labels = labels.contiguous()
+    rows, vocab = logits.shape
+    loss = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    lse = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    rc = lib.mogt_lm_ce_fwd(logits.data_ptr(), logits.stride(0), dtype_code(logits.dtype, "lm_ce_fwd"),
+                            labels.data_ptr(), rows, vocab, int(ignore_index), loss.data_ptr(),
+                            lse.data_ptr(), _stream_handle(logits.device))
+    _lib.check(rc, "mogt_lm_ce_fwd")
+    return loss, lse
+
+
+@_lm_ce_fwd_op.register_fake
+def _(logits, labels, ignore_index):
+    rows = logits.shape[0]
+    return logits.new_empty(rows, dtype=torch.float32), logits.new_empty(rows, dtype=torch.float32)
+
+
+def lm_ce_forward(logits: torch.Tensor, labels: torch.Tensor, *, ignore_index: int = -100):
+    """Per-row cross-entropy of a logits block: ``(loss_rows, lse_rows)``, both
+    fp32 [rows]; ``loss = logsumexp(logits) - logits[label]`` (0 where the label
+    is ``ignore_index``), as F.cross_entropy(..., reduction="none")."""
+    _check_ce_rows(logits, labels, "lm_ce_forward")
+    return torch.ops.mogt.lm_ce_fwd(logits, labels, int(ignore_index))
+
+
+@torch.library.custom_op("mogt::lm_ce_bwd_", mutates_args=("logits",))
+def _lm_ce_bwd_op(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor, scale: torch.Tensor,
+                  ignore_index: int) -> None:
+    lib = _lib.load()
+    labels = labels.contiguous()
+    lse = lse.contiguous()
+    rows, vocab = logits.shape
+    code = dtype_code(logits.dtype, "lm_ce_bwd")
+    rc = lib.mogt_lm_ce_bwd(logits.data_ptr(), logits.stride(0), code, labels.data_ptr(), lse.data_ptr(),
+                            rows, vocab, int(ignore_index), scale.data_ptr(), logits.data_ptr(),
+                            logits.stride(0), code, _stream_handle(logits.device))
+    _lib.check(rc, "mogt_lm_ce_bwd")
+
+
+@_lm_ce_bwd_op.register_fake
+def _(logits, labels, lse, scale, ignore_index):
+    return None
+
+
+def lm_ce_backward_(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor,
+                    scale: torch.Tensor, *, ignore_index: int = -100) -> torch.Tensor:
+    """Overwrite a logits block with ``scale * (softmax(logits) - onehot(labels))``
+    (zero rows where the label is ``ignore_index``); ``scale`` is a one-element
+    fp32 device tensor (``grad_output / tokens``), read by the kernel."""
+    _check_ce_rows(logits, labels, "lm_ce_backward_")
+    if lse.shape != labels.shape or lse.dtype != torch.float32:
+        raise ValueError("lm_ce_backward_: lse must be float32 [rows]")
+    if scale.numel() != 1 or scale.dtype != torch.float32 or scale.device != logits.device:
+        raise ValueError("lm_ce_backward_: scale must be a one-element float32 tensor on the logits' device")
+    torch.ops.mogt.lm_ce_bwd_(logits, labels, lse, scale.reshape(1).contiguous(), int(ignore_index))
+    return logits

@@ -59,6 +59,14 @@ def test_argument_errors_without_device(lib):
     assert rc == -1
     # zero-size problems are a no-op success
     assert lib.mogt_diag_scan_fwd(None, None, None, None, 0, 8, 8, 0, 0, None, 0, None) == 0
+    # cross-entropy rows: stride shorter than the vocabulary, bad dtype, in place
+    # with a different stride; zero rows are a no-op
+    rc = lib.mogt_lm_ce_fwd(1, 10, 0, 1, 4, 32, -100, 1, 1, None)
+    assert rc == -1 and b"stride" in lib.mogt_last_error()
+    assert lib.mogt_lm_ce_fwd(1, 32, 5, 1, 4, 32, -100, 1, 1, None) == -1
+    rc = lib.mogt_lm_ce_bwd(8, 32, 0, 1, 1, 4, 32, -100, 1, 8, 40, 0, None)
+    assert rc == -1 and b"in place" in lib.mogt_last_error()
+    assert lib.mogt_lm_ce_fwd(None, 32, 0, None, 0, 32, -100, None, None, None) == 0
 
 
 def test_tile_lists(lib):

@@ -311,3 +311,77 @@ def test_planted_mistakes_are_caught():
         return out
 
     assert rel_err(fold_wrong_order(U, V), ref) > 1e-3
+
+
+# --------------------------------------------------------------------------- chunked tied-head CE
+def _ce_case(seed, rows=37, vocab=53, ignore_every=0):
+    g = synthetic.rng(seed)
+    x = g.standard_normal((rows, vocab)) * 3.0
+    lab = g.integers(0, vocab, size=rows)
+    if ignore_every:
+        lab[::ignore_every] = -100
+    return x, lab
+
+
+def test_ce_rows_match_torch_cross_entropy():
+    from oracle import lm_loss_oracle as lo
+    import torch.nn.functional as F
+
+    for ignore_every in (0, 4):
+        x, lab = _ce_case(31, ignore_every=ignore_every)
+        loss, lse = lo.ce_rows(x, lab)
+        xt = torch.from_numpy(x)
+        ref = F.cross_entropy(xt, torch.from_numpy(lab), reduction="none").numpy()
+        assert rel_err(loss, ref) <= 1e-12
+        assert rel_err(lse, torch.logsumexp(xt, dim=1).numpy()) <= 1e-12
+        # a per-row constant shift leaves the loss unchanged and moves lse with it
+        loss2, lse2 = lo.ce_rows(x + 1000.0, lab)
+        assert rel_err(loss2, loss) <= 1e-9 and rel_err(lse2 - 1000.0, lse) <= 1e-9
+
+
+def test_ce_rows_grad_matches_autograd():
+    from oracle import lm_loss_oracle as lo
+    import torch.nn.functional as F
+
+    x, lab = _ce_case(32, ignore_every=5)
+    xt = torch.from_numpy(x).requires_grad_()
+    (F.cross_entropy(xt, torch.from_numpy(lab), reduction="sum") * 0.37).backward()
+    assert rel_err(lo.ce_rows_grad(x, lab, 0.37), xt.grad.numpy()) <= 1e-12
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 1000])
+def test_chunked_linear_ce_matches_unchunked_autograd(chunk):
+    from oracle import lm_loss_oracle as lo
+    import torch.nn.functional as F
+
+    g = synthetic.rng(33)
+    B, L, D, V = 2, 9, 12, 29
+    h = g.standard_normal((B, L, D))
+    w = g.standard_normal((V, D)) * 0.5
+    lab = g.integers(0, V, size=(B, L))
+    lab[0, 3] = -100
+    loss, gh, gw = lo.chunked_linear_ce(h, w, lab, chunk, grad_output=1.7)
+    ht = torch.from_numpy(h).requires_grad_()
+    wt = torch.from_numpy(w).requires_grad_()
+    ref = F.cross_entropy((ht @ wt.t()).reshape(-1, V), torch.from_numpy(lab).reshape(-1),
+                          reduction="sum") / (B * L)
+    (ref * 1.7).backward()
+    assert abs(loss - float(ref.detach())) <= 1e-12 * abs(float(ref.detach()))
+    assert rel_err(gh, ht.grad.numpy()) <= 1e-12
+    assert rel_err(gw, wt.grad.numpy()) <= 1e-12
+
+
+def test_ce_planted_mistakes_are_caught():
+    """Plausible slips in the CE restatement fail the library pins."""
+    import torch.nn.functional as F
+
+    x, lab = _ce_case(34)
+    ref = F.cross_entropy(torch.from_numpy(x), torch.from_numpy(lab), reduction="none").numpy()
+    no_max = np.log(np.exp(x).sum(1)) - x[np.arange(len(lab)), lab]   # fine in float64 ...
+    assert rel_err(no_max, ref) <= 1e-9                                 # ... so the shift test matters:
+    big = x + 1000.0
+    with np.errstate(over="ignore", invalid="ignore"):
+        no_max_big = np.log(np.exp(big).sum(1)) - big[np.arange(len(lab)), lab]
+    assert not np.all(np.isfinite(no_max_big))
+    wrong_pick = np.log(np.exp(x).sum(1)) - x[np.arange(len(lab)), (lab + 1) % x.shape[1]]
+    assert rel_err(wrong_pick, ref) > 1e-2
