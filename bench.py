@@ -440,6 +440,57 @@ def measure_backbone(torch, layers, ffn_hidden, vocab, L, iters, warmup):
             "params": params}
 
 
+def measure_backbone_train(torch, layers, ffn_hidden, vocab, L, iters, warmup, fused=True):
+    """One training step of the backbone (forward + backward of a mean-square
+    loss on its output, bf16 autocast, no optimizer): through the fused block
+    path (every kernel with its backward) or forced onto the generic op-by-op
+    path, same weights and inputs."""
+    from mogt_amd.model_mogt import MOGTBlock, MOGTModel, configure_coupled_gate
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = MOGTModel(vocab_size=vocab, d_model=768, num_layers=layers, r=16,
+                      ffn_hidden=ffn_hidden).to(dev)
+    configure_coupled_gate(model, zero_gate_weight=False)
+    with torch.no_grad():
+        for name, prm in model.named_parameters():
+            if "norm" not in name and not name.endswith("bias"):
+                prm.normal_(0.0, 0.02)
+    model.train()
+    ids = torch.randint(0, vocab, (1, L), device=dev)
+    orig = MOGTBlock.fused_path_ok
+    if not fused:
+        MOGTBlock.fused_path_ok = lambda self: False
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = model(ids)
+        loss = out.float().pow(2).mean()
+        loss.backward()
+        return loss
+
+    try:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(iters):
+            loss = step()
+        end.record()
+        torch.cuda.synchronize()
+    finally:
+        MOGTBlock.fused_path_ok = orig
+    ms = start.elapsed_time(end) / iters
+    assert torch.isfinite(loss)
+    del model
+    return {"ms": round(ms, 3), "tokens_per_s": round(L * 1000.0 / ms),
+            "peak_mem_mb": round(torch.cuda.max_memory_allocated(dev) / 2**20, 1)}
+
+
 def cpu_baseline(L=32768, D=768):
     """Reference CPU PyTorch scan (sequential bmm loop, fp32 state) on the folded
     R=C=1 workload, on this host's cores."""
@@ -617,6 +668,12 @@ def main():
         extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
             r, ffn_hidden=2048, vocab=4096,
             note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
+        rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 2, fused=True)
+        rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 2, fused=False)
+        extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(
+            rf, generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
+            note="forward + backward (mean-square loss on the backbone output, no optimizer), "
+                 "bf16 autocast; fused block path vs the generic op-by-op path on the same weights")
         log(f"extras: {json.dumps(extras)}")
 
     cpu = None

@@ -100,6 +100,16 @@ int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                float damping, int z_dtype, int v_dtype, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
+/* Gradient epilogue of the coupled scan's backward (the autograd of the
+ * fused gate + scan; the reference differentiates model_mogt.py:166-203
+ * through torch ops): given G (fp32 [B, L, R*C], the reverse scan
+ * G_t = dH_t + a_{t+1} G_{t+1}), the gate logits z (fp32 [B, L, R]), v and
+ * the forward output h (fp32), writes dv = G * round(sigmoid(z)) in v's dtype
+ * and dz = g (1 - g) (sum_c G v - damping sum_c G h_{t-1}) (fp32 [B, L, R]).
+ * channels must be a multiple of 4 and rank * channels <= 4096.            */
+int mogt_coupled_rank_scan_grad(const void* G, const float* z, const void* v, const float* h, void* dv,
+                                float* dz, int64_t batch, int64_t length, int64_t rank,
+                                int64_t channels, float damping, int v_dtype, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Dense affine scan  H_t = U_t H_{t-1} + V_t,  H_0 = 0  (R <= 32, any C).
@@ -182,6 +192,23 @@ int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float
                          int z_dtype, int out_dtype, void* stream);
 int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
                       void* stream);
+
+/* Backward of the row kernels (the autograd of RMSNorm and SwiGLU,
+ * model_mogt.py:15-20, 29-30, as torch differentiates the reference's
+ * expressions).
+ * mogt_rmsnorm_bwd: dx = r (dy*w - n mean(dy*w*n)) [+ dres], n = x r,
+ *   r = rsqrt(mean(x^2) + eps); dx has x's dtype, dy fp32 or bf16; dres
+ *   (fp32 [rows, dim], may be null) is the residual stream's own gradient of
+ *   add_rmsnorm (x fp32).  dw_partial: fp32 [ceil(rows / rows_per_wave), dim]
+ *   partial sums of dy * n.type_as(x); the caller sums them over rows.
+ * mogt_silu_mul_bwd: y = [rows, 2*hidden] (forward input), dout = [rows,
+ *   hidden]; dy = [rows, 2*hidden] = [dout*b*silu'(a) | dout*silu(a)],
+ *   rounded where torch's bf16 autograd rounds.                            */
+int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const float* dres, void* dx,
+                     float* dw_partial, int64_t rows, int64_t dim, float eps, int rows_per_wave,
+                     int x_dtype, int dy_dtype, void* stream);
+int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, int64_t hidden,
+                      int dtype, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Connection map of the transport, U = damping * f(scale * A) for a batch of

@@ -50,6 +50,9 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int,
          _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_coupled_rank_scan_grad": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
+                 _c_i64, _c_float, _c_int, _c_void_p]),
     "mogt_affine_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "mogt_affine_scan_fwd": (
         _c_int,
@@ -78,6 +81,10 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
          _c_int, _c_int, _c_void_p]),
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_rmsnorm_bwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
+                 _c_int, _c_int, _c_int, _c_void_p]),
+    "mogt_silu_mul_bwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "mogt_connection_map_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
     "mogt_lm_ce_fwd": (

@@ -111,3 +111,99 @@ extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
     return coupled_run(z, v, h, batch, length, rank, channels, damping, z_dtype, v_dtype, out_dtype,
                        t, workspace, workspace_bytes, stream);
 }
+
+// ---------------------------------------------------------------------------
+// Gradient epilogue of the coupled scan (the backward of
+// mogt_coupled_rank_scan_fwd, after the reverse scan has produced
+// G_t = dH_t + a_{t+1} G_{t+1}).  Per (b, t, i) with g = sigmoid(z[b,t,i]) and
+// g_io = g rounded to v's dtype (the gate as multiplied into v):
+//   dv[b,t,i,c] = G[b,t,i,c] * g_io                                  (v's dtype)
+//   dz[b,t,i]   = g (1 - g) (sum_c G v - damping sum_c G h[b,t-1])   (fp32)
+// since h_t = damping (1 - g_t) h_{t-1} + round(v_t g_t) and the rounding passes
+// gradients through, as a dtype cast does under autograd.  A work-group walks
+// CG_ROWS rows (b, t); per row, thread f covers features 4f .. 4f + 3 (coalesced
+// 16-byte fp32 / 8-byte bf16 vectors), writes dv and leaves its two partial
+// dot products in LDS, and thread i then sums rank i's C / 4 partials.
+// ---------------------------------------------------------------------------
+namespace mogt {
+
+constexpr int CG_THREADS = 256;
+constexpr int CG_ROWS = 8;
+constexpr int CG_MAX_VEC = 1024;   // D <= 4096
+
+template <typename TV>
+__global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* __restrict__ G,
+                                                                  const float* __restrict__ z,
+                                                                  const TV* __restrict__ v,
+                                                                  const float* __restrict__ h,
+                                                                  TV* __restrict__ dv, float* __restrict__ dz,
+                                                                  int64_t nrows, int64_t L, int R, int C,
+                                                                  float damping) {
+    __shared__ float s_v[CG_MAX_VEC], s_h[CG_MAX_VEC];
+    const int tid = threadIdx.x;
+    const int D = R * C, nvec = D / 4, vpr = C / 4;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.x) * CG_ROWS;
+    const int64_t r1 = r0 + CG_ROWS < nrows ? r0 + CG_ROWS : nrows;
+    for (int64_t row = r0; row < r1; ++row) {
+        const bool has_prev = row % L != 0;
+        const int64_t base = row * D;
+        for (int f = tid; f < nvec; f += CG_THREADS) {
+            const int i = f / vpr;
+            const float g_io = IO<TV>::ld(IO<TV>::st(sigmoidf_(z[row * R + i])));
+            float gv[4], vv[4], hv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o[4];
+            load_vec<float, 4>(G + base + 4 * f, gv);
+            load_vec<TV, 4>(v + base + 4 * f, vv);
+            if (has_prev) load_vec<float, 4>(h + base - D + 4 * f, hv);
+            float sv = 0.0f, sh = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sv = fmaf(gv[e], vv[e], sv);
+                sh = fmaf(gv[e], hv[e], sh);
+                o[e] = gv[e] * g_io;
+            }
+            store_vec<TV, 4>(dv + base + 4 * f, o);
+            s_v[f] = sv;
+            s_h[f] = sh;
+        }
+        __syncthreads();
+        for (int i = tid; i < R; i += CG_THREADS) {
+            float sv = 0.0f, sh = 0.0f;
+            for (int k = i * vpr; k < (i + 1) * vpr; ++k) {
+                sv += s_v[k];
+                sh += s_h[k];
+            }
+            const float gg = sigmoidf_(z[row * R + i]);
+            dz[row * R + i] = (sv - damping * sh) * gg * (1.0f - gg);
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace mogt
+
+extern "C" int mogt_coupled_rank_scan_grad(const void* G, const float* z, const void* v, const float* h, void* dv,
+                                           float* dz, int64_t batch, int64_t length, int64_t rank,
+                                           int64_t channels, float damping, int v_dtype, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || channels % 4 != 0 || rank * channels > 4 * CG_MAX_VEC)
+        return set_error(MOGT_E_INVALID,
+                         "coupled grad: channels a positive multiple of 4 and rank * channels <= 4096");
+    if (!dtype_ok(v_dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!G || !z || !v || !h || !dv || !dz) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    const int64_t nrows = batch * length;
+    const int64_t blocks = (nrows + CG_ROWS - 1) / CG_ROWS;
+    if (blocks > 0x7fffffffLL) return set_error(MOGT_E_INVALID, "coupled grad: problem too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int R = static_cast<int>(rank), C = static_cast<int>(channels);
+    if (v_dtype == MOGT_F32)
+        hipLaunchKernelGGL((coupled_grad_kernel<float>), dim3(static_cast<unsigned>(blocks)), dim3(CG_THREADS), 0, st,
+                           static_cast<const float*>(G), z, static_cast<const float*>(v), h,
+                           static_cast<float*>(dv), dz, nrows, length, R, C, damping);
+    else
+        hipLaunchKernelGGL((coupled_grad_kernel<bf16_t>), dim3(static_cast<unsigned>(blocks)), dim3(CG_THREADS), 0,
+                           st, static_cast<const float*>(G), z, static_cast<const bf16_t*>(v), h,
+                           static_cast<bf16_t*>(dv), dz, nrows, length, R, C, damping);
+    return check_launch("coupled_grad_kernel");
+}

@@ -91,9 +91,142 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ y, 
     }
 }
 
+// Backward of rmsnorm / add_rmsnorm (model_mogt.py:15-20).  With r =
+// rsqrt(mean(x^2) + eps), n = x r, n_t = n rounded to x's dtype (the
+// .type_as(x); a no-op for the fp32 residual of add_rmsnorm) and y = n_t w:
+//   dw = sum over rows of dy n_t
+//   dx = r (dn - n mean(dn n)) + dres,   dn = dy w
+// (the rounding of n_t passes the gradient straight through, as autograd of
+// the reference's expression does).  One wave per group of rows_per_wave rows:
+// each lane keeps its columns' dw sums in registers and the wave writes one
+// partial row, which the caller sums; dres (the residual stream's own
+// gradient, add_rmsnorm) may be null.
+template <typename TX, typename TG, int VPL>
+__global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
+    const TX* __restrict__ x, const float* __restrict__ w, const TG* __restrict__ dy,
+    const float* __restrict__ dres, TX* __restrict__ dx, float* __restrict__ dw_part, int64_t rows, int D,
+    float eps, int rows_per_wave) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * NA_WAVES + (threadIdx.x >> 6);
+    const int64_t r0 = gw * rows_per_wave;
+    if (r0 >= rows) return;
+    const int64_t r1 = r0 + rows_per_wave < rows ? r0 + rows_per_wave : rows;
+    float ww[VPL][4], acc[VPL][4];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int c = (k * 64 + lane) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ww[k][e] = acc[k][e] = 0.0f;
+        if (c < D) load_vec<float, 4>(w + c, ww[k]);
+    }
+    const float inv_d = 1.0f / static_cast<float>(D);
+    for (int64_t row = r0; row < r1; ++row) {
+        float v[VPL][4], g[VPL][4];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const int c = (k * 64 + lane) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[k][e] = g[k][e] = 0.0f;
+            if (c < D) {
+                load_vec<TX, 4>(x + row * D + c, v[k]);
+                load_vec<TG, 4>(dy + row * D + c, g[k]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+        }
+        const float r = rsqrtf(wave_sum(ss) * inv_d + eps);
+        float dot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float n = v[k][e] * r;
+                acc[k][e] = fmaf(g[k][e], rnd<TX>(n), acc[k][e]);
+                g[k][e] *= ww[k][e];   // dn
+                dot = fmaf(g[k][e], n, dot);
+            }
+        const float mdot = wave_sum(dot) * inv_d;
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const int c = (k * 64 + lane) * 4;
+            if (c < D) {
+                float o[4], rr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (dres) load_vec<float, 4>(dres + row * D + c, rr);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = r * (g[k][e] - v[k][e] * r * mdot) + rr[e];
+                store_vec<TX, 4>(dx + row * D + c, o);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int c = (k * 64 + lane) * 4;
+        if (c < D) store_vec<float, 4>(dw_part + gw * D + c, acc[k]);
+    }
+}
+
+// Backward of silu_mul: with a = y[:, :H], b = y[:, H:], s = silu(a) rounded to
+// the tensor dtype (as in the forward), out = s b:
+//   db = d s,   ds = d b,   da = ds sigmoid(a) (1 + a (1 - sigmoid(a)))
+// each rounded to the dtype where torch's bf16 autograd rounds (mul backward,
+// then silu_backward in fp32 and cast).  dy = [da | db], the gradient of the
+// fused [w1; w2] projection's output.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_bwd_kernel(const T* __restrict__ y, const T* __restrict__ dout,
+                                                           T* __restrict__ dy, int64_t rows, int64_t H) {
+    const int64_t nvec = rows * H / 4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t e = i * 4;
+        const int64_t r = e / H;
+        const int64_t c = e - r * H;
+        float a[4], b[4], d[4], da[4], db[4];
+        load_vec<T, 4>(y + r * 2 * H + c, a);
+        load_vec<T, 4>(y + r * 2 * H + H + c, b);
+        load_vec<T, 4>(dout + r * H + c, d);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float sg = 1.0f / (1.0f + expf(-a[k]));
+            const float s = rnd<T>(a[k] / (1.0f + expf(-a[k])));
+            db[k] = d[k] * s;
+            const float ds = rnd<T>(d[k] * b[k]);
+            da[k] = ds * sg * (1.0f + a[k] * (1.0f - sg));
+        }
+        store_vec<T, 4>(dy + r * 2 * H + c, da);
+        store_vec<T, 4>(dy + r * 2 * H + H + c, db);
+    }
+}
+
 namespace {
 
 bool dt_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
+
+template <typename TX, typename TG>
+int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* dres, void* dx, float* dw_part,
+                    int64_t rows, int D, float eps, int rpw, hipStream_t st) {
+    const int vpl = (D + 255) / 256;
+    const int64_t waves = (rows + rpw - 1) / rpw;
+    const dim3 grid(static_cast<unsigned>((waves + NA_WAVES - 1) / NA_WAVES));
+    const dim3 block(64 * NA_WAVES);
+    const TX* xp = static_cast<const TX*>(x);
+    const TG* gp = static_cast<const TG*>(dy);
+    TX* dxp = static_cast<TX*>(dx);
+#define MOGT_NORM_BWD_CASE(V)                                                                     \
+    if (vpl <= V) {                                                                                \
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<TX, TG, V>), grid, block, 0, st, xp, w, gp, dres, dxp, \
+                           dw_part, rows, D, eps, rpw);                                             \
+        return check_launch("rmsnorm_bwd_kernel");                                                 \
+    }
+    MOGT_NORM_BWD_CASE(1)
+    MOGT_NORM_BWD_CASE(2)
+    MOGT_NORM_BWD_CASE(3)
+    MOGT_NORM_BWD_CASE(4)
+    MOGT_NORM_BWD_CASE(8)
+    MOGT_NORM_BWD_CASE(16)
+#undef MOGT_NORM_BWD_CASE
+    return set_error(MOGT_E_INVALID, "rmsnorm_bwd: row length %d > 4096", D);
+}
 
 template <typename TX, typename TZ, typename TO, bool ADD>
 int launch_norm(const void* x, const void* z, float scale, const float* w, float* x_out, void* out,
@@ -189,4 +322,48 @@ extern "C" int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t
         hipLaunchKernelGGL((silu_mul_kernel<bf16_t>), dim3(grid), dim3(256), 0, st,
                            static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), rows, hidden);
     return check_launch("silu_mul_kernel");
+}
+
+extern "C" int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const float* dres, void* dx,
+                                float* dw_partial, int64_t rows, int64_t dim, float eps, int rows_per_wave,
+                                int x_dtype, int dy_dtype, void* stream) {
+    clear_error();
+    int rc = check_norm_args(rows, dim);
+    if (rc) return rc;
+    if (!dt_ok(x_dtype) || !dt_ok(dy_dtype)) return set_error(MOGT_E_INVALID, "rmsnorm_bwd: dtype");
+    if (rows_per_wave <= 0) return set_error(MOGT_E_INVALID, "rmsnorm_bwd: rows_per_wave must be positive");
+    if (dres && x_dtype != MOGT_F32)
+        return set_error(MOGT_E_INVALID, "rmsnorm_bwd: a residual gradient needs the fp32 residual stream");
+    if (rows == 0) return MOGT_OK;
+    if (!x || !weight || !dy || !dx || !dw_partial) return set_error(MOGT_E_INVALID, "rmsnorm_bwd: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int D = static_cast<int>(dim);
+    if (x_dtype == MOGT_F32 && dy_dtype == MOGT_F32)
+        return launch_norm_bwd<float, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+    if (x_dtype == MOGT_F32)
+        return launch_norm_bwd<float, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+    if (dy_dtype == MOGT_F32)
+        return launch_norm_bwd<bf16_t, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+    return launch_norm_bwd<bf16_t, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+}
+
+extern "C" int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, int64_t hidden,
+                                 int dtype, void* stream) {
+    clear_error();
+    if (rows < 0 || hidden <= 0 || hidden % 4 != 0)
+        return set_error(MOGT_E_INVALID, "silu_mul_bwd: hidden must be a positive multiple of 4");
+    if (!dt_ok(dtype)) return set_error(MOGT_E_INVALID, "silu_mul_bwd: dtype");
+    if (rows == 0) return MOGT_OK;
+    if (!y || !dout || !dy) return set_error(MOGT_E_INVALID, "silu_mul_bwd: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t nvec = rows * hidden / 4;
+    const unsigned grid = static_cast<unsigned>(nvec / 256 + 1 < 8192 ? nvec / 256 + 1 : 8192);
+    if (dtype == MOGT_F32)
+        hipLaunchKernelGGL((silu_mul_bwd_kernel<float>), dim3(grid), dim3(256), 0, st, static_cast<const float*>(y),
+                           static_cast<const float*>(dout), static_cast<float*>(dy), rows, hidden);
+    else
+        hipLaunchKernelGGL((silu_mul_bwd_kernel<bf16_t>), dim3(grid), dim3(256), 0, st,
+                           static_cast<const bf16_t*>(y), static_cast<const bf16_t*>(dout),
+                           static_cast<bf16_t*>(dy), rows, hidden);
+    return check_launch("silu_mul_bwd_kernel");
 }

@@ -50,8 +50,6 @@ class RMSNorm(nn.Module):
 
     def forward(self, x):
         ops.require_cuda("RMSNorm", x)
-        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
-            return self._norm(x.float()).type_as(x) * self.weight
         return ops.rmsnorm(x, self.weight, self.eps,
                            out_dtype=torch.promote_types(x.dtype, self.weight.dtype))
 
@@ -66,8 +64,8 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(hidden_dim, d_model, bias=False)
 
     def forward(self, x):
-        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            return self.w3(F.silu(self.w1(x)) * self.w2(x))
+        # one GEMM against [w1; w2], then the fused gate (autograd through the
+        # silu_mul backward kernel and torch.cat back to w1, w2)
         w12 = torch.cat([self.w1.weight, self.w2.weight], dim=0)
         return self.w3(ops.silu_mul(F.linear(x, w12)))
 
@@ -117,9 +115,11 @@ class MOGTBlock(nn.Module):
 
     def fused_path_ok(self) -> bool:
         """Identity connection, no transport gate, rank-wide value gate coupled to
-        the forget gate, an affine scan_impl, no autograd."""
+        the forget gate, an affine scan_impl; with autograd, no learned residual
+        gate (its scale enters the fused residual update as a constant)."""
         gate = getattr(self, "phi_value_gate", None)
-        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+        if (torch.is_grad_enabled() and getattr(self, "mogt_residual_gate_enabled", False)
+                and any(p.requires_grad for p in self.parameters())):
             return False
         return (self._resolve_connection_impl() == "identity"
                 and getattr(self, "phi_transport_gate", None) is None
@@ -277,7 +277,7 @@ class MOGTBlock(nn.Module):
         return (z + const).contiguous()
 
     def forward_fused(self, x: torch.Tensor, prefix_condition, pending):
-        """Fused inference forward.  ``pending = (z, scale)`` is the previous
+        """Fused forward (differentiable: every kernel has its backward).  ``pending = (z, scale)`` is the previous
         block's last residual term (added here inside the first RMSNorm).
         Returns ``(x_after_mixer, (ffn_out, ffn_scale))``: the caller adds the
         FFN term (or hands it to the next block)."""

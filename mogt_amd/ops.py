@@ -235,9 +235,33 @@ def _(z, v, rank, damping, out_dtype):
     return v.new_empty(v.shape, dtype=out_dtype)
 
 
+@torch.library.custom_op("mogt::coupled_grad", mutates_args=())
+def _coupled_grad_op(G: torch.Tensor, z: torch.Tensor, v: torch.Tensor, h: torch.Tensor, rank: int,
+                     damping: float) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    B, L, D = v.shape
+    G = G.contiguous()
+    z = z.contiguous().to(torch.float32)
+    v = v.contiguous()
+    h = h.contiguous().to(torch.float32)
+    dv = torch.empty_like(v)
+    dz = torch.empty((B, L, rank), dtype=torch.float32, device=v.device)
+    rc = lib.mogt_coupled_rank_scan_grad(G.data_ptr(), z.data_ptr(), v.data_ptr(), h.data_ptr(), dv.data_ptr(),
+                                         dz.data_ptr(), B, L, rank, D // rank, float(damping),
+                                         dtype_code(v.dtype, "coupled_grad"), _stream_handle(v.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_grad")
+    return dv, dz
+
+
+@_coupled_grad_op.register_fake
+def _(G, z, v, h, rank, damping):
+    return torch.empty_like(v), v.new_empty((*v.shape[:2], rank), dtype=torch.float32)
+
+
 def _coupled_setup(ctx, inputs, output):
     z, v, rank, damping, _ = inputs
-    ctx.save_for_backward(z, v)
+    # the fp32 output is the forward state h; the dz term needs it (h_{t-1})
+    ctx.save_for_backward(z, v, output if output.dtype == torch.float32 else None)
     ctx.rank = rank
     ctx.damping = damping
 
@@ -246,24 +270,33 @@ def _coupled_backward(ctx, grad_h):
     """Backward of the fused gate + scan.  With g = sigmoid(z), a = damping (1-g)
     (per rank, over its c channels) and v' = v * g:  G = dH + a_{t+1} G_{t+1}
     (GPU reverse scan), dv = G * g, and per rank
-    dg = sum_c G * v - damping * sum_c G * h_{t-1}, dz = dg * g (1 - g), with h
-    recomputed in fp32 (the reference recomputes too, triton_scan.py:370-378).
+    dg = sum_c G * v - damping * sum_c G * h_{t-1}, dz = dg * g (1 - g): one HIP
+    epilogue kernel (channels a multiple of 4, D <= 4096) over G, z, v and the saved fp32
+    forward output h (recomputed in fp32 when the forward rounded it, as the
+    reference recomputes, triton_scan.py:370-378).
     The bf16 rounding of v * g (model_mogt.py:180) passes gradients through
     unchanged, as a dtype cast does under autograd."""
-    z, v = ctx.saved_tensors
+    z, v, h = ctx.saved_tensors
     r, damping = ctx.rank, ctx.damping
     B, L, D = v.shape
     c = D // r
     g = torch.sigmoid(z.float())                                   # [B, L, r]
     a_full = (damping * (1.0 - g)).unsqueeze(-1).expand(B, L, r, c).reshape(B, L, D)
     G = torch.ops.mogt.diag_scan_rev(a_full, grad_h)               # fp32 [B, L, D]
+    if c % 4 == 0 and D <= 4096:
+        if h is None:   # the forward returned a rounded h: recompute the fp32 state
+            h = torch.ops.mogt.coupled_rank_scan(z, v, r, damping, torch.float32)
+        dv, dz = torch.ops.mogt.coupled_grad(G, z, v, h, r, damping)
+        return (dz.to(z.dtype) if ctx.needs_input_grad[0] else None,
+                dv if ctx.needs_input_grad[1] else None, None, None, None)
     Gr = G.view(B, L, r, c)
     dz = dv = None
     if ctx.needs_input_grad[1]:
         g_io = g.to(v.dtype).float()                               # the gate as multiplied into v
         dv = (Gr * g_io.unsqueeze(-1)).reshape(B, L, D).to(v.dtype)
     if ctx.needs_input_grad[0]:
-        h = torch.ops.mogt.coupled_rank_scan(z, v, r, damping, torch.float32)
+        if h is None:
+            h = torch.ops.mogt.coupled_rank_scan(z, v, r, damping, torch.float32)
         hp = _shift_prev(h).view(B, L, r, c)
         dg = (Gr * v.float().view(B, L, r, c)).sum(-1) - damping * (Gr * hp).sum(-1)
         dz = (dg * g * (1.0 - g)).to(z.dtype)
@@ -590,6 +623,105 @@ def _silu_mul_op(y: torch.Tensor) -> torch.Tensor:
 @_silu_mul_op.register_fake
 def _(y):
     return y.new_empty((*y.shape[:-1], y.shape[-1] // 2))
+
+
+# backward of the row kernels -------------------------------------------------
+def _rows_per_wave(rows: int) -> int:
+    # about 2048 waves, at least 4 rows each: the dw partials stay a few MB
+    return max(4, -(-rows // 2048))
+
+
+@torch.library.custom_op("mogt::rmsnorm_bwd", mutates_args=())
+def _rmsnorm_bwd_op(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dres: torch.Tensor | None,
+                    eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    x = x.contiguous()
+    dy = dy.contiguous()
+    w = weight.contiguous().to(torch.float32)
+    D = x.shape[-1]
+    rows = x.numel() // D
+    rpw = _rows_per_wave(rows)
+    dx = torch.empty_like(x)
+    parts = torch.empty((max(1, -(-rows // rpw)), D), dtype=torch.float32, device=x.device)
+    if dres is not None:
+        dres = dres.contiguous().to(torch.float32)
+    rc = lib.mogt_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
+                              dres.data_ptr() if dres is not None else None, dx.data_ptr(),
+                              parts.data_ptr(), rows, D, float(eps), rpw, dtype_code(x.dtype, "rmsnorm_bwd"),
+                              dtype_code(dy.dtype, "rmsnorm_bwd"), _stream_handle(x.device))
+    _lib.check(rc, "mogt_rmsnorm_bwd")
+    dw = parts.sum(0) if rows > 0 else torch.zeros(D, dtype=torch.float32, device=x.device)
+    return dx, dw
+
+
+@_rmsnorm_bwd_op.register_fake
+def _(x, weight, dy, dres, eps):
+    return torch.empty_like(x), x.new_empty(x.shape[-1], dtype=torch.float32)
+
+
+def _rmsnorm_setup(ctx, inputs, output):
+    x, weight, eps, out_dtype = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.eps = eps
+
+
+def _rmsnorm_backward(ctx, g):
+    x, weight = ctx.saved_tensors
+    dx, dw = torch.ops.mogt.rmsnorm_bwd(x, weight, g, None, ctx.eps)
+    return dx, dw.to(weight.dtype), None, None
+
+
+torch.library.register_autograd("mogt::rmsnorm", _rmsnorm_backward, setup_context=_rmsnorm_setup)
+
+
+def _add_rmsnorm_setup(ctx, inputs, output):
+    x, z, scale, weight, eps, out_dtype = inputs
+    ctx.save_for_backward(output[0], weight)
+    ctx.scale = scale
+    ctx.eps = eps
+    ctx.z_dtype = z.dtype
+
+
+def _add_rmsnorm_backward(ctx, g_xout, g_out):
+    x_out, weight = ctx.saved_tensors
+    if g_out is None:
+        g_out = torch.zeros_like(x_out)
+    dx, dw = torch.ops.mogt.rmsnorm_bwd(x_out, weight, g_out, g_xout, ctx.eps)
+    dz = (dx * ctx.scale).to(ctx.z_dtype)
+    return dx, dz, None, dw.to(weight.dtype), None, None
+
+
+torch.library.register_autograd("mogt::add_rmsnorm", _add_rmsnorm_backward, setup_context=_add_rmsnorm_setup)
+
+
+@torch.library.custom_op("mogt::silu_mul_bwd", mutates_args=())
+def _silu_mul_bwd_op(y: torch.Tensor, dout: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    y = y.contiguous()
+    dout = dout.contiguous().to(y.dtype)
+    H2 = y.shape[-1]
+    dy = torch.empty_like(y)
+    rc = lib.mogt_silu_mul_bwd(y.data_ptr(), dout.data_ptr(), dy.data_ptr(), y.numel() // H2, H2 // 2,
+                               dtype_code(y.dtype, "silu_mul_bwd"), _stream_handle(y.device))
+    _lib.check(rc, "mogt_silu_mul_bwd")
+    return dy
+
+
+@_silu_mul_bwd_op.register_fake
+def _(y, dout):
+    return torch.empty_like(y)
+
+
+def _silu_mul_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+
+
+def _silu_mul_backward(ctx, g):
+    (y,) = ctx.saved_tensors
+    return torch.ops.mogt.silu_mul_bwd(y, g)
+
+
+torch.library.register_autograd("mogt::silu_mul", _silu_mul_backward, setup_context=_silu_mul_setup)
 
 
 def silu_mul(y: torch.Tensor) -> torch.Tensor:

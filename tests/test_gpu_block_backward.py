@@ -1,0 +1,145 @@
+"""GPU backward of the fused MOGT block's row kernels and of the fused block.
+
+RMSNorm / residual-add + RMSNorm / SwiGLU gate backward kernels (through the
+autograd of ``mogt::rmsnorm``, ``mogt::add_rmsnorm``, ``mogt::silu_mul``)
+against float64 torch autograd of the reference's expressions
+(model_mogt.py:15-20, 29-30, 243-256) on the same inputs; then a training step
+through the fused block path against the generic op-by-op path (whose
+pieces are each checked against float64 elsewhere), for every parameter.
+Bars: fp32 <= 1e-4 (rows: 1e-5), bf16 <= 2e-2 (normwise)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce, rel_err, to_np
+
+pytestmark = pytest.mark.gpu
+
+ROW_TOL = 1e-5
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def _rms64(x, w, eps=1e-6):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+@pytest.mark.parametrize("shape,dtype", [((2, 77, 768), torch.float32), ((3, 5, 8), torch.float32),
+                                         ((1, 300, 4096), torch.float32), ((1, 129, 1028), torch.float32),
+                                         ((2, 200, 768), torch.bfloat16)])
+def test_rmsnorm_backward(gpu, shape, dtype):
+    announce(f"rmsnorm backward {shape} {dtype}")
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(shape[1])
+    x = (torch.randn(*shape, generator=g) * 2 + 0.3).to(dtype)
+    w = 1 + 0.2 * torch.randn(shape[-1], generator=g)
+    dy = torch.randn(*shape, generator=g)
+    xt = x.to(gpu).requires_grad_()
+    wt = w.to(gpu).requires_grad_()
+    y = ops.rmsnorm(xt, wt, 1e-6, out_dtype=torch.float32)
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    x64 = x.double().requires_grad_()
+    w64 = w.double().requires_grad_()
+    _rms64(x64, w64).backward(dy.double())
+    tol = ROW_TOL if dtype == torch.float32 else BF16_TOL
+    assert xt.grad.dtype == dtype and wt.grad.dtype == torch.float32
+    assert rel_err(to_np(xt.grad), x64.grad.numpy()) <= tol
+    assert rel_err(to_np(wt.grad), w64.grad.numpy()) <= (tol if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("zdt", [torch.float32, torch.bfloat16])
+def test_add_rmsnorm_backward(gpu, zdt):
+    announce(f"add_rmsnorm backward z={zdt}")
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(9)
+    B, L, D = 2, 150, 768
+    x = torch.randn(B, L, D, generator=g)
+    z = torch.randn(B, L, D, generator=g).to(zdt)
+    w = 1 + 0.2 * torch.randn(D, generator=g)
+    c1 = torch.randn(B, L, D, generator=g)
+    c2 = torch.randn(B, L, D, generator=g)
+    xt, zt, wt = (t.to(gpu).requires_grad_() for t in (x, z, w))
+    x_out, out = ops.add_rmsnorm(xt, zt, 0.7, wt, 1e-6, out_dtype=torch.float32)
+    ((x_out * c1.to(gpu)).sum() + (out * c2.to(gpu)).sum()).backward()
+    torch.cuda.synchronize()
+    x64, z64, w64 = (t.double().requires_grad_() for t in (x, z, w))
+    xo = x64 + 0.7 * z64
+    ((xo * c1.double()).sum() + (_rms64(xo, w64) * c2.double()).sum()).backward()
+    # bf16 z: the forward rounds 0.7 z to bf16, which the float64 reference does not
+    tol = FP32_TOL if zdt == torch.float32 else BF16_TOL
+    assert zt.grad.dtype == zdt
+    errs = [rel_err(to_np(xt.grad), x64.grad.numpy()), rel_err(to_np(zt.grad), z64.grad.numpy()),
+            rel_err(to_np(wt.grad), w64.grad.numpy())]
+    assert max(errs) <= tol, errs
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul_backward(gpu, dtype):
+    announce(f"silu_mul backward {dtype}")
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(4)
+    rows, H = 333, 512
+    y = (torch.randn(rows, 2 * H, generator=g) * 2).to(dtype)
+    d = torch.randn(rows, H, generator=g).to(dtype)
+    yt = y.to(gpu).requires_grad_()
+    out = ops.silu_mul(yt)
+    out.backward(d.to(gpu))
+    torch.cuda.synchronize()
+    y64 = y.double().requires_grad_()
+    (torch.nn.functional.silu(y64[:, :H]) * y64[:, H:]).backward(d.double())
+    tol = ROW_TOL if dtype == torch.float32 else BF16_TOL
+    assert yt.grad.dtype == dtype
+    assert rel_err(to_np(yt.grad), y64.grad.numpy()) <= tol
+    if dtype == torch.bfloat16:
+        # bit-level: torch's own bf16 autograd of the same expression
+        yb = y.to(gpu).requires_grad_()
+        (torch.nn.functional.silu(yb[:, :H]) * yb[:, H:]).backward(d.to(gpu))
+        assert rel_err(to_np(yt.grad), to_np(yb.grad)) <= 1e-2
+
+
+def _train_grads(model, ids, labels, fused: bool):
+    model.zero_grad(set_to_none=True)
+    for b in model.mogt.blocks:
+        b._force_generic = not fused
+    _, loss = model(ids, labels=labels)
+    loss.backward()
+    torch.cuda.synchronize()
+    return float(loss.detach()), {k: p.grad.detach().clone() for k, p in model.named_parameters()
+                                   if p.grad is not None}
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_fused_block_training_step_matches_generic(gpu, autocast):
+    """One training step (loss.backward) of a 2-layer coupled-gate model through
+    the fused block path vs the generic path: same loss, same gradients for
+    every parameter."""
+    announce(f"fused vs generic training step autocast={autocast}")
+    from mogt_amd.model_mogt import MOGTForCausalLM, MOGTBlock, configure_coupled_gate
+
+    torch.manual_seed(7)
+    model = MOGTForCausalLM(vocab_size=512, d_model=256, num_layers=2, r=16).to(gpu)
+    configure_coupled_gate(model, connection_damping=0.995, zero_gate_weight=False)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "theta_read" in name or "ffn.w3" in name:
+                p.normal_(0.0, 0.02)
+    ids = torch.randint(0, 512, (1, 600), device=gpu)
+    labels = torch.randint(0, 512, (1, 600), device=gpu)
+    orig = MOGTBlock.fused_path_ok
+    MOGTBlock.fused_path_ok = lambda self: (not getattr(self, "_force_generic", False)) and orig(self)
+    try:
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            assert all(orig(b) for b in model.mogt.blocks)
+            lf, gf = _train_grads(model, ids, labels, fused=True)
+            lg, gg = _train_grads(model, ids, labels, fused=False)
+    finally:
+        MOGTBlock.fused_path_ok = orig
+    tol = BF16_TOL if autocast else FP32_TOL
+    assert abs(lf - lg) <= tol * abs(lg)
+    assert set(gf) == set(gg)
+    for k in gg:
+        assert rel_err(to_np(gf[k]), to_np(gg[k])) <= tol, k
