@@ -110,11 +110,13 @@ def test_fused_backbone_bf16_autocast(gpu):
     assert rel_err(to_np(out), ref.numpy()) <= BF16_TOL
 
 
-@pytest.mark.parametrize("conn", ["matrix_exp", "cayley", "identity"])
-def test_generic_block_matches_oracle(gpu, conn):
+@pytest.mark.parametrize("conn,tmode", [("matrix_exp", "multiply"), ("cayley", "multiply"),
+                                        ("identity", "multiply"), ("matrix_exp", "residual"),
+                                        ("cayley", "forget_relu")])
+def test_generic_block_matches_oracle(gpu, conn, tmode):
     """The generic path (dense HIP scan) with a non-identity connection, a
-    transport gate and a scalar value gate."""
-    announce(f"generic MOGT block {conn}")
+    transport gate (model_mogt.py:141-163, every mode) and a scalar value gate."""
+    announce(f"generic MOGT block {conn} transport gate {tmode}")
     import torch.nn as nn
 
     from mogt_amd.model_mogt import MOGTBlock
@@ -125,7 +127,8 @@ def test_generic_block_matches_oracle(gpu, conn):
     blk.connection_damping = 0.99
     blk.scan_impl = "triton_hybrid"
     blk.phi_transport_gate = nn.Linear(64, 16, bias=True).to(gpu)
-    blk.transport_gate_mode = "multiply"
+    blk.transport_gate_mode = tmode
+    blk.transport_gate_scale = 0.5
     blk.phi_value_gate = nn.Linear(128, 1, bias=True).to(gpu)
     blk.value_gate_input_mode = "current_prev"
     blk.couple_forget_to_value_gate = True
@@ -137,7 +140,7 @@ def test_generic_block_matches_oracle(gpu, conn):
     torch.cuda.synchronize()
     cfg = {"r": 16, "connection_impl": conn, "connection_damping": 0.99,
            "value_gate_input_mode": "current_prev", "couple_forget_to_value_gate": True,
-           "transport_gate_mode": "multiply"}
+           "transport_gate_mode": tmode, "transport_gate_scale": 0.5}
     p = {k: v.detach().double().cpu() for k, v in blk.state_dict().items()}
     ref = mo.block_forward(p, x.double(), None, cfg)
     assert rel_err(to_np(out), ref.numpy()) <= FP32_TOL
