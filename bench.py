@@ -668,8 +668,11 @@ def main():
         extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
             r, ffn_hidden=2048, vocab=4096,
             note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
-        rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 2, fused=True)
-        rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 2, fused=False)
+        # 10 warm-up steps: the first training steps of a process run slow for
+        # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
+        # with 10-20), independent of which path runs first
+        rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
+        rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=False)
         extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(
             rf, generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
             note="forward + backward (mean-square loss on the backbone output, no optimizer), "
