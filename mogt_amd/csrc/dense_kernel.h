@@ -78,6 +78,11 @@ constexpr int64_t kDenseNarrowWaves = 256;
 template <int RT, int CTW, bool WITHP, bool U4, bool W16, typename TV, typename TO, int MODE, bool VK>
 __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
     constexpr bool FIXED = MODE != CM_LOCAL;   // trip count kDenseChunk
+    // OUTPUT passes write H (and P) non-temporally: lines left dirty in the
+    // caches are otherwise written back while the next pass streams its
+    // operands (measured: level-0 summary after an OUTPUT pass 37-39 -> 23 us
+    // at R = 16, C = 48; configs[3] 540 -> 519 us).
+    constexpr int kOutPolicy = MODE == CM_OUTPUT ? 2 : 0;
     constexpr int NT = RT + CTW;               // column tiles: RT of P, then CTW of H
     constexpr int D = RT == 1 ? 8 : 4;         // steps of operands in flight
     static_assert(!FIXED || kDenseChunk % D == 0, "chunk must be a multiple of the prefetch depth");
@@ -362,8 +367,8 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                 if (live(ct)) X[rt][ct] = acc[rt][ct];
     };
     auto st_elem = [](__amdgpu_buffer_rsrc_t r, int off, float x) {
-        if constexpr (ES == 4) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, 0);
-        else __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(x), r, off, 0, 0);
+        if constexpr (ES == 4) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, off, 0, kOutPolicy);
+        else __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(x), r, off, 0, kOutPolicy);
     };
     // Per-step output of the state X to row `t` (P columns when WITHP; H
     // columns); `valid` false (a padding step) stores nothing.
@@ -404,7 +409,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                     };
                     piece = u32x4{pk(lo[0], lo[1]), pk(lo[2], lo[3]), pk(hi[0], hi[1]), pk(hi[2], hi[3])};
                 }
-                __builtin_amdgcn_raw_buffer_store_b128(piece, rh, offH[j][0][0], 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(piece, rh, offH[j][0][0], 0, kOutPolicy);
             }
             lds_order();
         } else if constexpr (STORES) {

@@ -473,9 +473,9 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
                 const float val = acc[r];
                 const int off = t * static_cast<int>(rowStrideB) + colB;
                 if constexpr (sizeof(TO) == 4)
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), ry, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), ry, off, 0, 2);
                 else
-                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(val), ry, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(val), ry, off, 0, 2);
             }
         }
         __syncthreads();   // sQ, sP and the old state halves are consumed
