@@ -100,6 +100,19 @@ int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                float damping, int z_dtype, int v_dtype, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
+/* Reverse scan of the coupled scan's backward: G_t = dh_t + a_{t+1} G_{t+1},
+ * G_L = 0, with a_t = damping * (1 - sigmoid(z[b,t,i])) over rank i's C
+ * channels, formed from the gate logits z [B, L, R] (fp32 or bf16) inside the
+ * scan; dh, G fp32 [B, L, R*C].  The reverse scan of the reference's backward
+ * (_triton_affine_scan_hybrid_backward, triton_scan.py:359-426, and
+ * affine_scan_sequential_backward, affine_scan.py:65-124) for the diagonal
+ * U_t = damping (1 - g_t) I of the coupled identity connection
+ * (model_mogt.py:166-203).  Workspace:
+ * mogt_diag_scan_workspace_bytes(batch, length, rank * channels, MOGT_F32). */
+int mogt_coupled_rank_scan_rev_fwd(const void* z, const float* dh, float* G,
+                                   int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                   float damping, int z_dtype,
+                                   void* workspace, size_t workspace_bytes, void* stream);
 /* Gradient epilogue of the coupled scan's backward (the autograd of the
  * fused gate + scan; the reference differentiates model_mogt.py:166-203
  * through torch ops): given G (fp32 [B, L, R*C], the reverse scan

@@ -50,7 +50,10 @@ namespace mogt {
 // MODE_DIAG_REV: the backward recurrence of MODE_DIAG, run in reverse time
 // with the decay shifted by one step: h_t = a_{t+1} h_{t+1} + b_t (a_L := 0),
 // i.e. G_t = dH_t + a_{t+1} G_{t+1} of affine_scan.py:65-124 for R = C = 1.
-enum DiagMode { MODE_DIAG = 0, MODE_COUPLED = 1, MODE_DIAG_REV = 2 };
+// MODE_COUPLED_REV: the same backward recurrence for MODE_COUPLED, whose decay
+// a = damping * (1 - sigmoid(z)) is formed from the gate logits (per gate,
+// over its C channels) instead of being read as a [B, L, D] tensor.
+enum DiagMode { MODE_DIAG = 0, MODE_COUPLED = 1, MODE_DIAG_REV = 2, MODE_COUPLED_REV = 3 };
 
 struct DiagParams {
     const void* a;      // [B, L, D] (DIAG)            | gate logits z [B, L, R] (COUPLED)
@@ -81,14 +84,15 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int T = VW * S;         // steps per chunk
     constexpr int NR = NT / FW;       // look-back window (predecessors read per round)
     static_assert(64 % FWL == 0 && FWL >= 16, "a row spans 16, 32 or 64 lanes");
-    constexpr bool COUPLED = MODE == MODE_COUPLED;
-    constexpr bool REV = MODE == MODE_DIAG_REV;
+    constexpr bool COUPLED = MODE == MODE_COUPLED;                 // gated write v * g
+    constexpr bool GATED = COUPLED || MODE == MODE_COUPLED_REV;   // decay from gate logits
+    constexpr bool REV = MODE == MODE_DIAG_REV || MODE == MODE_COUPLED_REV;
     static_assert(!(PREFIX && REV), "prefix output is a forward option");
     constexpr bool BF16_IN = std::is_same<TIn, bf16_t>::value;
     // Stash (32-bit registers per step and lane): DIAG fp32 a[VEC], b[VEC];
     // DIAG bf16 raw a and b words (two values per word); COUPLED the gate logit
     // (then the gate) and the raw v words.
-    static_assert(!(PREFIX && COUPLED), "prefix output is a DIAG-mode option");
+    static_assert(!(PREFIX && GATED), "prefix output is a DIAG-mode option");
 
     __shared__ int s_pending[2];
     __shared__ float s_cwA[VW][FW];   // level-1 summaries, then exclusive prefixes over VW
@@ -134,8 +138,8 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     // with no wait in between; steps outside the problem are replaced by the
     // identity (a = 1, b = 0) where the values are used.
     constexpr int NWB = BF16_IN ? (VEC + 1) / 2 : VEC;   // raw 32-bit words per row of b or v
-    constexpr int NA = COUPLED ? 1 : (BF16_IN ? NWB : VEC);
-    float ra[S][NA];      // DIAG fp32: a; DIAG bf16: raw a words; COUPLED: raw z, then gate g
+    constexpr int NA = GATED ? 1 : (BF16_IN ? NWB : VEC);
+    float ra[S][NA];      // DIAG fp32: a; DIAG bf16: raw a words; GATED: raw z, then decay
     uint32_t rb[S][NWB];  // raw words of b (DIAG) or v (COUPLED)
     int nv;               // valid steps of this lane (0 .. S)
     {
@@ -151,8 +155,10 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         const TIn* pb = static_cast<const TIn*>(p.b) + wbase;
         const TZ* pz = nullptr;
         int gi = 0;
-        if constexpr (COUPLED) {
-            pz = static_cast<const TZ*>(p.a) + (row0 + tw) * p.R;
+        if constexpr (GATED) {
+            // forward: the gate row of step tw + rel; REV: the row after it in
+            // memory (a_{t+1}), row L - 1 for logical step 0 (decay unused)
+            pz = static_cast<const TZ*>(p.a) + (REV ? rbase - tw : row0 + tw) * p.R;
             gi = static_cast<int>((fbase + flc) / p.C);
         }
 #pragma unroll
@@ -160,9 +166,10 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
             const int rel = min(q * S + s, lastrel);
             const int off = rel * Ds + flc;
             load_raw<sizeof(TIn) * VEC>(pb + off, rb[s]);
-            if constexpr (COUPLED) {
+            if constexpr (GATED) {
                 uint32_t zw[1];
-                load_raw_cached<sizeof(TZ)>(pz + rel * p.R + gi, zw);
+                const int zrel = REV ? ((tw + rel != 0) ? 1 - rel : -rel) : rel;
+                load_raw_cached<sizeof(TZ)>(pz + zrel * p.R + gi, zw);
                 ra[s][0] = __uint_as_float(zw[0]);
             } else {
                 uint32_t aw[NA];
@@ -177,28 +184,31 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     // a = damping * (1 - g) replaces the logit, and b = v * g (rounded to v's
     // dtype exactly where the reference's product is) replaces v in place --
     // b is exactly representable in v's dtype, so the stash keeps its size.
-    // Steps outside the problem become the identity (a = 1, b = 0).
-    if constexpr (COUPLED) {
+    // Steps outside the problem become the identity (a = 1, b = 0).  The
+    // reverse mode only forms the decay (b is the incoming gradient).
+    if constexpr (GATED) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const uint32_t zb = __float_as_uint(ra[s][0]);
             const float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
             const bool ok = s < nv;
             const float gg = sigmoidf_(z);
-            // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)
-            const float g_io = IO<TIn>::ld(IO<TIn>::st(gg));
             ra[s][0] = ok ? p.damping * (1.0f - gg) : 1.0f;
+            if constexpr (COUPLED) {
+                // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)
+                const float g_io = IO<TIn>::ld(IO<TIn>::st(gg));
 #pragma unroll
-            for (int j = 0; j < NWB; ++j) {
-                uint32_t w = rb[s][j];
-                if constexpr (BF16_IN) {
-                    const uint32_t lo = f32_to_bf16(__uint_as_float(w << 16) * g_io);
-                    const uint32_t hi = f32_to_bf16(__uint_as_float(w & 0xffff0000u) * g_io);
-                    w = lo | (hi << 16);
-                } else {
-                    w = __float_as_uint(__uint_as_float(w) * g_io);
+                for (int j = 0; j < NWB; ++j) {
+                    uint32_t w = rb[s][j];
+                    if constexpr (BF16_IN) {
+                        const uint32_t lo = f32_to_bf16(__uint_as_float(w << 16) * g_io);
+                        const uint32_t hi = f32_to_bf16(__uint_as_float(w & 0xffff0000u) * g_io);
+                        w = lo | (hi << 16);
+                    } else {
+                        w = __float_as_uint(__uint_as_float(w) * g_io);
+                    }
+                    rb[s][j] = ok ? w : 0u;
                 }
-                rb[s][j] = ok ? w : 0u;
             }
         }
     }
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         if constexpr (REV) {
             if (s == 0 && first) return 0.0f;
         }
-        if constexpr (COUPLED) return ra[s][0];
+        if constexpr (GATED) return ra[s][0];
         else if constexpr (BF16_IN) return s < nv ? bf16_at(__float_as_uint(ra[s][v >> 1]), v) : 1.0f;
         else return s < nv ? ra[s][v] : 1.0f;
     };
@@ -234,7 +244,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
         s_cwA[vw][flane + v] = A;
         s_cwH[vw][flane + v] = hh;
     }
-    if constexpr (BF16_IN || COUPLED) {
+    if constexpr (BF16_IN || GATED) {
         // Keep only the compact stash live across the look-back: an empty asm
         // that "rewrites" it stops the compiler from holding unpacked values.
 #pragma unroll

@@ -235,6 +235,29 @@ def _(z, v, rank, damping, out_dtype):
     return v.new_empty(v.shape, dtype=out_dtype)
 
 
+@torch.library.custom_op("mogt::coupled_scan_rev", mutates_args=())
+def _coupled_scan_rev_op(z: torch.Tensor, grad_h: torch.Tensor, rank: int, damping: float) -> torch.Tensor:
+    """G_t = dH_t + a_{t+1} G_{t+1} with a = damping (1 - sigmoid(z)) per rank,
+    the decay formed from the gate logits inside the reverse scan."""
+    lib = _lib.load()
+    z = z.contiguous()
+    g = grad_h.contiguous().to(torch.float32)
+    B, L, D = g.shape
+    out = torch.empty_like(g)
+    nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, _lib.MOGT_F32)
+    ws = workspace(nbytes, g.device)
+    rc = lib.mogt_coupled_rank_scan_rev_fwd(z.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, rank, D // rank,
+                                            float(damping), dtype_code(z.dtype, "coupled_scan_rev"), ws.data_ptr(),
+                                            ws.numel(), _stream_handle(g.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_rev_fwd")
+    return out
+
+
+@_coupled_scan_rev_op.register_fake
+def _(z, grad_h, rank, damping):
+    return grad_h.new_empty(grad_h.shape, dtype=torch.float32)
+
+
 @torch.library.custom_op("mogt::coupled_grad", mutates_args=())
 def _coupled_grad_op(G: torch.Tensor, z: torch.Tensor, v: torch.Tensor, h: torch.Tensor, rank: int,
                      damping: float) -> tuple[torch.Tensor, torch.Tensor]:
@@ -269,7 +292,7 @@ def _coupled_setup(ctx, inputs, output):
 def _coupled_backward(ctx, grad_h):
     """Backward of the fused gate + scan.  With g = sigmoid(z), a = damping (1-g)
     (per rank, over its c channels) and v' = v * g:  G = dH + a_{t+1} G_{t+1}
-    (GPU reverse scan), dv = G * g, and per rank
+    (GPU reverse scan forming a from z in registers), dv = G * g, and per rank
     dg = sum_c G * v - damping * sum_c G * h_{t-1}, dz = dg * g (1 - g): one HIP
     epilogue kernel (channels a multiple of 4, D <= 4096) over G, z, v and the saved fp32
     forward output h (recomputed in fp32 when the forward rounded it, as the
@@ -280,15 +303,14 @@ def _coupled_backward(ctx, grad_h):
     r, damping = ctx.rank, ctx.damping
     B, L, D = v.shape
     c = D // r
-    g = torch.sigmoid(z.float())                                   # [B, L, r]
-    a_full = (damping * (1.0 - g)).unsqueeze(-1).expand(B, L, r, c).reshape(B, L, D)
-    G = torch.ops.mogt.diag_scan_rev(a_full, grad_h)               # fp32 [B, L, D]
+    G = torch.ops.mogt.coupled_scan_rev(z, grad_h, r, damping)    # fp32 [B, L, D]
     if c % 4 == 0 and D <= 4096:
         if h is None:   # the forward returned a rounded h: recompute the fp32 state
             h = torch.ops.mogt.coupled_rank_scan(z, v, r, damping, torch.float32)
         dv, dz = torch.ops.mogt.coupled_grad(G, z, v, h, r, damping)
         return (dz.to(z.dtype) if ctx.needs_input_grad[0] else None,
                 dv if ctx.needs_input_grad[1] else None, None, None, None)
+    g = torch.sigmoid(z.float())                                   # [B, L, r]
     Gr = G.view(B, L, r, c)
     dz = dv = None
     if ctx.needs_input_grad[1]:

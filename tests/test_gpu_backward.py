@@ -107,7 +107,8 @@ def _coupled_ref(z, v, r, damping):
     return torch.stack(out, 1).reshape(B, L, D)
 
 
-@pytest.mark.parametrize("L,r,c,vdt", [(200, 4, 6, "fp32"), (513, 16, 48, "fp32"), (300, 16, 48, "bf16")])
+@pytest.mark.parametrize("L,r,c,vdt", [(200, 4, 6, "fp32"), (513, 16, 48, "fp32"), (300, 16, 48, "bf16"),
+                                        (150, 3, 5, "fp32")])
 def test_coupled_scan_backward(gpu, L, r, c, vdt):
     announce(f"coupled backward L={L} r={r} c={c} v={vdt}")
     import mogt_amd
@@ -130,3 +131,40 @@ def test_coupled_scan_backward(gpu, L, r, c, vdt):
     assert vt.grad.dtype == vt.dtype
     assert rel_err(to_np(vt.grad), v64.grad.numpy()) <= tol
     assert rel_err(to_np(zt.grad), z64.grad.numpy()) <= tol
+
+
+def _coupled_rev64(z, dh, r, damping):
+    """float64 reverse recurrence G_t = dh_t + a_{t+1} G_{t+1}, G_L = 0, with
+    a = damping (1 - sigmoid(z)) per rank (triton_scan.py:359-426 for the
+    diagonal U of the coupled identity connection)."""
+    B, L, D = dh.shape
+    c = D // r
+    a = np.repeat(damping * (1.0 - 1.0 / (1.0 + np.exp(-z.astype(np.float64)))), c, axis=2)
+    G = np.zeros((B, L, D))
+    acc = np.zeros((B, D))
+    for t in range(L - 1, -1, -1):
+        acc = dh[:, t].astype(np.float64) + (a[:, t + 1] * acc if t + 1 < L else 0.0)
+        G[:, t] = acc
+    return G
+
+
+@pytest.mark.parametrize("B,L,r,c,zdt", [(2, 300, 4, 6, "fp32"), (1, 1, 16, 48, "fp32"), (1, 2049, 16, 48, "bf16"),
+                                         (2, 77, 3, 5, "fp32"), (1, 32768, 16, 48, "fp32")])
+def test_coupled_reverse_scan(gpu, B, L, r, c, zdt):
+    """The coupled reverse scan (decay formed from the gate logits inside the
+    scan) against the float64 recurrence; odd channel counts take the
+    one-feature-per-lane tiles."""
+    announce(f"coupled reverse scan B={B} L={L} r={r} c={c} z={zdt}")
+    from mogt_amd import ops  # noqa: F401  (registers the ops)
+
+    rng = np.random.default_rng(L + c)
+    z = (rng.standard_normal((B, L, r)) * 2).astype(np.float32)
+    dh = rng.standard_normal((B, L, r * c)).astype(np.float32)
+    zt = torch.from_numpy(z).to(gpu)
+    if zdt == "bf16":
+        zt = zt.bfloat16()
+    G = torch.ops.mogt.coupled_scan_rev(zt, torch.from_numpy(dh).to(gpu), r, 0.995)
+    torch.cuda.synchronize()
+    ref = _coupled_rev64(to_np(zt).astype(np.float64), dh, r, 0.995)
+    assert G.dtype == torch.float32 and G.shape == (B, L, r * c)
+    assert rel_err(to_np(G), ref) <= FP32_TOL

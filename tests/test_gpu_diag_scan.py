@@ -197,6 +197,53 @@ def test_coupled_rank_scan(gpu, L, r, c, vdt):
     assert float(np.median(err)) <= 1e-6   # the bulk is exact to fp32 accumulation
 
 
+def test_mixed_modes_share_workspace(gpu):
+    """Forward (fp32, bf16), coupled and both reverse-time scans of different shapes
+    interleaved on one stream share one workspace (as a training step does):
+    every result stays exact."""
+    announce("diag / coupled / reverse / coupled reverse interleaved x25")
+    import mogt_amd
+    from mogt_amd import ops
+
+    a, b = synthetic.diag_inputs(1, 5000, 768, seed=31)
+    at, bt = torch.from_numpy(a).to(gpu), torch.from_numpy(b).to(gpu)
+    ab, bb = at.bfloat16(), bt.bfloat16()
+    ref_f = so.diag_scan(a, b)
+    ref_b = so.diag_scan(to_np(ab), to_np(bb))
+    z, v = synthetic.coupled_inputs(1, 3001, 16, 48, seed=32)
+    zt, vt = torch.from_numpy(z).to(gpu), torch.from_numpy(v).to(gpu)
+    ref_c = so.coupled_rank_scan(z, v, 16)
+    a2, g2 = synthetic.diag_inputs(2, 777, 320, seed=33)
+    a2t, g2t = torch.from_numpy(a2).to(gpu), torch.from_numpy(g2).to(gpu)
+    # reverse-time recurrence = forward scan of the time-reversed sequence with
+    # the decay shifted by one step (a_{t+1}, and 0 past the end)
+    a_sh = np.concatenate([a2[:, 1:], np.zeros_like(a2[:, :1])], axis=1)
+    ref_r = so.diag_scan(a_sh[:, ::-1], g2[:, ::-1])[:, ::-1]
+    # coupled reverse scan: the same with a = 0.999 (1 - sigmoid(z)) per rank
+    dh = np.random.default_rng(34).standard_normal(v.shape).astype(np.float32)
+    dht = torch.from_numpy(dh).to(gpu)
+    a_c = np.repeat(0.999 * (1.0 - 1.0 / (1.0 + np.exp(-z.astype(np.float64)))), 48, axis=2)
+    a_c = np.concatenate([a_c[:, 1:], np.zeros_like(a_c[:, :1])], axis=1).astype(np.float32)
+    ref_cr = so.diag_scan(a_c[:, ::-1], dh[:, ::-1])[:, ::-1]
+    outs = []
+    for it in range(25):
+        k = it % 5
+        if k == 0:
+            outs.append((mogt_amd.diag_scan(at, bt), ref_f, FP32_TOL))
+        elif k == 1:
+            outs.append((mogt_amd.diag_scan(ab, bb, out_dtype=torch.float32), ref_b, FP32_TOL))
+        elif k == 2:
+            outs.append((mogt_amd.coupled_rank_scan(zt, vt), ref_c, FP32_TOL))
+        elif k == 3:
+            outs.append((torch.ops.mogt.diag_scan_rev(a2t, g2t), ref_r, FP32_TOL))
+        else:
+            outs.append((torch.ops.mogt.coupled_scan_rev(zt, dht, 16, 0.999), ref_cr, FP32_TOL))
+    torch.cuda.synchronize()
+    for h, ref, tol in outs:
+        assert rel_err(to_np(h), ref) <= tol
+    assert ops.workspace_faults() == 0
+
+
 def test_zz_no_lookback_wait_gave_up(gpu):
     """Every bounded wait of every launch above completed normally."""
     from mogt_amd import ops
