@@ -257,14 +257,17 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_summary_kernel(Rank1Params p
     Tile8<TI> kt = load_tile<TI>(kp, rowbase, t0, p.L, p.H);
     Tile8<TI> vt = load_tile<TI>(vp, rowbase, t0, p.L, p.H);
 
-    // block-wide inclusive log-decay cumsum over the 256 steps (one per thread)
-    const float fv = fval<TF>(fraw, t0 + tid, p.L);
+    // block-wide inclusive log-decay cumsum over the super-chunk (one step per
+    // thread; threads past it act as f = 1)
+    static_assert(R1_RS <= R1_THREADS, "one thread per step of the super-chunk");
+    const bool tin = tid < R1_RS;
+    const float fv = tin ? fval<TF>(fraw, t0 + tid, p.L) : 1.0f;
     float lc = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
     if (lane == 63) sWave[w] = lc;
     __syncthreads();
     for (int i = 0; i < w; ++i) lc += sWave[i];
     const float lcT = sWave[0] + sWave[1] + sWave[2] + sWave[3];
-    sW[tid] = exp2_hw(lcT - lc) * (1.0f - fv);
+    if (tin) sW[tid] = exp2_hw(lcT - lc) * (1.0f - fv);
 
     const int ib = w >> 1, jb = w & 1;   // this wave's 32x32 tile of dS[i][j]
     const int m = tile_m();
