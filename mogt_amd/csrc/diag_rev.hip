@@ -5,7 +5,7 @@
 
 namespace mogt {
 
-#define MOGT_DIAG_REV_TILES(X) X(2, 32, 32, 8) X(2, 32, 16, 8) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_DIAG_REV_TILES(X) X(2, 32, 32, 8) X(2, 32, 32, 4) X(2, 32, 16, 8) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 
 int diag_run_rev(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
 #define MOGT_CASE(V_, F_, S_, W_)                                                         \
@@ -28,16 +28,6 @@ int coupled_rev_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t s
 #undef MOGT_CASE
     return set_error(MOGT_E_INVALID, "coupled reverse scan: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
                      t.vec, t.lanes, t.steps, t.waves);
-}
-
-// Tile of the reverse scans: the fp32 default list (chunks of 512 steps x 64
-// features, two features per lane where the features, the pointers and -- for
-// the coupled scan, whose lanes must share a gate -- the channel count allow).
-DiagTile rev_tile(int64_t B, int64_t L, int64_t D, bool vec2) {
-    static const TileChoice v2[] = {{{2, 32, 32, 8}, 128}, {{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128},
-                                    {{1, 64, 8, 16}, 0}};
-    static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
-    return vec2 ? pick_tile(B, L, D, v2, 4) : pick_tile(B, L, D, v1, 3);
 }
 
 }  // namespace
@@ -63,7 +53,9 @@ extern "C" int mogt_coupled_rank_scan_rev_fwd(const void* z, const float* dh, fl
     const int64_t D = rank * channels;
     const bool vec2 = channels % 2 == 0 && reinterpret_cast<uintptr_t>(dh) % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(G) % 8 == 0;
-    const DiagTile t = rev_tile(batch, length, D, vec2);
+    // the fp32 default tile; two features per lane only where the lanes of a
+    // vector share a gate (an even channel count) and the pointers allow
+    const DiagTile t = f32_tile(batch, length, D, vec2);
     DiagParams prm{};
     const int rc = diag_prepare(prm, batch, length, D, t, workspace, workspace_bytes);
     if (rc) return rc;

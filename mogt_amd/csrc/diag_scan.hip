@@ -19,11 +19,11 @@ namespace {
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 
 // Default tile (measured on MI355X, B = 1, D = 768, L = 8k..32k): chunks of
-// 512 steps x 64 features, rows of 256 B.  fp32: two features per lane, 32
-// lanes per row; bf16: four features per lane, 16 lanes per row (the packed
-// stash holds both inputs in one register per element).  Vectors need D to be
-// a multiple of the vector and aligned pointers; short problems fall back to
-// shorter chunks so the grid still covers the GPU.
+// 512 steps x 64 features, rows of 256 B.  fp32: f32_tile; bf16: four
+// features per lane, 16 lanes per row (the packed stash holds both inputs in
+// one register per element).  Vectors need D to be a multiple of the vector
+// and aligned pointers; short problems fall back to shorter chunks so the
+// grid still covers the GPU.
 DiagTile default_tile(int64_t B, int64_t L, int64_t D, bool bf16_in, int align_elems) {
     if (bf16_in) {
         static const TileChoice v4[] = {{{4, 16, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
@@ -33,11 +33,7 @@ DiagTile default_tile(int64_t B, int64_t L, int64_t D, bool bf16_in, int align_e
         if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 3);
         return pick_tile(B, L, D, v1, 3);
     }
-    static const TileChoice v2[] = {{{2, 32, 32, 8}, 128}, {{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128},
-                                    {{1, 64, 8, 16}, 0}};
-    static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
-    if (D % 2 == 0 && align_elems % 2 == 0) return pick_tile(B, L, D, v2, 4);
-    return pick_tile(B, L, D, v1, 3);
+    return f32_tile(B, L, D, D % 2 == 0 && align_elems % 2 == 0);
 }
 
 // rev: the reverse-time recurrence h_t = a_{t+1} h_{t+1} + b_t (fp32 only).

@@ -74,12 +74,14 @@ def test_diag_scan_backward_bf16(gpu):
     assert rel_err(to_np(at.grad), da_ref) <= BF16_TOL
 
 
-def test_diag_scan_backward_full_size(gpu):
-    """configs[1] shape (B=1, D=768, L=32768), fp32."""
-    announce("diag backward full size")
+@pytest.mark.parametrize("L", [16384, 32768])
+def test_diag_scan_backward_full_size(gpu, L):
+    """configs[1] shapes (B=1, D=768, L=16384 and 32768, which take different
+    default tiles), fp32."""
+    announce(f"diag backward full size L={L}")
     import mogt_amd
 
-    a, b = synthetic.cfg2_inputs(32768, seed=9)
+    a, b = synthetic.cfg2_inputs(L, seed=9)
     w = np.random.default_rng(10).standard_normal(a.shape).astype(np.float32)
     at = torch.from_numpy(a).to(gpu).requires_grad_()
     bt = torch.from_numpy(b).to(gpu).requires_grad_()
@@ -149,7 +151,8 @@ def _coupled_rev64(z, dh, r, damping):
 
 
 @pytest.mark.parametrize("B,L,r,c,zdt", [(2, 300, 4, 6, "fp32"), (1, 1, 16, 48, "fp32"), (1, 2049, 16, 48, "bf16"),
-                                         (2, 77, 3, 5, "fp32"), (1, 32768, 16, 48, "fp32")])
+                                         (2, 77, 3, 5, "fp32"), (1, 16384, 16, 48, "fp32"),
+                                         (1, 32768, 16, 48, "fp32")])
 def test_coupled_reverse_scan(gpu, B, L, r, c, zdt):
     """The coupled reverse scan (decay formed from the gate logits inside the
     scan) against the float64 recurrence; odd channel counts take the
