@@ -182,3 +182,64 @@ def test_fused_path_equals_generic_path(gpu):
         generic = model.norm_f(model.blocks[0]._forward_generic(x, x[:, 1, :]))
     torch.cuda.synchronize()
     assert rel_err(to_np(fused), to_np(generic).astype(np.float64)) <= FP32_TOL
+
+
+def _torch_sequential_scan(U, V, *, block_size=256, block_c=32, carry_scan="sequential", output_dtype=None,
+                           return_prefix=False):
+    """affine_scan_sequential (affine_scan.py:14-62) as torch ops on the GPU:
+    H_t = U_t H_{t-1} + V_t with an fp32 state, outputs cast to output_dtype."""
+    out_dtype = output_dtype or V.dtype
+    B, L, R, C = V.shape
+    H = torch.zeros(B, R, C, dtype=torch.float32, device=V.device)
+    outs = []
+    for t in range(L):
+        H = torch.bmm(U[:, t].float().contiguous(), H) + V[:, t].float()
+        outs.append(H.to(out_dtype))
+    return torch.stack(outs, 1)
+
+
+def test_bf16_training_regression(gpu, monkeypatch):
+    """sanity_triton_training.py:17-86: a 1-layer bf16 model (vocab 257, d 64,
+    r 16, seed 1234) trained one AdamW step through the HIP scan
+    (scan_impl "triton_hybrid", block 16, block_c 4, doubling carry) and through
+    a torch sequential scan: logits, loss, the five gradients of the reference's
+    list and the parameters after the step agree to its 5e-4."""
+    announce("bf16 training regression (sanity_triton_training)")
+    import copy
+
+    from mogt_amd import model_mogt, triton_scan
+    from mogt_amd.model_mogt import MOGTForCausalLM
+
+    keys = ["mogt.blocks.0.phi_conn.weight", "mogt.blocks.0.phi_val.weight", "mogt.blocks.0.theta_read.weight",
+            "mogt.blocks.0.ffn.w1.weight", "mogt.embedding.weight"]
+    torch.manual_seed(1234)
+    base = MOGTForCausalLM(vocab_size=257, d_model=64, num_layers=1, r=16).to(gpu).to(torch.bfloat16)
+    seq, hyb = copy.deepcopy(base), copy.deepcopy(base)
+    seq.mogt.blocks[0].scan_impl = "sequential"
+    hyb.mogt.blocks[0].scan_impl = "triton_hybrid"
+    hyb.mogt.blocks[0].scan_block_size = 16
+    hyb.mogt.blocks[0].scan_block_c = 4
+    hyb.mogt.blocks[0].block_carry_scan = "doubling"
+    ids = torch.randint(0, 257, (1, 32), device=gpu)
+    labels = torch.randint(0, 257, (1, 32), device=gpu)
+    opt_s = torch.optim.AdamW(seq.parameters(), lr=1e-3)
+    opt_h = torch.optim.AdamW(hyb.parameters(), lr=1e-3)
+    with monkeypatch.context() as m:
+        m.setattr(triton_scan, "triton_affine_scan_hybrid", _torch_sequential_scan)
+        assert model_mogt.triton_scan.triton_affine_scan_hybrid is _torch_sequential_scan
+        logits_s, loss_s = seq(ids, labels)
+        loss_s.backward()
+    logits_h, loss_h = hyb(ids, labels)
+    loss_h.backward()
+    torch.cuda.synchronize()
+    diffs = {"logits": float((logits_s.float() - logits_h.float()).abs().max()),
+             "loss": float((loss_s.float() - loss_h.float()).abs())}
+    ps, ph = dict(seq.named_parameters()), dict(hyb.named_parameters())
+    for k in keys:
+        diffs[k + ".grad"] = float((ps[k].grad.float() - ph[k].grad.float()).abs().max())
+    opt_s.step()
+    opt_h.step()
+    for k in keys:
+        diffs[k] = float((ps[k].float() - ph[k].float()).abs().max())
+    assert max(diffs.values()) <= 5e-4, diffs
+    assert ph["mogt.blocks.0.theta_read.weight"].grad.abs().sum() > 0
