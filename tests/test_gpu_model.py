@@ -232,14 +232,14 @@ def test_bf16_training_regression(gpu, monkeypatch):
     logits_h, loss_h = hyb(ids, labels)
     loss_h.backward()
     torch.cuda.synchronize()
-    diffs = {"logits": float((logits_s.float() - logits_h.float()).abs().max()),
-             "loss": float((loss_s.float() - loss_h.float()).abs())}
+    diffs = {"logits": float((logits_s.float() - logits_h.float()).abs().max().detach()),
+             "loss": float((loss_s.float() - loss_h.float()).abs().detach())}
     ps, ph = dict(seq.named_parameters()), dict(hyb.named_parameters())
     for k in keys:
         diffs[k + ".grad"] = float((ps[k].grad.float() - ph[k].grad.float()).abs().max())
     opt_s.step()
     opt_h.step()
     for k in keys:
-        diffs[k] = float((ps[k].float() - ph[k].float()).abs().max())
+        diffs[k] = float((ps[k].float() - ph[k].float()).abs().max().detach())
     assert max(diffs.values()) <= 5e-4, diffs
     assert ph["mogt.blocks.0.theta_read.weight"].grad.abs().sum() > 0
