@@ -171,7 +171,8 @@ extern "C" int mogt_affine_scan_vk_fwd(const void* U, const void* v, const void*
                                        int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                        int vk_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
                                        void* stream) {
-    if (channels > 0 && (!v || !k)) {
+    // empty problems return before any pointer is needed (as in run_dense)
+    if (batch > 0 && length > 0 && channels > 0 && (!v || !k)) {
         clear_error();
         return set_error(MOGT_E_INVALID, "null tensor pointer");
     }

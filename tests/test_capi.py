@@ -69,6 +69,38 @@ def test_argument_errors_without_device(lib):
     assert lib.mogt_lm_ce_fwd(None, 32, 0, None, 0, 32, -100, None, None, None) == 0
 
 
+def test_empty_problems_are_noops_without_device(lib):
+    """Zero batch, length or rows: every compute entry point returns success
+    before it needs a pointer or the device."""
+    N = None
+    calls = {
+        "diag": lambda B, L: lib.mogt_diag_scan_fwd(N, N, N, N, B, L, 8, 0, 0, N, 0, N),
+        "diag_rev": lambda B, L: lib.mogt_diag_scan_rev_fwd(N, N, N, B, L, 8, N, 0, N),
+        "coupled": lambda B, L: lib.mogt_coupled_rank_scan_fwd(N, N, N, B, L, 4, 6, 1.0, 0, 0, 0, N, 0, N),
+        "coupled_rev": lambda B, L: lib.mogt_coupled_rank_scan_rev_fwd(N, N, N, B, L, 4, 6, 1.0, 0, N, 0, N),
+        "coupled_grad": lambda B, L: lib.mogt_coupled_rank_scan_grad(N, N, N, N, N, N, B, L, 4, 8, 1.0, 0, N),
+        "dense": lambda B, L: lib.mogt_affine_scan_fwd(N, N, N, N, B, L, 16, 8, 0, 0, N, 0, N),
+        "dense_vk": lambda B, L: lib.mogt_affine_scan_vk_fwd(N, N, N, N, N, B, L, 16, 16, 0, 0, N, 0, N),
+        "fused": lambda B, L: lib.mogt_fused_scan_fwd(N, N, B, L, 16, 0, N, 0, N),
+        "local": lambda B, L: lib.mogt_affine_local_scan(N, N, N, N, N, N, B, L, 16, 8, 32, 0, N),
+        "rank1": lambda B, L: lib.mogt_rank1_coupled_scan_fwd(N, N, N, N, N, B, L, 3, 64, 0, 0, 0, N, 0, N),
+    }
+    for name, call in calls.items():
+        for B, L in ((0, 5), (2, 0)):
+            assert call(B, L) == 0, (name, B, L, lib.mogt_last_error())
+    rows = {
+        "rmsnorm": lambda: lib.mogt_rmsnorm_fwd(N, N, N, 0, 64, 1e-6, 0, 0, N),
+        "add_rmsnorm": lambda: lib.mogt_add_rmsnorm_fwd(N, N, 0.5, N, N, N, 0, 64, 1e-6, 0, 0, N),
+        "silu_mul": lambda: lib.mogt_silu_mul_fwd(N, N, 0, 64, 0, N),
+        "rmsnorm_bwd": lambda: lib.mogt_rmsnorm_bwd(N, N, N, N, N, N, 0, 64, 1e-6, 4, 0, 0, N),
+        "silu_mul_bwd": lambda: lib.mogt_silu_mul_bwd(N, N, N, 0, 64, 0, N),
+        "connection_map": lambda: lib.mogt_connection_map_fwd(N, N, 0, 16, 1.0, 1.0, 0, 0, N),
+        "lm_ce_bwd": lambda: lib.mogt_lm_ce_bwd(N, 32, 0, N, N, 0, 32, -100, N, N, 32, 0, N),
+    }
+    for name, call in rows.items():
+        assert call() == 0, (name, lib.mogt_last_error())
+
+
 def test_tile_lists(lib):
     for fam in (0, 1, 2):
         tiles = _lib.diag_tiles(fam)
