@@ -42,7 +42,9 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--only", choices=["diag", "all"], default="all")
+    p.add_argument("--only", choices=["diag", "rank1", "dense", "all"], default="all",
+                   help="after the headline: every extra (all), none (diag), or only the rank-1 "
+                        "(configs[2]) or dense (core shape and configs[3]) lines")
     p.add_argument("--tile", default=None,
                    help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
@@ -594,89 +596,94 @@ def main():
     log(f"headline: {head['ms'] * 1e3:.1f} us/launch, {head['gbs']:.0f} GB/s")
 
     extras = {}
-    if not args.no_extras and args.only == "all":
-        for L in (8192, 16384):
-            r = measure_diag(torch, lib, ops, L, torch.float32, torch.float32, args.steps,
-                             args.warmup)
-            extras[f"diag_fp32_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-                                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
-        for L in (8192, 32768):
-            r = measure_diag(torch, lib, ops, L, torch.bfloat16, torch.bfloat16, args.steps,
-                             args.warmup)
-            extras[f"diag_bf16_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-                                         "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
-        r = measure_diag_rev(torch, lib, ops, 32768, args.steps, args.warmup)
-        extras["diag_rev_fp32_L32768"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
-        r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
-        extras["coupled_rank_scan_r16c48_L32768"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
-        r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
-        extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out)"}
-        r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
-        extras["dense_affine_r16_c48_L32768"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "vs_reference_triton_hybrid_L4_5.48ms": round(REF_TRITON_CORE_MS_L4 / r["ms"], 1),
-            "note": "U [1,L,16,16] + V [1,L,16,48] fp32 -> H fp32; the reference's core-operator "
-                    "shape (its 5.48 ms was measured on an NVIDIA L4)"}
-        r = measure_dense(torch, lib, ops, 8, 16384, 32, 32, max(3, args.steps // 10), 1,
-                          cayley=True, sets=2)
-        extras["dense_cayley_cfg4_h8_d32_L16384"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
-            "note": "BASELINE configs[3]: U=gate*Cayley(W) [8,L,32,32], V=v k^T [8,L,32,32] fp32"}
-        r = measure_dense(torch, lib, ops, 8, 16384, 32, 32, max(3, args.steps // 10), 1, sets=2, vk=True)
-        extras["dense_cayley_cfg4_vk_h8_d32_L16384"] = {
-            "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
-            "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
-            "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
-            "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
-                    "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
-        for impl in ("matrix_exp", "cayley"):
-            r = measure_connection_map(torch, lib, ops, impl, 32768, 16, args.steps, args.warmup)
-            extras[f"connection_map_{impl}_r16_n32768"] = {
-                "us": round(r["ms"] * 1e3, 2), "torch_us": round(r["ms_torch"] * 1e3, 2),
-                "note": "U = f(A) for 32768 skew 16x16 generators (one MOGT layer at L = 32768); "
-                        "torch_us: torch.matrix_exp / torch.linalg.solve on the same GPU inputs"}
-        r = measure_lm_ce(torch, lib, args.steps, args.warmup)
-        extras["lm_ce_rows_4096x32000_fp32"] = {
-            "fwd_us": round(r["fwd_ms"] * 1e3, 2), "fwd_GB/s": round(r["fwd_gbs"], 1),
-            "fwd_frac": round(r["fwd_gbs"] / HBM_PEAK_GBS, 4),
-            "bwd_us": round(r["bwd_ms"] * 1e3, 2), "bwd_GB/s": round(r["bwd_gbs"], 1),
-            "bwd_frac": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4),
-            "note": "cross-entropy rows of one logits block: forward reads it once (lse, loss), "
-                    "backward reads it and writes the softmax gradient"}
-        extras["chunked_linear_ce_L32768_d768_v32000_fwd_bwd_ms"] = {
-            "ms": round(r["e2e_ms"], 2), "reference_torch_ops_ms": round(r["ref_ms"], 2),
-            "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
-                    "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
-                    "torch ops on the same GPU"}
-        r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
-        extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
-            r, ffn_hidden=3072, vocab=32000,
-            note="BASELINE configs[4]: 4 layers, 4x gated MLP, bf16 autocast; target < 77.56 ms")
-        r = measure_backbone(torch, 2, None, 4096, 32768, 10, 3)
-        extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
-            r, ffn_hidden=2048, vocab=4096,
-            note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
-        # 10 warm-up steps: the first training steps of a process run slow for
-        # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
-        # with 10-20), independent of which path runs first
-        rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
-        rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=False)
-        extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(
-            rf, generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
-            note="forward + backward (mean-square loss on the backbone output, no optimizer), "
-                 "bf16 autocast; fused block path vs the generic op-by-op path on the same weights")
+    if not args.no_extras and args.only != "diag":
+        full = args.only == "all"
+        if full:
+            for L in (8192, 16384):
+                r = measure_diag(torch, lib, ops, L, torch.float32, torch.float32, args.steps,
+                                 args.warmup)
+                extras[f"diag_fp32_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            for L in (8192, 32768):
+                r = measure_diag(torch, lib, ops, L, torch.bfloat16, torch.bfloat16, args.steps,
+                                 args.warmup)
+                extras[f"diag_bf16_L{L}"] = {"us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                                             "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}
+            r = measure_diag_rev(torch, lib, ops, 32768, args.steps, args.warmup)
+            extras["diag_rev_fp32_L32768"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
+            r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
+            extras["coupled_rank_scan_r16c48_L32768"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
+        if full or args.only == "rank1":
+            r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
+            extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out)"}
+        if full or args.only == "dense":
+            r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
+            extras["dense_affine_r16_c48_L32768"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "vs_reference_triton_hybrid_L4_5.48ms": round(REF_TRITON_CORE_MS_L4 / r["ms"], 1),
+                "note": "U [1,L,16,16] + V [1,L,16,48] fp32 -> H fp32; the reference's core-operator "
+                        "shape (its 5.48 ms was measured on an NVIDIA L4)"}
+            r = measure_dense(torch, lib, ops, 8, 16384, 32, 32, max(3, args.steps // 10), 1,
+                              cayley=True, sets=2)
+            extras["dense_cayley_cfg4_h8_d32_L16384"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
+                "note": "BASELINE configs[3]: U=gate*Cayley(W) [8,L,32,32], V=v k^T [8,L,32,32] fp32"}
+            r = measure_dense(torch, lib, ops, 8, 16384, 32, 32, max(3, args.steps // 10), 1, sets=2, vk=True)
+            extras["dense_cayley_cfg4_vk_h8_d32_L16384"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
+                "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
+                        "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
+        if full:
+            for impl in ("matrix_exp", "cayley"):
+                r = measure_connection_map(torch, lib, ops, impl, 32768, 16, args.steps, args.warmup)
+                extras[f"connection_map_{impl}_r16_n32768"] = {
+                    "us": round(r["ms"] * 1e3, 2), "torch_us": round(r["ms_torch"] * 1e3, 2),
+                    "note": "U = f(A) for 32768 skew 16x16 generators (one MOGT layer at L = 32768); "
+                            "torch_us: torch.matrix_exp / torch.linalg.solve on the same GPU inputs"}
+            r = measure_lm_ce(torch, lib, args.steps, args.warmup)
+            extras["lm_ce_rows_4096x32000_fp32"] = {
+                "fwd_us": round(r["fwd_ms"] * 1e3, 2), "fwd_GB/s": round(r["fwd_gbs"], 1),
+                "fwd_frac": round(r["fwd_gbs"] / HBM_PEAK_GBS, 4),
+                "bwd_us": round(r["bwd_ms"] * 1e3, 2), "bwd_GB/s": round(r["bwd_gbs"], 1),
+                "bwd_frac": round(r["bwd_gbs"] / HBM_PEAK_GBS, 4),
+                "note": "cross-entropy rows of one logits block: forward reads it once (lse, loss), "
+                        "backward reads it and writes the softmax gradient"}
+            extras["chunked_linear_ce_L32768_d768_v32000_fwd_bwd_ms"] = {
+                "ms": round(r["e2e_ms"], 2), "reference_torch_ops_ms": round(r["ref_ms"], 2),
+                "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
+                        "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
+                        "torch ops on the same GPU"}
+            r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
+            extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
+                r, ffn_hidden=3072, vocab=32000,
+                note="BASELINE configs[4]: 4 layers, 4x gated MLP, bf16 autocast; target < 77.56 ms")
+            r = measure_backbone(torch, 2, None, 4096, 32768, 10, 3)
+            extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
+                r, ffn_hidden=2048, vocab=4096,
+                note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
+            # 10 warm-up steps: the first training steps of a process run slow for
+            # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
+            # with 10-20), independent of which path runs first
+            rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
+            rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=False)
+            extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(
+                rf, generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
+                note="forward + backward (mean-square loss on the backbone output, no optimizer), "
+                     "bf16 autocast; fused block path vs the generic op-by-op path on the same weights")
         log(f"extras: {json.dumps(extras)}")
 
     cpu = None
