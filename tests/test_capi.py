@@ -1,6 +1,5 @@
 """The C-ABI library loads without a GPU, exports every function declared in
 include/*.h, and rejects bad arguments before touching the device."""
-import ctypes
 import re
 from pathlib import Path
 

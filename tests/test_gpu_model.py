@@ -10,7 +10,6 @@ import pytest
 import torch
 
 from conftest import announce, rel_err, to_np
-from mogt_amd import synthetic
 from oracle import model_oracle as mo
 
 pytestmark = pytest.mark.gpu
