@@ -9,6 +9,8 @@
 // shuffles, and the row is written once.
 #include "common.h"
 
+#include <initializer_list>
+
 namespace mogt {
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -70,24 +72,50 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
     }
 }
 
-template <typename T>
+// sigmoid(a) = 1 / (1 + 2^(-a log2 e)) on the hardware exponential and
+// reciprocal (v_exp_f32, v_rcp_f32; about 2 ulp): a = -inf gives 0, +inf 1.
+__device__ __forceinline__ float sigmoid_hw(float a) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
+}
+
+// The SwiGLU row kernels walk the flattened [rows, H / VEC] vector index with a
+// grid stride; a thread's first (row, column) is one division and later ones
+// advance by the stride's quotient and remainder (no 64-bit division per
+// vector: these kernels are otherwise VALU-bound on the division alone).
+struct RowWalk {
+    int64_t i, r, c, S, sq, sr, hv;
+    __device__ RowWalk(int64_t hv_) : hv(hv_) {
+        S = static_cast<int64_t>(gridDim.x) * blockDim.x;
+        i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+        r = i / hv;
+        c = i - r * hv;
+        sq = S / hv;
+        sr = S - sq * hv;
+    }
+    __device__ __forceinline__ void next() {
+        i += S;
+        r += sq;
+        c += sr;
+        if (c >= hv) {
+            c -= hv;
+            ++r;
+        }
+    }
+};
+
+// SwiGLU gate (model_mogt.py:29-30): out = silu(a) * b for y = [a | b] rows.
+template <typename T, int VEC>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const T* __restrict__ y, T* __restrict__ out,
                                                        int64_t rows, int64_t H) {
-    const int64_t nvec = rows * H / 4;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t e = i * 4;
-        const int64_t r = e / H;
-        const int64_t c = e - r * H;
-        float a[4], b[4], o[4];
-        load_vec<T, 4>(y + r * 2 * H + c, a);
-        load_vec<T, 4>(y + r * 2 * H + H + c, b);
+    const int64_t nvec = rows * (H / VEC);
+    for (RowWalk w(H / VEC); w.i < nvec; w.next()) {
+        const T* ya = y + w.r * 2 * H + w.c * VEC;
+        float a[VEC], b[VEC], o[VEC];
+        load_vec<T, VEC>(ya, a);
+        load_vec<T, VEC>(ya + H, b);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float s = rnd<T>(a[k] / (1.0f + expf(-a[k])));   // F.silu on the bf16 tensor
-            o[k] = s * b[k];
-        }
-        store_vec<T, 4>(out + r * H + c, o);
+        for (int k = 0; k < VEC; ++k) o[k] = rnd<T>(a[k] * sigmoid_hw(a[k])) * b[k];   // F.silu on T
+        store_vec<T, VEC>(out + w.r * H + w.c * VEC, o);
     }
 }
 
@@ -172,35 +200,47 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
 // each rounded to the dtype where torch's bf16 autograd rounds (mul backward,
 // then silu_backward in fp32 and cast).  dy = [da | db], the gradient of the
 // fused [w1; w2] projection's output.
-template <typename T>
+template <typename T, int VEC>
 __global__ __launch_bounds__(256) void silu_mul_bwd_kernel(const T* __restrict__ y, const T* __restrict__ dout,
                                                            T* __restrict__ dy, int64_t rows, int64_t H) {
-    const int64_t nvec = rows * H / 4;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int64_t e = i * 4;
-        const int64_t r = e / H;
-        const int64_t c = e - r * H;
-        float a[4], b[4], d[4], da[4], db[4];
-        load_vec<T, 4>(y + r * 2 * H + c, a);
-        load_vec<T, 4>(y + r * 2 * H + H + c, b);
-        load_vec<T, 4>(dout + r * H + c, d);
+    const int64_t nvec = rows * (H / VEC);
+    for (RowWalk w(H / VEC); w.i < nvec; w.next()) {
+        const int64_t ia = w.r * 2 * H + w.c * VEC;
+        float a[VEC], b[VEC], d[VEC], da[VEC], db[VEC];
+        load_vec<T, VEC>(y + ia, a);
+        load_vec<T, VEC>(y + ia + H, b);
+        load_vec<T, VEC>(dout + w.r * H + w.c * VEC, d);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float sg = 1.0f / (1.0f + expf(-a[k]));
-            const float s = rnd<T>(a[k] / (1.0f + expf(-a[k])));
-            db[k] = d[k] * s;
+        for (int k = 0; k < VEC; ++k) {
+            const float sg = sigmoid_hw(a[k]);
+            db[k] = d[k] * rnd<T>(a[k] * sg);
             const float ds = rnd<T>(d[k] * b[k]);
             da[k] = ds * sg * (1.0f + a[k] * (1.0f - sg));
         }
-        store_vec<T, 4>(dy + r * 2 * H + c, da);
-        store_vec<T, 4>(dy + r * 2 * H + H + c, db);
+        store_vec<T, VEC>(dy + ia, da);
+        store_vec<T, VEC>(dy + ia + H, db);
     }
 }
 
 namespace {
 
 bool dt_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
+
+// Widest vector (elements, at most 16 bytes) that divides the hidden width and
+// that every pointer is aligned to.
+int swiglu_vec(int64_t hidden, size_t esz, std::initializer_list<const void*> ptrs) {
+    for (int v : {8, 4, 2}) {
+        if (v * esz > 16 || hidden % v) continue;
+        bool ok = true;
+        for (const void* p : ptrs) ok = ok && reinterpret_cast<uintptr_t>(p) % (v * esz) == 0;
+        if (ok) return v;
+    }
+    return 1;
+}
+dim3 swiglu_grid(int64_t rows, int64_t hidden, int vec) {
+    const int64_t nvec = rows * (hidden / vec);
+    return dim3(static_cast<unsigned>(nvec / 256 + 1 < 8192 ? nvec / 256 + 1 : 8192));
+}
 
 template <typename TX, typename TG>
 int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* dres, void* dx, float* dw_part,
@@ -313,15 +353,22 @@ extern "C" int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t
     if (rows == 0) return MOGT_OK;
     if (!y || !out) return set_error(MOGT_E_INVALID, "silu_mul: null pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int64_t nvec = rows * hidden / 4;
-    const unsigned grid = static_cast<unsigned>(nvec / 256 + 1 < 8192 ? nvec / 256 + 1 : 8192);
-    if (dtype == MOGT_F32)
-        hipLaunchKernelGGL((silu_mul_kernel<float>), dim3(grid), dim3(256), 0, st,
-                           static_cast<const float*>(y), static_cast<float*>(out), rows, hidden);
-    else
-        hipLaunchKernelGGL((silu_mul_kernel<bf16_t>), dim3(grid), dim3(256), 0, st,
-                           static_cast<const bf16_t*>(y), static_cast<bf16_t*>(out), rows, hidden);
-    return check_launch("silu_mul_kernel");
+    const size_t esz = dtype == MOGT_F32 ? 4 : 2;
+    const int vec = swiglu_vec(hidden, esz, {y, out});
+    const dim3 grid = swiglu_grid(rows, hidden, vec);
+#define MOGT_SILU_CASE(T, V)                                                                                      \
+    if (vec == V) {                                                                                               \
+        hipLaunchKernelGGL((silu_mul_kernel<T, V>), grid, dim3(256), 0, st, static_cast<const T*>(y),              \
+                           static_cast<T*>(out), rows, hidden);                                                   \
+        return check_launch("silu_mul_kernel");                                                                   \
+    }
+    if (dtype == MOGT_F32) {
+        MOGT_SILU_CASE(float, 4) MOGT_SILU_CASE(float, 2) MOGT_SILU_CASE(float, 1)
+    } else {
+        MOGT_SILU_CASE(bf16_t, 8) MOGT_SILU_CASE(bf16_t, 4) MOGT_SILU_CASE(bf16_t, 2) MOGT_SILU_CASE(bf16_t, 1)
+    }
+#undef MOGT_SILU_CASE
+    return set_error(MOGT_E_INVALID, "silu_mul: no vector width");
 }
 
 extern "C" int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const float* dres, void* dx,
@@ -356,14 +403,21 @@ extern "C" int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int6
     if (rows == 0) return MOGT_OK;
     if (!y || !dout || !dy) return set_error(MOGT_E_INVALID, "silu_mul_bwd: null pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int64_t nvec = rows * hidden / 4;
-    const unsigned grid = static_cast<unsigned>(nvec / 256 + 1 < 8192 ? nvec / 256 + 1 : 8192);
-    if (dtype == MOGT_F32)
-        hipLaunchKernelGGL((silu_mul_bwd_kernel<float>), dim3(grid), dim3(256), 0, st, static_cast<const float*>(y),
-                           static_cast<const float*>(dout), static_cast<float*>(dy), rows, hidden);
-    else
-        hipLaunchKernelGGL((silu_mul_bwd_kernel<bf16_t>), dim3(grid), dim3(256), 0, st,
-                           static_cast<const bf16_t*>(y), static_cast<const bf16_t*>(dout),
-                           static_cast<bf16_t*>(dy), rows, hidden);
-    return check_launch("silu_mul_bwd_kernel");
+    const size_t esz = dtype == MOGT_F32 ? 4 : 2;
+    const int vec = swiglu_vec(hidden, esz, {y, dout, dy});
+    const dim3 grid = swiglu_grid(rows, hidden, vec);
+#define MOGT_SILU_BWD_CASE(T, V)                                                                                  \
+    if (vec == V) {                                                                                               \
+        hipLaunchKernelGGL((silu_mul_bwd_kernel<T, V>), grid, dim3(256), 0, st, static_cast<const T*>(y),          \
+                           static_cast<const T*>(dout), static_cast<T*>(dy), rows, hidden);                       \
+        return check_launch("silu_mul_bwd_kernel");                                                               \
+    }
+    if (dtype == MOGT_F32) {
+        MOGT_SILU_BWD_CASE(float, 4) MOGT_SILU_BWD_CASE(float, 2) MOGT_SILU_BWD_CASE(float, 1)
+    } else {
+        MOGT_SILU_BWD_CASE(bf16_t, 8) MOGT_SILU_BWD_CASE(bf16_t, 4) MOGT_SILU_BWD_CASE(bf16_t, 2)
+        MOGT_SILU_BWD_CASE(bf16_t, 1)
+    }
+#undef MOGT_SILU_BWD_CASE
+    return set_error(MOGT_E_INVALID, "silu_mul_bwd: no vector width");
 }

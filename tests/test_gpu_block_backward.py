@@ -143,3 +143,30 @@ def test_fused_block_training_step_matches_generic(gpu, autocast):
     assert set(gf) == set(gg)
     for k in gg:
         assert rel_err(to_np(gf[k]), to_np(gg[k])) <= tol, k
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul_vector_widths(gpu, dtype):
+    """Hidden widths and storage offsets that select every vector width of the
+    SwiGLU kernels (16, 8, 4 and 2-byte accesses): forward and backward against
+    float64 autograd of silu(a) * b on the same (rounded) inputs."""
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(11)
+    rows = 37
+    for H in (4, 12, 8, 64):
+        for off in (0, 1, 2, 4):
+            announce(f"silu_mul widths {dtype} H={H} offset={off}")
+            base = (torch.randn(off + rows * 2 * H, generator=g) * 3).to(dtype).to(gpu)
+            gbase = torch.randn(off + rows * H, generator=g).to(dtype).to(gpu)
+            y = base[off:].view(rows, 2 * H).requires_grad_()
+            d = gbase[off:].view(rows, H)
+            out = ops.silu_mul(y)
+            out.backward(d)
+            torch.cuda.synchronize()
+            y64 = y.detach().double().cpu().requires_grad_()
+            ref = torch.nn.functional.silu(y64[:, :H]) * y64[:, H:]
+            ref.backward(d.double().cpu())
+            tol = ROW_TOL if dtype == torch.float32 else BF16_TOL
+            assert rel_err(to_np(out), ref.detach().numpy()) <= tol, (H, off)
+            assert rel_err(to_np(y.grad), y64.grad.numpy()) <= tol, (H, off)
