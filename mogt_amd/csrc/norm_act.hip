@@ -148,21 +148,31 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
         if (c < D) load_vec<float, 4>(w + c, ww[k]);
     }
     const float inv_d = 1.0f / static_cast<float>(D);
-    for (int64_t row = r0; row < r1; ++row) {
-        float v[VPL][4], g[VPL][4];
-        float ss = 0.0f;
+    // x, dy and dres of a row (zeros past D); the next row's are in flight
+    // while the current one reduces
+    auto load_row = [&](int64_t row, float (&v)[VPL][4], float (&g)[VPL][4], float (&rr)[VPL][4]) {
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int c = (k * 64 + lane) * 4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[k][e] = g[k][e] = 0.0f;
+            for (int e = 0; e < 4; ++e) v[k][e] = g[k][e] = rr[k][e] = 0.0f;
             if (c < D) {
                 load_vec<TX, 4>(x + row * D + c, v[k]);
                 load_vec<TG, 4>(dy + row * D + c, g[k]);
+                if (dres) load_vec<float, 4>(dres + row * D + c, rr[k]);
             }
+        }
+    };
+    float v[VPL][4], g[VPL][4], rr[VPL][4];
+    load_row(r0, v, g, rr);
+    for (int64_t row = r0; row < r1; ++row) {
+        float vn[VPL][4], gn[VPL][4], rn[VPL][4];
+        if (row + 1 < r1) load_row(row + 1, vn, gn, rn);
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
 #pragma unroll
             for (int e = 0; e < 4; ++e) ss = fmaf(v[k][e], v[k][e], ss);
-        }
         const float r = rsqrtf(wave_sum(ss) * inv_d + eps);
         float dot = 0.0f;
 #pragma unroll
@@ -179,12 +189,21 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
         for (int k = 0; k < VPL; ++k) {
             const int c = (k * 64 + lane) * 4;
             if (c < D) {
-                float o[4], rr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (dres) load_vec<float, 4>(dres + row * D + c, rr);
+                float o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = r * (g[k][e] - v[k][e] * r * mdot) + rr[e];
+                for (int e = 0; e < 4; ++e) o[e] = r * (g[k][e] - v[k][e] * r * mdot) + rr[k][e];
                 store_vec<TX, 4>(dx + row * D + c, o);
             }
+        }
+        if (row + 1 < r1) {
+#pragma unroll
+            for (int k = 0; k < VPL; ++k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[k][e] = vn[k][e];
+                    g[k][e] = gn[k][e];
+                    rr[k][e] = rn[k][e];
+                }
         }
     }
 #pragma unroll
