@@ -308,9 +308,9 @@ def measure_lm_ce(torch, lib, steps, warmup, rows=4096, vocab=32000, L=32768, D=
             "e2e_ms": ms_e2e, "ref_ms": ms_ref}
 
 
-def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
+def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48, tile=None):
     """Model-shaped coupled per-rank gate scan (config 2'): z fp32 [1,L,16],
-    v bf16 [1,L,768] -> h fp32 [1,L,768]."""
+    v bf16 [1,L,768] -> h fp32 [1,L,768]; ``tile`` forces a compiled tile."""
     from mogt_amd import synthetic
 
     dev = torch.device("cuda:0")
@@ -319,16 +319,22 @@ def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48):
     vt = torch.from_numpy(v).to(dev).bfloat16()
     sets = 4
     bufs = [(zt.clone(), vt.clone(), torch.empty(1, L, r * c, device=dev)) for _ in range(sets)]
-    nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(1, L, r, c, 1)
+    if tile is None:
+        nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(1, L, r, c, 1)
+    else:
+        nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(1, L, r * c, *tile)
     ws = ops.workspace(nbytes, dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    fn = lib.mogt_coupled_rank_scan_fwd
 
     def launch(i):
         zz, vv, hh = bufs[i % sets]
-        rc = fn(zz.data_ptr(), vv.data_ptr(), hh.data_ptr(), 1, L, r, c, 1.0, 0, 1, 0,
-                ws.data_ptr(), ws.numel(), sh)
+        if tile is None:
+            rc = lib.mogt_coupled_rank_scan_fwd(zz.data_ptr(), vv.data_ptr(), hh.data_ptr(), 1, L, r, c, 1.0, 0, 1,
+                                                0, ws.data_ptr(), ws.numel(), sh)
+        else:
+            rc = lib.mogt_coupled_rank_scan_fwd_cfg(zz.data_ptr(), vv.data_ptr(), hh.data_ptr(), 1, L, r, c, 1.0,
+                                                    0, 1, 0, *tile, ws.data_ptr(), ws.numel(), sh)
         if rc:
             raise RuntimeError(lib.mogt_last_error().decode())
 
@@ -622,6 +628,10 @@ def main():
                     r = measure_diag(torch, lib, ops, L, dt, dt, args.steps, args.warmup, tile=t)
                     log(f"sweep L={L} {dt} tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
                         f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+            for t in mogt_amd._lib.diag_tiles(2):
+                r = measure_coupled(torch, lib, ops, L, args.steps, args.warmup, tile=t)
+                log(f"sweep L={L} coupled tile={t}: {r['ms'] * 1e3:.1f} us  {r['gbs']:.0f} GB/s "
+                    f"({r['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
 
     log("headline: diag scan fp32 B=1 D=768 L=32768")
     head = measure_diag(torch, lib, ops, 32768, torch.float32, torch.float32, args.steps,

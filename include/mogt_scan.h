@@ -100,6 +100,15 @@ int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                float damping, int z_dtype, int v_dtype, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
+/* mogt_coupled_rank_scan_fwd with an explicit tile, one of
+ * mogt_diag_scan_tiles(2) whose vector divides `channels` (v and h aligned to
+ * it, up to 16 bytes); for sweeps and tile coverage tests.  Workspace:
+ * mogt_diag_scan_workspace_bytes_cfg(batch, length, rank * channels, tile). */
+int mogt_coupled_rank_scan_fwd_cfg(const void* z, const void* v, void* h,
+                                   int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                   float damping, int z_dtype, int v_dtype, int out_dtype,
+                                   int vec, int lanes, int steps, int waves,
+                                   void* workspace, size_t workspace_bytes, void* stream);
 /* Reverse scan of the coupled scan's backward: G_t = dh_t + a_{t+1} G_{t+1},
  * G_L = 0, with a_t = damping * (1 - sigmoid(z[b,t,i])) over rank i's C
  * channels, formed from the gate logits z [B, L, R] (fp32 or bf16) inside the

@@ -112,6 +112,36 @@ extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                        t, workspace, workspace_bytes, stream);
 }
 
+// The same with an explicit tile (sweeps and tests): the tile must be one of
+// mogt_diag_scan_tiles(2), its vector must divide the channel count, and v and
+// h must be aligned to the vector (at most 16 bytes).  Workspace:
+// mogt_diag_scan_workspace_bytes_cfg(batch, length, rank * channels, tile).
+extern "C" int mogt_coupled_rank_scan_fwd_cfg(const void* z, const void* v, void* h, int64_t batch,
+                                              int64_t length, int64_t rank, int64_t channels, float damping,
+                                              int z_dtype, int v_dtype, int out_dtype, int vec, int lanes,
+                                              int steps, int waves, void* workspace, size_t workspace_bytes,
+                                              void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "rank and channels must be positive");
+    if (!dtype_ok(z_dtype) || !dtype_ok(v_dtype) || !dtype_ok(out_dtype))
+        return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    const DiagTile t{vec, lanes, steps, waves};
+    if (!diag_tile_compiled(2, t))
+        return set_error(MOGT_E_INVALID, "coupled scan: tile (%d,%d,%d,%d) not compiled", vec, lanes, steps, waves);
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!z || !v || !h) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    auto aligned = [&](const void* p, int dt) {
+        const uintptr_t bytes = static_cast<uintptr_t>(vec) * (dt == MOGT_BF16 ? 2 : 4);
+        return reinterpret_cast<uintptr_t>(p) % (bytes < 16 ? bytes : 16) == 0;
+    };
+    if (!aligned(v, v_dtype) || !aligned(h, out_dtype))
+        return set_error(MOGT_E_INVALID, "v and h must be aligned to the tile's vector");
+    return coupled_run(z, v, h, batch, length, rank, channels, damping, z_dtype, v_dtype, out_dtype, t, workspace,
+                       workspace_bytes, stream);
+}
+
 // ---------------------------------------------------------------------------
 // Gradient epilogue of the coupled scan (the backward of
 // mogt_coupled_rank_scan_fwd, after the reverse scan has produced

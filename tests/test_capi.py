@@ -111,10 +111,11 @@ def test_tile_lists(lib):
 
 
 def test_gpu_tile_lists_match_library(lib):
-    from test_gpu_diag_scan import TILES_BF16, TILES_F32
+    from test_gpu_diag_scan import TILES_BF16, TILES_COUPLED, TILES_F32
 
     assert _lib.diag_tiles(0) == TILES_F32
     assert _lib.diag_tiles(1) == TILES_BF16
+    assert _lib.diag_tiles(2) == TILES_COUPLED
 
 
 def test_check_maps_codes_to_python_errors(lib):

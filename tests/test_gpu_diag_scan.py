@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from conftest import announce, rel_err, to_np
-from mogt_amd import synthetic
+from mogt_amd import _lib, synthetic
 from oracle import scan_oracle as so
 
 pytestmark = pytest.mark.gpu
@@ -24,6 +24,8 @@ TILES_F32 = [(2, 32, 32, 8), (2, 32, 16, 16), (2, 32, 16, 8), (2, 32, 32, 4), (2
              (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
 TILES_BF16 = [(4, 16, 16, 8), (4, 16, 16, 16), (4, 16, 8, 8), (4, 32, 16, 8), (2, 32, 16, 8),
               (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
+TILES_COUPLED = [(4, 16, 8, 16), (4, 16, 8, 8), (4, 16, 16, 16), (4, 32, 8, 16), (2, 32, 16, 8), (2, 32, 16, 16),
+                 (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
 
 
 def _run_cfg(a, b, out_dtype, cfg, prefix=False):
@@ -195,6 +197,40 @@ def test_coupled_rank_scan(gpu, L, r, c, vdt):
     err = np.abs(to_np(h).astype(np.float64) - ref) / np.max(np.abs(ref))
     assert float(err.max()) <= tol
     assert float(np.median(err)) <= 1e-6   # the bulk is exact to fp32 accumulation
+
+
+@pytest.mark.parametrize("vdt", ["fp32", "bf16"])
+@pytest.mark.parametrize("tile", TILES_COUPLED)
+def test_every_coupled_tile(gpu, tile, vdt):
+    """Every compiled coupled tile through the tile-override entry point: ragged
+    L, two sequences, 48 channels per gate (divisible by every vector width);
+    bf16 z, bf16 output for half of the cases."""
+    announce(f"coupled tile {tile} v={vdt}")
+    from mogt_amd import ops
+
+    B, L, r, c = 2, 2777, 4, 48
+    z, v = synthetic.coupled_inputs(B, L, r, c, seed=sum(tile))
+    zt, vt = torch.from_numpy(z).to(gpu), torch.from_numpy(v).to(gpu)
+    if vdt == "bf16":
+        vt = vt.bfloat16()
+    zb = tile[0] % 2 == 0 and vdt == "bf16"   # bf16 gate logits on some cases
+    if zb:
+        zt = zt.bfloat16()
+    ob = tile[2] % 16 == 0                     # bf16 output on some cases
+    h = torch.empty(B, L, r * c, device=gpu, dtype=torch.bfloat16 if ob else torch.float32)
+    lib = _lib.load()
+    nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, r * c, *tile)
+    ws = ops.workspace(nbytes, zt.device)
+    rc = lib.mogt_coupled_rank_scan_fwd_cfg(zt.data_ptr(), vt.data_ptr(), h.data_ptr(), B, L, r, c, 0.999,
+                                            ops.dtype_code(zt.dtype, "z"), ops.dtype_code(vt.dtype, "v"),
+                                            ops.dtype_code(h.dtype, "h"), *tile, ws.data_ptr(), ws.numel(),
+                                            ops._stream_handle(zt.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_fwd_cfg")
+    torch.cuda.synchronize()
+    ref = so.coupled_rank_scan(to_np(zt), to_np(vt), r, damping=0.999, v_is_bf16=(vdt == "bf16"))
+    tol = FP32_TOL if (vdt == "fp32" and not ob) else BF16_TOL
+    assert rel_err(to_np(h), ref) <= tol
+    assert ops.workspace_faults() == 0
 
 
 def test_mixed_modes_share_workspace(gpu):
