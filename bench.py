@@ -42,9 +42,10 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--only", choices=["diag", "rank1", "dense", "all"], default="all",
+    p.add_argument("--only", choices=["diag", "rank1", "dense", "backbone", "all"], default="all",
                    help="after the headline: every extra (all), none (diag), or only the rank-1 "
-                        "(configs[2]) or dense (core shape and configs[3]) lines")
+                        "(configs[2]), dense (core shape and configs[3]) or backbone (configs[4] "
+                        "forward and training step) lines")
     p.add_argument("--tile", default=None,
                    help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
@@ -717,6 +718,7 @@ def main():
                 "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
                         "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
                         "torch ops on the same GPU"}
+        if full or args.only == "backbone":
             r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
             extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
                 r, ffn_hidden=3072, vocab=32000,
