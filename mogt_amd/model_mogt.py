@@ -36,6 +36,30 @@ def _autocast_dtype() -> torch.dtype | None:
     return None
 
 
+def _gemm_weight(owner: nn.Module, name: str, params: tuple, build):
+    """A GEMM operand built from parameters (a concatenation of weights, cast
+    to the autocast dtype when autocast is on -- the cast F.linear would make).
+    Without gradient recording it is cached on ``owner`` until a parameter
+    changes (storage or version counter), the autocast dtype or the inference
+    mode flag changes; with gradients it is rebuilt on every call so autograd
+    reaches the parameters."""
+    ad = _autocast_dtype()
+
+    def make():
+        w = build()
+        return w.to(ad) if ad is not None and w.is_floating_point() else w
+
+    if torch.is_grad_enabled():
+        return make()
+    key = (tuple((p.data_ptr(), p._version, p.dtype) for p in params), ad, torch.is_inference_mode_enabled())
+    cache = owner.__dict__.setdefault("_gemm_weight_cache", {})
+    hit = cache.get(name)
+    if hit is None or hit[0] != key:
+        hit = (key, make())
+        cache[name] = hit
+    return hit[1]
+
+
 class RMSNorm(nn.Module):
     """x * rsqrt(mean(x^2) + eps), computed in fp32, ``type_as(x)``, times
     ``weight`` (model_mogt.py:9-20)."""
@@ -66,8 +90,10 @@ class SwiGLU(nn.Module):
     def forward(self, x):
         # one GEMM against [w1; w2], then the fused gate (autograd through the
         # silu_mul backward kernel and torch.cat back to w1, w2)
-        w12 = torch.cat([self.w1.weight, self.w2.weight], dim=0)
-        return self.w3(ops.silu_mul(F.linear(x, w12)))
+        w12 = _gemm_weight(self, "w12", (self.w1.weight, self.w2.weight),
+                           lambda: torch.cat([self.w1.weight, self.w2.weight], dim=0))
+        w3 = _gemm_weight(self, "w3", (self.w3.weight,), lambda: self.w3.weight)
+        return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
 
 
 def reference_ffn_hidden(d_model: int) -> int:
@@ -264,7 +290,8 @@ class MOGTBlock(nn.Module):
         if "prev" in mode:
             parts.append(W[:, off:off + D])
             off += D
-        y = F.linear(xn, torch.cat(parts, dim=0)).float()   # [B, L, r * n_parts]
+        Wg = _gemm_weight(self, "gate", (W,), lambda: torch.cat(parts, dim=0))
+        y = F.linear(xn, Wg).float()   # [B, L, r * n_parts]
         r = self.r
         z = y[..., :r]
         if "prev" in mode:
@@ -290,19 +317,19 @@ class MOGTBlock(nn.Module):
             x, xn = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_mogt.weight, eps,
                                     out_dtype=gemm_dtype)
         with torch.autograd.profiler.record_function("mogt.value_projection"):
-            v_raw = F.linear(xn, self.phi_val.weight)
+            v_raw = F.linear(xn, _gemm_weight(self, "phi_val", (self.phi_val.weight,), lambda: self.phi_val.weight))
             z = self._gate_logits(xn, prefix_condition)
         with torch.autograd.profiler.record_function("mogt.affine_scan"):
             h = ops.coupled_rank_scan(z, v_raw, damping=float(getattr(self, "connection_damping", 0.999)),
                                       out_dtype=torch.float32)
         with torch.autograd.profiler.record_function("mogt.readout"):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
-            Z = F.linear(hn, self.theta_read.weight)
+            Z = F.linear(hn, _gemm_weight(self, "theta_read", (self.theta_read.weight,),
+                                          lambda: self.theta_read.weight))
         with torch.autograd.profiler.record_function("mogt.ffn"):
             x, xn2 = ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight,
                                      self.norm_ffn.eps, out_dtype=gemm_dtype)
-            f = self.ffn.w3(ops.silu_mul(F.linear(xn2, torch.cat([self.ffn.w1.weight,
-                                                                  self.ffn.w2.weight], dim=0))))
+            f = self.ffn(xn2)
         return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
 
 

@@ -242,3 +242,40 @@ def test_bf16_training_regression(gpu, monkeypatch):
         diffs[k] = float((ps[k].float() - ph[k].float()).abs().max().detach())
     assert max(diffs.values()) <= 5e-4, diffs
     assert ph["mogt.blocks.0.theta_read.weight"].grad.abs().sum() > 0
+
+
+def test_inference_weight_cache_follows_parameter_updates(gpu):
+    """Inference forwards reuse the cast / concatenated GEMM weights; an in-place
+    parameter update (optimizer step, load_state_dict) must invalidate them."""
+    announce("inference GEMM-weight cache invalidation")
+    from mogt_amd.model_mogt import MOGTModel, configure_coupled_gate
+
+    torch.manual_seed(5)
+    model = MOGTModel(vocab_size=300, d_model=64, num_layers=2, r=16).to(gpu)
+    configure_coupled_gate(model, zero_gate_weight=False)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" not in name and not name.endswith("bias"):
+                p.normal_(0.0, 0.05)
+    ids = torch.randint(0, 300, (1, 256), device=gpu)
+
+    def run():
+        with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(ids).float().clone()
+
+    y1 = run()
+    assert torch.equal(run(), y1)                       # cached weights: same result
+    with torch.no_grad():
+        for p in model.parameters():
+            p.mul_(0.9)
+    y2 = run()
+    for m in model.modules():
+        m.__dict__.pop("_gemm_weight_cache", None)
+    y3 = run()
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y3) and not torch.equal(y1, y2)
+    model.load_state_dict({k: v * 1.1 for k, v in model.state_dict().items()})
+    y4 = run()
+    for m in model.modules():
+        m.__dict__.pop("_gemm_weight_cache", None)
+    assert torch.equal(y4, run())
