@@ -223,12 +223,14 @@ int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, in
  *   (fp32 [rows, dim], may be null) is the residual stream's own gradient of
  *   add_rmsnorm (x fp32).  dw_partial: fp32 [ceil(rows / rows_per_wave), dim]
  *   partial sums of dy * n.type_as(x); the caller sums them over rows.
+ *   dz (may be null): also writes dz = dx * dz_scale in dz_dtype, the
+ *   gradient of add_rmsnorm's scaled residual term x + scale * z.
  * mogt_silu_mul_bwd: y = [rows, 2*hidden] (forward input), dout = [rows,
  *   hidden]; dy = [rows, 2*hidden] = [dout*b*silu'(a) | dout*silu(a)],
  *   rounded where torch's bf16 autograd rounds.                            */
 int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const float* dres, void* dx,
                      float* dw_partial, int64_t rows, int64_t dim, float eps, int rows_per_wave,
-                     int x_dtype, int dy_dtype, void* stream);
+                     int x_dtype, int dy_dtype, void* dz, float dz_scale, int dz_dtype, void* stream);
 int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, int64_t hidden,
                       int dtype, void* stream);
 

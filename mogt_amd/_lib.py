@@ -93,7 +93,7 @@ SIGNATURES: dict[str, tuple] = {
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "mogt_rmsnorm_bwd": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
-                 _c_int, _c_int, _c_int, _c_void_p]),
+                 _c_int, _c_int, _c_int, _c_void_p, _c_float, _c_int, _c_void_p]),
     "mogt_silu_mul_bwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "mogt_connection_map_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),

@@ -133,7 +133,7 @@ template <typename TX, typename TG, int VPL>
 __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
     const TX* __restrict__ x, const float* __restrict__ w, const TG* __restrict__ dy,
     const float* __restrict__ dres, TX* __restrict__ dx, float* __restrict__ dw_part, int64_t rows, int D,
-    float eps, int rows_per_wave) {
+    float eps, int rows_per_wave, void* __restrict__ dz, float dz_scale, int dz_bf16) {
     const int lane = threadIdx.x & 63;
     const int64_t gw = static_cast<int64_t>(blockIdx.x) * NA_WAVES + (threadIdx.x >> 6);
     const int64_t r0 = gw * rows_per_wave;
@@ -193,6 +193,15 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o[e] = r * (g[k][e] - v[k][e] * r * mdot) + rr[k][e];
                 store_vec<TX, 4>(dx + row * D + c, o);
+                if (dz) {   // the gradient of the scaled term: (dx * scale) in z's dtype
+                    float oz[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) oz[e] = rnd<TX>(o[e]) * dz_scale;
+                    if (dz_bf16)
+                        store_vec<bf16_t, 4>(static_cast<bf16_t*>(dz) + row * D + c, oz);
+                    else
+                        store_vec<float, 4>(static_cast<float*>(dz) + row * D + c, oz);
+                }
             }
         }
         if (row + 1 < r1) {
@@ -263,7 +272,8 @@ dim3 swiglu_grid(int64_t rows, int64_t hidden, int vec) {
 
 template <typename TX, typename TG>
 int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* dres, void* dx, float* dw_part,
-                    int64_t rows, int D, float eps, int rpw, hipStream_t st) {
+                    int64_t rows, int D, float eps, int rpw, void* dz, float dz_scale, int dz_bf16,
+                    hipStream_t st) {
     const int vpl = (D + 255) / 256;
     const int64_t waves = (rows + rpw - 1) / rpw;
     const dim3 grid(static_cast<unsigned>((waves + NA_WAVES - 1) / NA_WAVES));
@@ -274,7 +284,7 @@ int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* 
 #define MOGT_NORM_BWD_CASE(V)                                                                     \
     if (vpl <= V) {                                                                                \
         hipLaunchKernelGGL((rmsnorm_bwd_kernel<TX, TG, V>), grid, block, 0, st, xp, w, gp, dres, dxp, \
-                           dw_part, rows, D, eps, rpw);                                             \
+                           dw_part, rows, D, eps, rpw, dz, dz_scale, dz_bf16);                      \
         return check_launch("rmsnorm_bwd_kernel");                                                 \
     }
     MOGT_NORM_BWD_CASE(1)
@@ -392,11 +402,13 @@ extern "C" int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t
 
 extern "C" int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const float* dres, void* dx,
                                 float* dw_partial, int64_t rows, int64_t dim, float eps, int rows_per_wave,
-                                int x_dtype, int dy_dtype, void* stream) {
+                                int x_dtype, int dy_dtype, void* dz, float dz_scale, int dz_dtype,
+                                void* stream) {
     clear_error();
     int rc = check_norm_args(rows, dim);
     if (rc) return rc;
-    if (!dt_ok(x_dtype) || !dt_ok(dy_dtype)) return set_error(MOGT_E_INVALID, "rmsnorm_bwd: dtype");
+    if (!dt_ok(x_dtype) || !dt_ok(dy_dtype) || (dz && !dt_ok(dz_dtype)))
+        return set_error(MOGT_E_INVALID, "rmsnorm_bwd: dtype");
     if (rows_per_wave <= 0) return set_error(MOGT_E_INVALID, "rmsnorm_bwd: rows_per_wave must be positive");
     if (dres && x_dtype != MOGT_F32)
         return set_error(MOGT_E_INVALID, "rmsnorm_bwd: a residual gradient needs the fp32 residual stream");
@@ -405,12 +417,16 @@ extern "C" int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* 
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int D = static_cast<int>(dim);
     if (x_dtype == MOGT_F32 && dy_dtype == MOGT_F32)
-        return launch_norm_bwd<float, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+        return launch_norm_bwd<float, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, dz,
+                                         dz_scale, dz_dtype == MOGT_BF16, st);
     if (x_dtype == MOGT_F32)
-        return launch_norm_bwd<float, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+        return launch_norm_bwd<float, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, dz,
+                                         dz_scale, dz_dtype == MOGT_BF16, st);
     if (dy_dtype == MOGT_F32)
-        return launch_norm_bwd<bf16_t, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
-    return launch_norm_bwd<bf16_t, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, st);
+        return launch_norm_bwd<bf16_t, float>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, dz,
+                                         dz_scale, dz_dtype == MOGT_BF16, st);
+    return launch_norm_bwd<bf16_t, bf16_t>(x, weight, dy, dres, dx, dw_partial, rows, D, eps, rows_per_wave, dz,
+                                         dz_scale, dz_dtype == MOGT_BF16, st);
 }
 
 extern "C" int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, int64_t hidden,

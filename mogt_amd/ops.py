@@ -653,9 +653,8 @@ def _rows_per_wave(rows: int) -> int:
     return max(4, -(-rows // 2048))
 
 
-@torch.library.custom_op("mogt::rmsnorm_bwd", mutates_args=())
-def _rmsnorm_bwd_op(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dres: torch.Tensor | None,
-                    eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+def _rmsnorm_bwd_launch(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dres: torch.Tensor | None,
+                        eps: float, dz: torch.Tensor | None, dz_scale: float):
     lib = _lib.load()
     x = x.contiguous()
     dy = dy.contiguous()
@@ -670,15 +669,40 @@ def _rmsnorm_bwd_op(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dre
     rc = lib.mogt_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
                               dres.data_ptr() if dres is not None else None, dx.data_ptr(),
                               parts.data_ptr(), rows, D, float(eps), rpw, dtype_code(x.dtype, "rmsnorm_bwd"),
-                              dtype_code(dy.dtype, "rmsnorm_bwd"), _stream_handle(x.device))
+                              dtype_code(dy.dtype, "rmsnorm_bwd"), dz.data_ptr() if dz is not None else None,
+                              float(dz_scale), dtype_code(dz.dtype, "rmsnorm_bwd") if dz is not None else 0,
+                              _stream_handle(x.device))
     _lib.check(rc, "mogt_rmsnorm_bwd")
     dw = parts.sum(0) if rows > 0 else torch.zeros(D, dtype=torch.float32, device=x.device)
     return dx, dw
 
 
+@torch.library.custom_op("mogt::rmsnorm_bwd", mutates_args=())
+def _rmsnorm_bwd_op(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dres: torch.Tensor | None,
+                    eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    return _rmsnorm_bwd_launch(x, weight, dy, dres, eps, None, 0.0)
+
+
 @_rmsnorm_bwd_op.register_fake
 def _(x, weight, dy, dres, eps):
     return torch.empty_like(x), x.new_empty(x.shape[-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("mogt::add_rmsnorm_bwd", mutates_args=())
+def _add_rmsnorm_bwd_op(x_out: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, dres: torch.Tensor | None,
+                        eps: float, scale: float, z_dtype: torch.dtype
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of add_rmsnorm in one pass: dx (the residual stream), dz =
+    (dx * scale) in z's dtype, and dw."""
+    dz = torch.empty(x_out.shape, dtype=z_dtype, device=x_out.device)
+    dx, dw = _rmsnorm_bwd_launch(x_out, weight, dy, dres, eps, dz, scale)
+    return dx, dz, dw
+
+
+@_add_rmsnorm_bwd_op.register_fake
+def _(x_out, weight, dy, dres, eps, scale, z_dtype):
+    return (torch.empty_like(x_out), x_out.new_empty(x_out.shape, dtype=z_dtype),
+            x_out.new_empty(x_out.shape[-1], dtype=torch.float32))
 
 
 def _rmsnorm_setup(ctx, inputs, output):
@@ -708,8 +732,8 @@ def _add_rmsnorm_backward(ctx, g_xout, g_out):
     x_out, weight = ctx.saved_tensors
     if g_out is None:
         g_out = torch.zeros_like(x_out)
-    dx, dw = torch.ops.mogt.rmsnorm_bwd(x_out, weight, g_out, g_xout, ctx.eps)
-    dz = (dx * ctx.scale).to(ctx.z_dtype)
+    dx, dz, dw = torch.ops.mogt.add_rmsnorm_bwd(x_out, weight, g_out, g_xout, ctx.eps, float(ctx.scale),
+                                                ctx.z_dtype)
     return dx, dz, None, dw.to(weight.dtype), None, None
 
 

@@ -91,7 +91,7 @@ def test_empty_problems_are_noops_without_device(lib):
         "rmsnorm": lambda: lib.mogt_rmsnorm_fwd(N, N, N, 0, 64, 1e-6, 0, 0, N),
         "add_rmsnorm": lambda: lib.mogt_add_rmsnorm_fwd(N, N, 0.5, N, N, N, 0, 64, 1e-6, 0, 0, N),
         "silu_mul": lambda: lib.mogt_silu_mul_fwd(N, N, 0, 64, 0, N),
-        "rmsnorm_bwd": lambda: lib.mogt_rmsnorm_bwd(N, N, N, N, N, N, 0, 64, 1e-6, 4, 0, 0, N),
+        "rmsnorm_bwd": lambda: lib.mogt_rmsnorm_bwd(N, N, N, N, N, N, 0, 64, 1e-6, 4, 0, 0, N, 1.0, 0, N),
         "silu_mul_bwd": lambda: lib.mogt_silu_mul_bwd(N, N, N, 0, 64, 0, N),
         "connection_map": lambda: lib.mogt_connection_map_fwd(N, N, 0, 16, 1.0, 1.0, 0, 0, N),
         "lm_ce_bwd": lambda: lib.mogt_lm_ce_bwd(N, 32, 0, N, N, 0, 32, -100, N, N, 32, 0, N),
