@@ -1,0 +1,33 @@
+"""Host-side logic that needs no GPU: the GEMM-weight cache of the MOGT
+blocks (built from parameters, reused only while no gradient is recorded and
+no parameter changed)."""
+import torch
+import torch.nn as nn
+
+from mogt_amd.model_mogt import _gemm_weight
+
+
+def test_gemm_weight_cache_reuse_and_invalidation():
+    torch.manual_seed(0)
+    owner = nn.Module()
+    a, b = nn.Linear(4, 3, bias=False), nn.Linear(4, 2, bias=False)
+    build = lambda: torch.cat([a.weight, b.weight], dim=0)
+    with torch.no_grad():
+        w1 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+        assert _gemm_weight(owner, "ab", (a.weight, b.weight), build) is w1   # reused
+        a.weight.mul_(2.0)                                                    # version bump
+        w2 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+        assert w2 is not w1 and torch.equal(w2, build())
+        b.weight.data = torch.randn(2, 4)                                     # new storage
+        w3 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+        assert w3 is not w2 and torch.equal(w3, build())
+    with torch.inference_mode():
+        w4 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+        assert w4 is not w3                                                   # inference-mode entry of its own
+        assert _gemm_weight(owner, "ab", (a.weight, b.weight), build) is w4
+    # with gradients: rebuilt every call and differentiable to the parameters
+    g1 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+    g2 = _gemm_weight(owner, "ab", (a.weight, b.weight), build)
+    assert g1 is not g2 and g1.grad_fn is not None
+    g1.sum().backward()
+    assert torch.equal(a.weight.grad, torch.ones(3, 4)) and torch.equal(b.weight.grad, torch.ones(2, 4))
