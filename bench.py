@@ -42,10 +42,10 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--only", choices=["diag", "rank1", "dense", "backbone", "all"], default="all",
-                   help="after the headline: every extra (all), none (diag), or only the rank-1 "
-                        "(configs[2]), dense (core shape and configs[3]) or backbone (configs[4] "
-                        "forward and training step) lines")
+    p.add_argument("--only", choices=["diag", "coupled", "rank1", "dense", "backbone", "all"], default="all",
+                   help="after the headline: every extra (all), none (diag), or only the coupled "
+                        "mixer scan, rank-1 (configs[2]), dense (core shape and configs[3]) or "
+                        "backbone (configs[4] forward and training step) lines")
     p.add_argument("--tile", default=None,
                    help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
@@ -665,6 +665,7 @@ def main():
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                 "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
+        if full or args.only == "coupled":
             r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
             extras["coupled_rank_scan_r16c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
