@@ -105,8 +105,27 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     __shared__ float s_inH[FW];
 
     const int blk = blockIdx.x;
-    const int pos = blk / p.G;                 // chunk position along L
-    const int g = blk - pos * p.G;             // chain
+    // Block -> (chunk position, chain).  Position-major by default.  GATED:
+    // positions in groups of 8, block b of a group at position b % 8, so the
+    // chains of one position share b % 8 -- one XCD under round-robin dispatch,
+    // which then fetches that position's gate-logit rows once instead of once
+    // per XCD.  Either way a chain's chunks have increasing block ids.
+    int pos, g;
+    if constexpr (GATED) {
+        const int full = (p.n_ch / 8) * 8 * p.G;   // blocks of whole groups of 8 positions
+        if (blk < full) {
+            const int grp = blk / (8 * p.G), rem = blk - grp * 8 * p.G;
+            g = rem / 8;
+            pos = 8 * grp + (rem - g * 8);
+        } else {
+            const int rel = blk - full;
+            pos = (p.n_ch / 8) * 8 + rel / p.G;
+            g = rel - (rel / p.G) * p.G;
+        }
+    } else {
+        pos = blk / p.G;
+        g = blk - pos * p.G;
+    }
     const int bi = g / p.n_fg;
     const int fg = g - bi * p.n_fg;
 
