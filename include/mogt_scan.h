@@ -43,6 +43,17 @@ const char* mogt_last_error(void);
 /* ABI version of the loaded library (bumped on incompatible changes). */
 int mogt_abi_version(void);
 
+/* Health of a single-pass scan workspace (the diag, coupled and reverse
+ * scans' look-back buffer): *count receives the number of bounded waits that
+ * gave up in launches on it since it was zero-filled.  It must be 0; a
+ * look-back that gives up also writes NaN into its chunk's carry, so the
+ * outputs it affected are visibly invalid.  Copies 4 bytes on `stream` and
+ * waits for the stream (a debugging / checked-mode query).  The reference has
+ * no counterpart: its scans (triton_scan.py:232-311) have no cross-block
+ * protocol that could fail.                                                 */
+int mogt_workspace_faults(const void* workspace, size_t workspace_bytes, uint32_t* count,
+                          void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Diagonal affine scan  h_t = a_t * h_{t-1} + b_t,  h_0 = 0, per feature.
  *

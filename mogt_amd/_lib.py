@@ -16,7 +16,7 @@ MOGT_F32 = 0
 MOGT_BF16 = 1
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -28,6 +28,7 @@ _c_float = ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
     "mogt_last_error": (ctypes.c_char_p, []),
     "mogt_abi_version": (_c_int, []),
+    "mogt_workspace_faults": (_c_int, [_c_void_p, _c_size, ctypes.POINTER(ctypes.c_uint32), _c_void_p]),
     "mogt_diag_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
     "mogt_diag_scan_fwd": (
         _c_int,

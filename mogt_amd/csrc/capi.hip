@@ -31,4 +31,22 @@ int check_launch(const char* what) {
 
 extern "C" const char* mogt_last_error(void) { return mogt::g_last_error; }
 
-extern "C" int mogt_abi_version(void) { return 2; }
+extern "C" int mogt_abi_version(void) { return 3; }
+
+extern "C" int mogt_workspace_faults(const void* workspace, size_t workspace_bytes, uint32_t* count,
+                                     void* stream) {
+    mogt::clear_error();
+    if (!workspace || !count) return mogt::set_error(MOGT_E_INVALID, "null workspace or count pointer");
+    if (workspace_bytes < mogt::WS_HDR_BYTES)
+        return mogt::set_error(MOGT_E_WORKSPACE, "workspace of at least %zu bytes expected, got %zu",
+                               mogt::WS_HDR_BYTES, workspace_bytes);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const char* hdr = static_cast<const char*>(workspace);
+    // header word 3: bounded waits that gave up (common.h)
+    hipError_t e = hipMemcpyAsync(count, hdr + 3 * sizeof(uint32_t), sizeof(uint32_t),
+                                  hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess)
+        return mogt::set_error(MOGT_E_LAUNCH, "mogt_workspace_faults: %s", hipGetErrorString(e));
+    return MOGT_OK;
+}

@@ -80,6 +80,9 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 //   hdr[2]  epoch (30 bits), read once by every work-group.
 //   hdr[3]  count of bounded waits that gave up (must stay 0; a non-zero value
 //           means the protocol was violated and the output is not valid).
+//           A look-back that gives up also writes NaN into its chunk's carry,
+//           so the affected outputs are visibly invalid; the count is read
+//           back with mogt_workspace_faults().
 //
 // Every published value is a 64-bit word {tag:32 | f32 bits:32} written with a
 // single agent-scope atomic store, tag = epoch << 2 | status.  A reader accepts

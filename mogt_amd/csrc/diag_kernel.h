@@ -342,7 +342,13 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
             __syncthreads();
             if (!s_pending[par]) break;
             if (++rounds > MAX_SPIN) {
+                // Gave up: the carry is unknown.  Count it and poison the
+                // carry, so this chunk's outputs and every later chunk of the
+                // chain (which fold this chunk's published prefix) read NaN
+                // instead of a silently wrong partial carry.
                 if (tid == 0) note_timeout(p.hdr);
+                cA = __builtin_nanf("");
+                cH = __builtin_nanf("");
                 break;
             }
             __builtin_amdgcn_s_sleep(1);

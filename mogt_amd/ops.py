@@ -8,6 +8,8 @@ the kernels leave reusable after every launch.
 """
 from __future__ import annotations
 
+import ctypes
+import os
 import threading
 
 import torch
@@ -18,6 +20,20 @@ _DTYPE_CODE = {torch.float32: _lib.MOGT_F32, torch.bfloat16: _lib.MOGT_BF16}
 
 _ws_lock = threading.Lock()
 _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+# Workspaces replaced by a larger one.  They are kept alive for the life of the
+# process: a HIP graph captured earlier still holds their address, and freeing
+# them would let the allocator hand the memory to another tensor that the
+# graph's replays would then overwrite.  Growth is geometric, so the retired
+# buffers together are smaller than the live one.
+_ws_retired: list[torch.Tensor] = []
+
+# Checked mode: after every single-pass scan, read the workspace's give-up
+# counter (a device synchronisation) and raise if it is non-zero.
+CHECK_WORKSPACE = os.environ.get("MOGT_CHECK_WORKSPACE", "0") not in ("", "0")
+
+
+class WorkspaceFault(RuntimeError):
+    """A single-pass scan's look-back gave up: its output is not valid."""
 
 
 def dtype_code(dt: torch.dtype, what: str) -> int:
@@ -46,21 +62,38 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
             size = max(int(nbytes), 1 << 16)
             if buf is not None:
                 size = max(size, 2 * buf.numel())
+                _ws_retired.append(buf)
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
         return buf
 
 
+def _faults_of(buf: torch.Tensor) -> int:
+    lib = _lib.load()
+    count = ctypes.c_uint32(0)
+    rc = lib.mogt_workspace_faults(buf.data_ptr(), buf.numel(), ctypes.byref(count),
+                                   _stream_handle(buf.device))
+    _lib.check(rc, "mogt_workspace_faults")
+    return int(count.value)
+
+
 def workspace_faults() -> int:
     """Number of bounded look-back waits that gave up, summed over every cached
-    workspace (header word 3).  Always 0 unless the protocol was violated;
-    synchronises the device."""
+    workspace (read through ``mogt_workspace_faults``).  Always 0 unless the
+    protocol was violated, in which case the affected outputs also hold NaN.
+    Synchronises the streams involved."""
     with _ws_lock:
-        bufs = list(_ws_cache.values())
-    total = 0
-    for buf in bufs:
-        total += int(buf[12:16].view(torch.int32).item())
-    return total
+        bufs = list(_ws_cache.values()) + list(_ws_retired)
+    return sum(_faults_of(b) for b in bufs)
+
+
+def _checked(ws: torch.Tensor, what: str) -> None:
+    """In checked mode (MOGT_CHECK_WORKSPACE=1) raise if the launch that just
+    used ``ws`` gave up a look-back wait."""
+    if CHECK_WORKSPACE and not torch.cuda.is_current_stream_capturing():
+        n = _faults_of(ws)
+        if n:
+            raise WorkspaceFault(f"{what}: {n} look-back wait(s) gave up; the output is invalid (NaN)")
 
 
 def require_cuda(what: str, *tensors: torch.Tensor) -> None:
@@ -94,6 +127,7 @@ def _diag_scan_launch(a: torch.Tensor, b: torch.Tensor, h: torch.Tensor,
                                         in_code, out_code, cfg[0], cfg[1], cfg[2], cfg[3],
                                         ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "mogt_diag_scan_fwd")
+    _checked(ws, "mogt_diag_scan_fwd")
 
 
 def _check_diag_inputs(a: torch.Tensor, b: torch.Tensor) -> None:
@@ -150,6 +184,7 @@ def _diag_scan_rev_op(a: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
     rc = lib.mogt_diag_scan_rev_fwd(a.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, D,
                                     ws.data_ptr(), ws.numel(), _stream_handle(a.device))
     _lib.check(rc, "mogt_diag_scan_rev_fwd")
+    _checked(ws, "mogt_diag_scan_rev_fwd")
     return out
 
 
@@ -227,6 +262,7 @@ def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: 
                                         float(damping), zc, vc, oc, ws.data_ptr(), ws.numel(),
                                         _stream_handle(v.device))
     _lib.check(rc, "mogt_coupled_rank_scan_fwd")
+    _checked(ws, "mogt_coupled_rank_scan_fwd")
     return h
 
 
@@ -250,6 +286,7 @@ def _coupled_scan_rev_op(z: torch.Tensor, grad_h: torch.Tensor, rank: int, dampi
                                             float(damping), dtype_code(z.dtype, "coupled_scan_rev"), ws.data_ptr(),
                                             ws.numel(), _stream_handle(g.device))
     _lib.check(rc, "mogt_coupled_rank_scan_rev_fwd")
+    _checked(ws, "mogt_coupled_rank_scan_rev_fwd")
     return out
 
 

@@ -145,3 +145,13 @@ def test_library_is_plain_c_abi():
     out = subprocess.run(["nm", "-D", "--undefined-only", str(_lib.library_path())],
                          capture_output=True, text=True).stdout
     assert "torch" not in out and "c10" not in out
+
+
+def test_workspace_fault_query_validates_arguments(lib):
+    import ctypes
+
+    count = ctypes.c_uint32(7)
+    assert lib.mogt_workspace_faults(None, 4096, ctypes.byref(count), None) == -1
+    assert b"null" in lib.mogt_last_error()
+    assert lib.mogt_workspace_faults(1, 16, ctypes.byref(count), None) == -2
+    assert b"workspace" in lib.mogt_last_error()
