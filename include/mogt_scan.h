@@ -85,6 +85,19 @@ int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix
                            void* workspace, size_t workspace_bytes, void* stream);
 int mogt_diag_scan_tiles(int family, int* out, int max_tiles);
 
+/* mogt_diag_scan_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * look-back state lives in a fixed 8 MiB device array of the library, one per
+ * GPU, held until the process ends (problems needing more are rejected with
+ * MOGT_E_INVALID; at the default tiles that is about 2.6e8 elements of B*L*D).
+ * The first call on a device clears the array on `stream`.  Calls on one GPU
+ * share the array: calls that may overlap in time (different streams) race
+ * and must not be issued.  Same results as mogt_diag_scan_fwd.               */
+int mogt_diag_scan_fwd_noalloc(const void* a, const void* b, void* h, void* a_prefix,
+                               int64_t batch, int64_t length, int64_t features,
+                               int in_dtype, int out_dtype, void* stream);
+
 /* Reverse-time diagonal scan h_t = a_{t+1} * h_{t+1} + b_t, h_L = 0 (a_L
  * unused), fp32 a, b, h [B, L, D]: with b = dH it is the gradient
  * G_t = dH_t + a_{t+1} G_{t+1} of the diagonal scan, the R = C = 1 case of

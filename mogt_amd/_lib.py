@@ -45,6 +45,10 @@ SIGNATURES: dict[str, tuple] = {
          _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
     "mogt_diag_scan_tiles": (_c_int, [_c_int, ctypes.POINTER(_c_int), _c_int]),
+    "mogt_diag_scan_fwd_noalloc": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_void_p],
+    ),
     "mogt_coupled_rank_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
     "mogt_coupled_rank_scan_fwd": (
         _c_int,

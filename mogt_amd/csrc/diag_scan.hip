@@ -1,5 +1,7 @@
 // C entry points of the single-pass diagonal affine scan (kernel: diag_kernel.h;
 // instantiations: diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
+#include <mutex>
+
 #include "diag_kernel.h"
 
 namespace mogt {
@@ -83,6 +85,53 @@ int common_alignment(const void* a, const void* b, const void* h, const void* p,
     return 1;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation entry point: the look-back workspace lives in a
+// file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes `scratch` itself (in host code it names a host-side
+// stand-in); it passes the device address that hipGetSymbolAddress returned
+// for the current device.
+// ---------------------------------------------------------------------------
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+
+__global__ __launch_bounds__(256) void clear_scratch_kernel(uint4* p, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Device address of the current device's scratch; on the first call for a
+// device it is looked up and the whole array is cleared on `stream` (a fill
+// kernel, so the set-up is also valid inside a captured graph).
+int noalloc_scratch(hipStream_t stream, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(MOGT_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return set_error(MOGT_E_INVALID, "device %d beyond the %d the library tracks", dev,
+                         NOALLOC_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return set_error(MOGT_E_LAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        const size_t n = NOALLOC_SCRATCH_BYTES / sizeof(uint4);
+        hipLaunchKernelGGL(clear_scratch_kernel, dim3(1024), dim3(256), 0, stream,
+                           static_cast<uint4*>(ptr), n);
+        const int rc = check_launch("clear_scratch_kernel");
+        if (rc) return rc;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MOGT_OK;
+}
+
 }  // namespace
 }  // namespace mogt
 
@@ -163,4 +212,29 @@ extern "C" int mogt_diag_scan_tiles(int family, int* out, int max_tiles) {
         out[4 * i + 3] = list[i].waves;
     }
     return n;
+}
+
+extern "C" int mogt_diag_scan_fwd_noalloc(const void* a, const void* b, void* h, void* a_prefix,
+                                          int64_t batch, int64_t length, int64_t features,
+                                          int in_dtype, int out_dtype, void* stream) {
+    clear_error();
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype))
+        return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (batch < 0 || length < 0 || features < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (batch == 0 || length == 0 || features == 0) return MOGT_OK;
+    const int al = common_alignment(a, b, h, a_prefix, in_dtype, out_dtype);
+    const DiagTile t = default_tile(batch, length, features, in_dtype == MOGT_BF16, al);
+    const size_t need = diag_geometry(batch, length, features, t).bytes;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return set_error(MOGT_E_INVALID,
+                         "diag scan of %lld x %lld x %lld needs %zu bytes of look-back scratch; the "
+                         "no-allocation entry point holds %zu (use mogt_diag_scan_fwd with a workspace)",
+                         (long long)batch, (long long)length, (long long)features, need,
+                         NOALLOC_SCRATCH_BYTES);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ws = nullptr;
+    const int rc = noalloc_scratch(st, &ws);
+    if (rc) return rc;
+    return run_scan(a, b, h, a_prefix, batch, length, features, in_dtype, out_dtype, t, ws,
+                    NOALLOC_SCRATCH_BYTES, stream);
 }
