@@ -2,24 +2,29 @@
 
 Same classes, constructor arguments, parameter names and duck-typed
 configuration attributes as the reference (model_mogt.py:9-380); configs and
-state dicts carry over.  The scan always runs on the HIP kernels:
+state dicts carry over.  The scan always runs on the HIP kernels.
 
-* generic path (any configuration, autograd): the reference's computation
-  op for op on the GPU, with every ``scan_impl`` routed to the HIP affine scan
-  (``sequential``, ``parallel_reference``, ``block_reference`` and
-  ``triton_hybrid`` evaluate the same recurrence; ``transport_triton`` runs the
-  HIP prefix product like the reference's transport-only mode);
-* fused path (inference with an identity connection and a rank-wide value gate
-  coupled to the forget gate -- the configuration of the reference's backbone
-  benchmark, benchmark_backbone_throughput.py:40-57): ``U = damping*(1-g)`` is
-  diagonal per rank, so gate + scan run as one HIP kernel (no [B,L,r,r] U, no
-  [B,L,3d] concatenation, no phi_conn GEMM whose result the identity
-  connection discards), RMSNorms and the SwiGLU gate are single-pass HIP
-  kernels, and each block's residual add is folded into the next RMSNorm.
+A block's configuration is resolved once per call into a :class:`MixerSpec`
+and the mixer is evaluated in one of three ways:
+
+* fused (identity connection, rank-wide value gate coupled to the forget gate,
+  no transport gate -- the wiring of the reference's backbone benchmark,
+  benchmark_backbone_throughput.py:40-57): gate + scan in one HIP kernel (no
+  ``[B,L,r,r]`` U, no ``[B,L,3d]`` gate input, no ``phi_conn`` GEMM whose result
+  the identity connection discards), single-pass RMSNorm / SwiGLU kernels,
+  residual adds folded into the next RMSNorm;
+* diagonal (any other identity-connection configuration): the transport is a
+  per-rank factor (damping x transport gate x (1 - value gate)), so the scan is
+  the HIP diagonal scan over ``[B, L, d]`` instead of a dense scan of ``r x r``
+  matrices;
+* dense (matrix_exp / Cayley connections): the connection map and the affine
+  scan on their HIP kernels.
 
 Tensors must be on the GPU; there is no CPU execution path.
 """
 from __future__ import annotations
+
+from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
@@ -27,7 +32,7 @@ import torch.nn.functional as F
 from torch.utils.checkpoint import checkpoint
 
 from . import ops, triton_scan
-from .chunked_lm_loss import chunked_linear_cross_entropy
+from .chunked_lm_loss import chunked_linear_cross_entropy, logits_cross_entropy
 
 
 def _autocast_dtype() -> torch.dtype | None:
@@ -36,13 +41,18 @@ def _autocast_dtype() -> torch.dtype | None:
     return None
 
 
+_CACHE_ATTR = "_gemm_weight_cache"
+
+
 def _gemm_weight(owner: nn.Module, name: str, params: tuple, build):
     """A GEMM operand built from parameters (a concatenation of weights, cast
     to the autocast dtype when autocast is on -- the cast F.linear would make).
     Without gradient recording it is cached on ``owner`` until a parameter
     changes (storage or version counter), the autocast dtype or the inference
     mode flag changes; with gradients it is rebuilt on every call so autograd
-    reaches the parameters."""
+    reaches the parameters.  Writes through ``p.data`` bypass the version
+    counter: call ``invalidate_weight_cache()`` after them (train(), eval()
+    and load_state_dict() do it)."""
     ad = _autocast_dtype()
 
     def make():
@@ -52,12 +62,29 @@ def _gemm_weight(owner: nn.Module, name: str, params: tuple, build):
     if torch.is_grad_enabled():
         return make()
     key = (tuple((p.data_ptr(), p._version, p.dtype) for p in params), ad, torch.is_inference_mode_enabled())
-    cache = owner.__dict__.setdefault("_gemm_weight_cache", {})
+    cache = owner.__dict__.setdefault(_CACHE_ATTR, {})
     hit = cache.get(name)
     if hit is None or hit[0] != key:
         hit = (key, make())
         cache[name] = hit
     return hit[1]
+
+
+class _WeightCacheOwner(nn.Module):
+    """Drops the cached GEMM operands of every submodule on train()/eval() and
+    after load_state_dict()."""
+
+    def __init__(self):
+        super().__init__()
+        self.register_load_state_dict_post_hook(lambda module, keys: module.invalidate_weight_cache())
+
+    def invalidate_weight_cache(self) -> None:
+        for m in self.modules():
+            m.__dict__.pop(_CACHE_ATTR, None)
+
+    def train(self, mode: bool = True):
+        self.invalidate_weight_cache()
+        return super().train(mode)
 
 
 class RMSNorm(nn.Module):
@@ -68,9 +95,6 @@ class RMSNorm(nn.Module):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(d_model))
-
-    def _norm(self, x):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps)
 
     def forward(self, x):
         ops.require_cuda("RMSNorm", x)
@@ -101,7 +125,104 @@ def reference_ffn_hidden(d_model: int) -> int:
     return 256 * ((int(8 * d_model / 3) + 255) // 256)
 
 
-class MOGTBlock(nn.Module):
+# ---------------------------------------------------------------------------
+# configuration
+# ---------------------------------------------------------------------------
+# transport-gate activations g(logit, scale) (model_mogt.py:152-162)
+_TRANSPORT_GATE_FN = {
+    "multiply": lambda g, s: torch.sigmoid(g),
+    "residual": lambda g, s: 1.0 + s * torch.tanh(g),
+    "forget_relu": lambda g, s: 1.0 - s * F.relu(torch.tanh(g)),
+}
+_CONNECTIONS = ("identity", "matrix_exp", "cayley")
+# every scan_impl that evaluates the affine recurrence (model_mogt.py:193-232);
+# "transport_triton" is the reference's transport-only mode (:187-192)
+_AFFINE_SCAN_IMPLS = frozenset({"triton_hybrid", "parallel_reference", "block_reference", "sequential"})
+_CARRY_HINT_IMPLS = frozenset({"triton_hybrid", "block_reference"})
+
+
+def _gate_input_parts(mode: str) -> tuple[str, ...]:
+    """Pieces of the value gate's input: the normalised token, then the
+    previous token and the prefix condition when the mode names them
+    (model_mogt.py:104-122)."""
+    if mode == "current":
+        return ("cur",)
+    return ("cur",) + (("prev",) if "prev" in mode else ()) + (("prefix",) if "prefix" in mode else ())
+
+
+@dataclass(frozen=True)
+class MixerSpec:
+    """A block's duck-typed configuration, resolved for one call."""
+    connection: str
+    damping: float
+    transport_gate: nn.Module | None
+    transport_mode: str
+    transport_scale: float
+    value_gate: nn.Module | None
+    gate_parts: tuple[str, ...]
+    coupled: bool
+    scan: str
+    residual_scale: float
+    residual_gate_logit: torch.Tensor | None
+    ffn_scale: float
+
+    @staticmethod
+    def of(block: "MOGTBlock") -> "MixerSpec":
+        scan = "transport_triton" if getattr(block, "fast_throughput_mode", False) else \
+            getattr(block, "scan_impl", "sequential")
+        gate_logit = getattr(block, "mogt_residual_gate_logit", None)
+        if not getattr(block, "mogt_residual_gate_enabled", False):
+            gate_logit = None
+        return MixerSpec(
+            connection=getattr(block, "connection_impl", "matrix_exp"),
+            damping=float(getattr(block, "connection_damping", 0.999)),
+            transport_gate=getattr(block, "phi_transport_gate", None),
+            transport_mode=getattr(block, "transport_gate_mode", "multiply"),
+            transport_scale=float(getattr(block, "transport_gate_scale", 1.0)),
+            value_gate=getattr(block, "phi_value_gate", None),
+            gate_parts=_gate_input_parts(getattr(block, "value_gate_input_mode", "current")),
+            coupled=bool(getattr(block, "couple_forget_to_value_gate", False)),
+            scan=scan,
+            residual_scale=float(getattr(block, "mogt_residual_scale", 1.0)),
+            residual_gate_logit=gate_logit,
+            ffn_scale=float(getattr(block, "mogt_ffn_residual_scale", 1.0)),
+        )
+
+    def validate(self) -> None:
+        if self.connection not in _CONNECTIONS:
+            raise ValueError(f"Unsupported connection_impl: {self.connection}")
+        if self.transport_gate is not None and self.transport_mode not in _TRANSPORT_GATE_FN:
+            raise ValueError(f"Unsupported transport_gate_mode: {self.transport_mode}")
+        if self.scan != "transport_triton" and self.scan not in _AFFINE_SCAN_IMPLS:
+            raise ValueError(f"Unsupported scan_impl: {self.scan}")
+
+    def residual_factor(self, like: torch.Tensor):
+        """Scale of the mixer's residual term: the constant scale, times the
+        learned gate sigmoid(logit) when enabled (model_mogt.py:243-249)."""
+        if self.residual_gate_logit is None:
+            return self.residual_scale
+        return self.residual_scale * torch.sigmoid(self.residual_gate_logit).to(dtype=like.dtype,
+                                                                                device=like.device)
+
+
+def _gate_input(xn: torch.Tensor, prefix_condition: torch.Tensor | None, parts: tuple[str, ...]):
+    """The value gate's input pieces side by side (model_mogt.py:104-122): the
+    normalised token, the previous one (zero at t = 0), the prefix condition
+    broadcast over time (zero without one)."""
+    pieces = []
+    for name in parts:
+        if name == "cur":
+            pieces.append(xn)
+        elif name == "prev":
+            pieces.append(F.pad(xn[:, :-1], (0, 0, 1, 0)))
+        else:
+            row = (xn.new_zeros(xn.size(0), 1, xn.size(-1)) if prefix_condition is None
+                   else prefix_condition.to(xn.dtype).view(xn.size(0), 1, xn.size(-1)))
+            pieces.append(row.expand_as(xn))
+    return pieces[0] if len(pieces) == 1 else torch.cat(pieces, dim=-1)
+
+
+class MOGTBlock(_WeightCacheOwner):
     """One MOGT layer (model_mogt.py:32-258).  ``ffn_hidden`` defaults to the
     reference's formula; pass e.g. ``4 * d_model`` for a 4x gated MLP."""
 
@@ -122,76 +243,28 @@ class MOGTBlock(nn.Module):
         self.norm_ffn = RMSNorm(d_model)
         self.ffn = SwiGLU(d_model, ffn_hidden or reference_ffn_hidden(d_model))
 
-    # ---------------------------------------------------------------- config
+    # ------------------------------------------------------------ dispatch
     def _resolve_scan_impl(self):
-        if getattr(self, "fast_throughput_mode", False):
-            return "transport_triton"
-        return getattr(self, "scan_impl", "sequential")
+        return MixerSpec.of(self).scan
 
     def _resolve_connection_impl(self):
-        return getattr(self, "connection_impl", "matrix_exp")
+        return MixerSpec.of(self).connection
 
     def _residual_scale(self, like: torch.Tensor) -> float:
-        scale = float(getattr(self, "mogt_residual_scale", 1.0))
-        gate_logit = getattr(self, "mogt_residual_gate_logit", None)
-        if getattr(self, "mogt_residual_gate_enabled", False) and gate_logit is not None:
-            gate = torch.sigmoid(gate_logit).to(dtype=like.dtype, device=like.device)
-            return float(scale * gate)
-        return scale
+        return float(MixerSpec.of(self).residual_factor(like))
 
     def fused_path_ok(self) -> bool:
         """Identity connection, no transport gate, rank-wide value gate coupled to
         the forget gate, an affine scan_impl; with autograd, no learned residual
         gate (its scale enters the fused residual update as a constant)."""
-        gate = getattr(self, "phi_value_gate", None)
-        if (torch.is_grad_enabled() and getattr(self, "mogt_residual_gate_enabled", False)
+        spec = MixerSpec.of(self)
+        if (torch.is_grad_enabled() and spec.residual_gate_logit is not None
                 and any(p.requires_grad for p in self.parameters())):
             return False
-        return (self._resolve_connection_impl() == "identity"
-                and getattr(self, "phi_transport_gate", None) is None
-                and isinstance(gate, nn.Linear) and gate.out_features == self.r
-                and bool(getattr(self, "couple_forget_to_value_gate", False))
-                and self._resolve_scan_impl() in {"triton_hybrid", "sequential",
-                                                  "parallel_reference", "block_reference"})
+        return (spec.connection == "identity" and spec.transport_gate is None
+                and isinstance(spec.value_gate, nn.Linear) and spec.value_gate.out_features == self.r
+                and spec.coupled and spec.scan in _AFFINE_SCAN_IMPLS)
 
-    # ------------------------------------------------------- reference pieces
-    def _build_transport(self, A: torch.Tensor, output_dtype: torch.dtype):
-        """model_mogt.py:79-102."""
-        A_fp32 = (A / self.r).to(torch.float32)
-        impl = self._resolve_connection_impl()
-        if impl in ("matrix_exp", "cayley"):
-            # HIP connection-map kernel (A is skew: A_raw - A_raw^T); damping and
-            # the output cast are applied below exactly as in the reference
-            name = "mogt.matrix_exp" if impl == "matrix_exp" else "mogt.cayley_solve"
-            with torch.autograd.profiler.record_function(name):
-                U_fp32 = ops.connection_map(A_fp32, impl)
-        elif impl == "identity":
-            U_fp32 = self._identity_r.view(1, 1, self.r, self.r).expand(
-                A.shape[0], A.shape[1], self.r, self.r)
-        else:
-            raise ValueError(f"Unsupported connection_impl: {impl}")
-        damping = float(getattr(self, "connection_damping", 0.999))
-        return (U_fp32 * damping).to(output_dtype)
-
-    def _build_value_gate_input(self, x_norm: torch.Tensor, prefix_condition: torch.Tensor | None):
-        """model_mogt.py:104-122."""
-        mode = getattr(self, "value_gate_input_mode", "current")
-        if mode == "current":
-            return x_norm
-        parts = [x_norm]
-        if "prev" in mode:
-            prev = torch.zeros_like(x_norm)
-            prev[:, 1:] = x_norm[:, :-1]
-            parts.append(prev)
-        if "prefix" in mode:
-            if prefix_condition is None:
-                prefix = torch.zeros_like(x_norm[:, :1])
-            else:
-                prefix = prefix_condition.to(dtype=x_norm.dtype).view(x_norm.size(0), 1, x_norm.size(-1))
-            parts.append(prefix.expand(x_norm.size(0), x_norm.size(1), x_norm.size(-1)))
-        return torch.cat(parts, dim=-1)
-
-    # ---------------------------------------------------------------- forward
     def forward(self, x, prefix_condition=None):
         ops.require_cuda("MOGTBlock", x)
         if self.fused_path_ok() and x.dtype == torch.float32:
@@ -199,109 +272,131 @@ class MOGTBlock(nn.Module):
             return x + s * z
         return self._forward_generic(x, prefix_condition)
 
-    def _forward_generic(self, x, prefix_condition):
-        """model_mogt.py:124-258 with the scan on the HIP kernels."""
-        residual = x
-        x_norm = self.norm_mogt(x)
-        B, L, D = x_norm.shape
-        impl = self._resolve_connection_impl()
-        with torch.autograd.profiler.record_function("mogt.connection"):
-            if impl == "identity":
-                A = x_norm.new_zeros(B, L, self.r, self.r)   # identity ignores A
-            else:
-                A_raw = self.phi_conn(x_norm).view(B, L, self.r, self.r)
-                A = A_raw - A_raw.transpose(-2, -1)
-        with torch.autograd.profiler.record_function("mogt.connection_map"):
-            U = self._build_transport(A, x_norm.dtype)
-            phi_transport_gate = getattr(self, "phi_transport_gate", None)
-            if phi_transport_gate is not None:
-                gate_raw = phi_transport_gate(x_norm).float()
-                if gate_raw.size(-1) == 1:
-                    gate_raw = gate_raw.view(B, L, 1, 1)
-                elif gate_raw.size(-1) == self.r:
-                    gate_raw = gate_raw.view(B, L, self.r, 1)
-                else:
-                    raise ValueError("phi_transport_gate must output either 1 scalar or r rank gates")
-                gate_mode = getattr(self, "transport_gate_mode", "multiply")
-                if gate_mode == "multiply":
-                    gate = torch.sigmoid(gate_raw)
-                elif gate_mode == "residual":
-                    gate = 1.0 + float(getattr(self, "transport_gate_scale", 1.0)) * torch.tanh(gate_raw)
-                elif gate_mode == "forget_relu":
-                    gate = 1.0 - float(getattr(self, "transport_gate_scale", 1.0)) * F.relu(torch.tanh(gate_raw))
-                else:
-                    raise ValueError(f"Unsupported transport_gate_mode: {gate_mode}")
-                U = U * gate.to(U.dtype)
-        with torch.autograd.profiler.record_function("mogt.value_projection"):
-            V_t_raw = self.phi_val(x_norm).view(B, L, self.r, self.c)
-            phi_value_gate = getattr(self, "phi_value_gate", None)
-            if phi_value_gate is not None:
-                value_gate_raw = phi_value_gate(self._build_value_gate_input(x_norm, prefix_condition)).float()
-                if value_gate_raw.size(-1) == 1:
-                    value_gate = torch.sigmoid(value_gate_raw).view(B, L, 1, 1)
-                elif value_gate_raw.size(-1) == self.r:
-                    value_gate = torch.sigmoid(value_gate_raw).view(B, L, self.r, 1)
-                else:
-                    raise ValueError("phi_value_gate must output either 1 scalar or r rank gates")
-                V_t_raw = V_t_raw * value_gate.to(V_t_raw.dtype)
-                if getattr(self, "couple_forget_to_value_gate", False):
-                    U = U * (1.0 - value_gate).to(U.dtype)
-        scan_impl = self._resolve_scan_impl()
-        with torch.autograd.profiler.record_function("mogt.affine_scan"):
-            if scan_impl == "transport_triton":
-                Y = triton_scan.triton_fused_scan(U)
-                V_t = torch.matmul(Y, V_t_raw.to(Y.dtype))
-            elif scan_impl in {"triton_hybrid", "parallel_reference", "block_reference", "sequential"}:
-                if scan_impl == "block_reference" or scan_impl == "triton_hybrid":
-                    carry = getattr(self, "block_carry_scan", "sequential")
-                else:
-                    carry = "sequential"
-                V_t = triton_scan.triton_affine_scan_hybrid(
-                    U, V_t_raw, block_size=getattr(self, "scan_block_size", 256),
-                    block_c=getattr(self, "scan_block_c", 32), carry_scan=carry,
-                    output_dtype=U.dtype)
-            else:
-                raise ValueError(f"Unsupported scan_impl: {scan_impl}")
-        V_t_flat = V_t.reshape(B, L, self.d_model)
-        with torch.autograd.profiler.record_function("mogt.readout"):
-            Z = self.theta_read(self.norm_out(V_t_flat))
-        mogt_residual_scale = float(getattr(self, "mogt_residual_scale", 1.0))
-        gate_logit = getattr(self, "mogt_residual_gate_logit", None)
-        if getattr(self, "mogt_residual_gate_enabled", False) and gate_logit is not None:
-            gate = torch.sigmoid(gate_logit).to(dtype=Z.dtype, device=Z.device)
-            x = residual + ((mogt_residual_scale * gate) * Z)
+    # ------------------------------------------------------------ generic path
+    def _build_transport(self, A: torch.Tensor, output_dtype: torch.dtype):
+        """``damping * map(A / r)`` as fp32 math cast to ``output_dtype``
+        (model_mogt.py:79-102); the maps run on the HIP connection-map kernel."""
+        spec = MixerSpec.of(self)
+        if spec.connection == "identity":
+            eye = self._identity_r.view(1, 1, self.r, self.r)
+            return (eye * spec.damping).to(output_dtype).expand(A.shape[0], A.shape[1], self.r, self.r)
+        if spec.connection not in _CONNECTIONS:
+            raise ValueError(f"Unsupported connection_impl: {spec.connection}")
+        label = "mogt.matrix_exp" if spec.connection == "matrix_exp" else "mogt.cayley_solve"
+        with torch.autograd.profiler.record_function(label):
+            mapped = ops.connection_map((A / self.r).to(torch.float32), spec.connection)
+        return (mapped * spec.damping).to(output_dtype)
+
+    def _value_gate_probs(self, spec: MixerSpec, xn, prefix_condition):
+        """sigmoid of the value gate, fp32, shaped [B, L, w, 1] (w = 1 or r).
+        A Linear gate never sees its concatenated input (``_gate_logits``);
+        any other module is called on it."""
+        if isinstance(spec.value_gate, nn.Linear):
+            z = self._gate_logits(xn, prefix_condition)
         else:
-            x = residual + (mogt_residual_scale * Z)
-        residual = x
+            z = spec.value_gate(_gate_input(xn, prefix_condition, spec.gate_parts)).float()
+        if z.size(-1) not in (1, self.r):
+            raise ValueError("phi_value_gate must output either 1 scalar or r rank gates")
+        return torch.sigmoid(z).unsqueeze(-1)
+
+    def _transport_gate(self, spec: MixerSpec, xn):
+        """The transport gate's factor, fp32, [B, L, w, 1] (w = 1 or r)."""
+        logits = spec.transport_gate(xn).float()
+        if logits.size(-1) not in (1, self.r):
+            raise ValueError("phi_transport_gate must output either 1 scalar or r rank gates")
+        return _TRANSPORT_GATE_FN[spec.transport_mode](logits.unsqueeze(-1), spec.transport_scale)
+
+    def _forward_generic(self, x, prefix_condition):
+        """MOGTBlock.forward (model_mogt.py:124-258), any configuration, with
+        autograd; the scan on the HIP diagonal or dense kernels."""
+        spec = MixerSpec.of(self)
+        spec.validate()
+        xn = self.norm_mogt(x)
+        B, L, D = xn.shape
+        r, c = self.r, self.c
+        diagonal = spec.connection == "identity" and spec.scan != "transport_triton"
+        with torch.autograd.profiler.record_function("mogt.connection_map"):
+            if diagonal:
+                # per-rank factor of U = factor * I: starts as the damping
+                factor = torch.full((1, 1, 1, 1), spec.damping, dtype=torch.float32,
+                                    device=xn.device).to(xn.dtype)
+                U = None
+            else:
+                if spec.connection == "identity":
+                    A = xn.new_zeros(B, L, r, r)   # the identity map ignores A
+                else:
+                    with torch.autograd.profiler.record_function("mogt.connection"):
+                        A_raw = self.phi_conn(xn).view(B, L, r, r)
+                        A = A_raw - A_raw.transpose(-2, -1)
+                U = self._build_transport(A, xn.dtype)
+            if spec.transport_gate is not None:
+                tg = self._transport_gate(spec, xn)
+                if diagonal:
+                    factor = factor * tg.to(factor.dtype)
+                else:
+                    U = U * tg.to(U.dtype)
+        with torch.autograd.profiler.record_function("mogt.value_projection"):
+            values = self.phi_val(xn).view(B, L, r, c)
+            if spec.value_gate is not None:
+                vg = self._value_gate_probs(spec, xn, prefix_condition)
+                values = values * vg.to(values.dtype)
+                if spec.coupled:
+                    keep = (1.0 - vg)
+                    if diagonal:
+                        factor = factor * keep.to(factor.dtype)
+                    else:
+                        U = U * keep.to(U.dtype)
+        out_dtype = xn.dtype   # the scan's output dtype is U's (model_mogt.py:202)
+        with torch.autograd.profiler.record_function("mogt.affine_scan"):
+            if diagonal:
+                decay = factor.float().expand(B, L, r, c).reshape(B, L, D)
+                h = ops.diag_scan(decay, values.float().reshape(B, L, D), out_dtype=out_dtype)
+            elif spec.scan == "transport_triton":
+                Y = triton_scan.triton_fused_scan(U)
+                h = torch.matmul(Y, values.to(Y.dtype)).reshape(B, L, D)
+            else:
+                carry = getattr(self, "block_carry_scan", "sequential") if spec.scan in _CARRY_HINT_IMPLS \
+                    else "sequential"
+                h = triton_scan.triton_affine_scan_hybrid(
+                    U, values, block_size=getattr(self, "scan_block_size", 256),
+                    block_c=getattr(self, "scan_block_c", 32), carry_scan=carry,
+                    output_dtype=out_dtype).reshape(B, L, D)
+        with torch.autograd.profiler.record_function("mogt.readout"):
+            z = self.theta_read(self.norm_out(h))
+        x = x + spec.residual_factor(z) * z
         with torch.autograd.profiler.record_function("mogt.ffn"):
-            x_norm = self.norm_ffn(x)
-            x = residual + (float(getattr(self, "mogt_ffn_residual_scale", 1.0)) * self.ffn(x_norm))
+            x = x + spec.ffn_scale * self.ffn(self.norm_ffn(x))
         return x
 
+    # ------------------------------------------------------------ fused path
     def _gate_logits(self, xn: torch.Tensor, prefix_condition: torch.Tensor | None) -> torch.Tensor:
-        """phi_value_gate over [x, x_{t-1}, prefix] without materialising the
-        concatenation: W = [W_cur | W_prev | W_pref] (model_mogt.py:104-122)."""
+        """The value gate's logits, fp32 [B, L, w], over the input pieces of
+        ``value_gate_input_mode`` without materialising their concatenation:
+        with W = [W_cur | W_prev | W_pref], one GEMM of x against [W_cur; W_prev]
+        gives the current term and the previous token's term (shifted by one
+        step, zero at t = 0), and the prefix term is one row per sequence
+        (zero without a prefix condition) -- model_mogt.py:104-122, :166-171."""
         gate: nn.Linear = self.phi_value_gate
-        mode = getattr(self, "value_gate_input_mode", "current")
+        parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
         D = self.d_model
+        w = gate.out_features
         W = gate.weight
-        parts = [W[:, :D]]
-        off = D
-        if "prev" in mode:
-            parts.append(W[:, off:off + D])
-            off += D
-        Wg = _gemm_weight(self, "gate", (W,), lambda: torch.cat(parts, dim=0))
-        y = F.linear(xn, Wg).float()   # [B, L, r * n_parts]
-        r = self.r
-        z = y[..., :r]
-        if "prev" in mode:
-            z = z.clone()
-            z[:, 1:] += y[:, :-1, r:2 * r]
-        const = gate.bias.float() if gate.bias is not None else torch.zeros(r, device=xn.device)
-        if "prefix" in mode and prefix_condition is not None:
+        if W.shape[1] != len(parts) * D:
+            raise RuntimeError(f"phi_value_gate takes {W.shape[1]} inputs, the gate input mode builds "
+                               f"{len(parts) * D}")
+        cols = {name: W[:, i * D:(i + 1) * D] for i, name in enumerate(parts)}
+        stacked = [cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
+        Wg = _gemm_weight(self, "gate", (W,), lambda: torch.cat(stacked, dim=0))
+        y = F.linear(xn, Wg).float()   # [B, L, w * (1 or 2)]
+        z = y[..., :w]
+        if "prev" in cols:
+            z = torch.cat([z[:, :1], z[:, 1:] + y[:, :-1, w:2 * w]], dim=1)
+        const = gate.bias.float() if gate.bias is not None else None
+        if "prefix" in cols and prefix_condition is not None:
             pref = prefix_condition.to(dtype=xn.dtype).view(xn.size(0), 1, D)
-            const = const + F.linear(pref, W[:, off:off + D]).float()
-        return (z + const).contiguous()
+            pt = F.linear(pref, cols["prefix"]).float()
+            const = pt if const is None else const + pt
+        return (z if const is None else z + const).contiguous()
 
     def forward_fused(self, x: torch.Tensor, prefix_condition, pending):
         """Fused forward (differentiable: every kernel has its backward).  ``pending = (z, scale)`` is the previous
@@ -333,7 +428,7 @@ class MOGTBlock(nn.Module):
         return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
 
 
-class MOGTModel(nn.Module):
+class MOGTModel(_WeightCacheOwner):
     """Embedding -> blocks -> norm_f (model_mogt.py:260-287)."""
 
     def __init__(self, vocab_size: int, d_model: int = 768, num_layers: int = 12, r: int = 16,
@@ -346,35 +441,44 @@ class MOGTModel(nn.Module):
         self.gradient_checkpointing = False
         self.checkpoint_every_n = 1
 
+    def _prefix_condition(self, h: torch.Tensor) -> torch.Tensor | None:
+        """The embedding row at ``prefix_condition_position`` (negative counts
+        from the end), or None when unset or outside the sequence."""
+        pos = getattr(self, "prefix_condition_position", None)
+        if pos is None:
+            return None
+        pos = int(pos)
+        return h[:, pos, :] if -h.size(1) <= pos < h.size(1) else None
+
+    def _checkpointed(self, index: int) -> bool:
+        if not (self.training and getattr(self, "gradient_checkpointing", False)):
+            return False
+        return index % max(1, int(getattr(self, "checkpoint_every_n", 1))) == 0
+
     def forward(self, input_ids):
-        x = self.embedding(input_ids)
-        prefix_condition = None
-        prefix_position = getattr(self, "prefix_condition_position", None)
-        if prefix_position is not None:
-            prefix_position = int(prefix_position)
-            if -x.size(1) <= prefix_position < x.size(1):
-                prefix_condition = x[:, prefix_position, :]
-        use_checkpoint = self.training and getattr(self, "gradient_checkpointing", False)
-        every = max(1, int(getattr(self, "checkpoint_every_n", 1)))
-        if (not use_checkpoint and x.dtype == torch.float32 and len(self.blocks) > 0
-                and all(b.fused_path_ok() for b in self.blocks)):
+        h = self.embedding(input_ids)
+        cond = self._prefix_condition(h)
+        chain_fused = (h.dtype == torch.float32 and len(self.blocks) > 0 and not self._checkpointed(0)
+                       and all(blk.fused_path_ok() for blk in self.blocks))
+        if chain_fused:
+            # each block hands its FFN term to the next block's first RMSNorm;
+            # the last one is added inside norm_f
             pending = None
-            for block in self.blocks:
-                x, pending = block.forward_fused(x, prefix_condition, pending)
-            _, out = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps,
-                                     out_dtype=torch.float32)
-            return out
-        for i, block in enumerate(self.blocks):
-            if use_checkpoint and (i % every == 0):
-                x = checkpoint(block, x, prefix_condition, use_reentrant=False)
-            else:
-                x = block(x, prefix_condition=prefix_condition)
-        return self.norm_f(x)
+            for blk in self.blocks:
+                h, pending = blk.forward_fused(h, cond, pending)
+            return ops.add_rmsnorm(h, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps,
+                                   out_dtype=torch.float32)[1]
+        for i, blk in enumerate(self.blocks):
+            h = checkpoint(blk, h, cond, use_reentrant=False) if self._checkpointed(i) \
+                else blk(h, prefix_condition=cond)
+        return self.norm_f(h)
 
 
-class MOGTForCausalLM(nn.Module):
-    """Backbone + weight-tied LM head (model_mogt.py:289-380); initialisation as
-    the reference (N(0, 0.02), phi_conn N(0, 1e-4), theta_read and ffn.w3 zero)."""
+class MOGTForCausalLM(_WeightCacheOwner):
+    """Backbone + weight-tied LM head (model_mogt.py:289-380)."""
+
+    INIT_STD = 0.02            # every Linear weight and the embedding (model_mogt.py:318-324)
+    CONNECTION_INIT_STD = 1e-4  # phi_conn: U starts near the identity (:308-310)
 
     def __init__(self, vocab_size: int, d_model: int = 768, num_layers: int = 12, r: int = 16,
                  ffn_hidden: int | None = None):
@@ -383,64 +487,46 @@ class MOGTForCausalLM(nn.Module):
                               ffn_hidden=ffn_hidden)
         self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
         self.lm_head.weight = self.mogt.embedding.weight
-        self.apply(self._init_weights)
-        for name, p in self.named_parameters():
-            if "phi_conn" in name:
-                torch.nn.init.normal_(p, mean=0.0, std=1e-4)
-            elif "theta_read" in name or "ffn.w3" in name:
-                torch.nn.init.zeros_(p)
+        self._initialise()
 
-    def _init_weights(self, module):
-        if isinstance(module, nn.Linear):
-            torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
-            if module.bias is not None:
-                torch.nn.init.zeros_(module.bias)
-        elif isinstance(module, nn.Embedding):
-            torch.nn.init.normal_(module.weight, mean=0.0, std=0.02)
-
-    def _chunked_lm_loss(self, hidden_states, labels, loss_chunk_size: int, return_logits: bool):
-        """Chunked loss that keeps the logits (model_mogt.py:326-348): per chunk of
-        positions the LM head and a summed cross-entropy, divided by the token
-        count."""
-        vocab_size = self.lm_head.weight.size(0)
-        total_loss = hidden_states.new_zeros(())
-        total_tokens = 0
-        logits_chunks = [] if return_logits else None
-        for start in range(0, hidden_states.size(1), loss_chunk_size):
-            end = min(start + loss_chunk_size, hidden_states.size(1))
-            logits_chunk = self.lm_head(hidden_states[:, start:end, :])
-            labels_chunk = labels[:, start:end]
-            total_loss = total_loss + F.cross_entropy(logits_chunk.reshape(-1, vocab_size),
-                                                      labels_chunk.reshape(-1), reduction="sum")
-            total_tokens += labels_chunk.numel()
-            if return_logits:
-                logits_chunks.append(logits_chunk)
-        loss = total_loss / total_tokens
-        logits = torch.cat(logits_chunks, dim=1) if return_logits else None
-        return logits, loss
+    @torch.no_grad()
+    def _initialise(self) -> None:
+        """The reference's initialisation, draw for draw: every Linear and
+        Embedding in module order gets N(0, INIT_STD) (biases zero; the tied
+        head redraws the shared matrix), then each block's phi_conn
+        N(0, CONNECTION_INIT_STD) and its read-outs (theta_read, ffn.w3) zero."""
+        for m in self.modules():
+            if isinstance(m, (nn.Linear, nn.Embedding)):
+                m.weight.normal_(0.0, self.INIT_STD)
+                if getattr(m, "bias", None) is not None:
+                    m.bias.zero_()
+        for blk in self.mogt.blocks:
+            blk.phi_conn.weight.normal_(0.0, self.CONNECTION_INIT_STD)
+            blk.theta_read.weight.zero_()
+            blk.ffn.w3.weight.zero_()
 
     def forward(self, input_ids, labels=None, *, return_logits=True, loss_chunk_size=0):
-        """model_mogt.py:350-380: with labels and ``loss_chunk_size > 0`` the loss
-        is chunked -- keeping the logits through the LM head, or, without
-        logits, through chunked_linear_cross_entropy (HIP cross-entropy rows)."""
-        x = self.mogt(input_ids)
-        logits = None
-        loss = None
-        loss_chunk_size = int(loss_chunk_size or 0)
+        """model_mogt.py:350-380.  Without labels: logits.  With labels and
+        ``loss_chunk_size <= 0``: F.cross_entropy over the full logits (mean
+        over non-ignored tokens).  With ``loss_chunk_size > 0``: the summed
+        cross-entropy divided by the token count -- from the kept logits
+        through the HIP cross-entropy rows (``return_logits``), or without
+        logits through chunked_linear_cross_entropy."""
+        hidden = self.mogt(input_ids)
+        chunk = int(loss_chunk_size or 0)
         with torch.autograd.profiler.record_function("mogt.lm_head_loss"):
-            if labels is not None and loss_chunk_size > 0:
-                if return_logits:
-                    logits, loss = self._chunked_lm_loss(x, labels, loss_chunk_size, True)
+            if labels is not None and chunk > 0 and not return_logits:
+                return None, chunked_linear_cross_entropy(hidden, self.lm_head.weight, labels,
+                                                          chunk_size=chunk)
+            logits = self.lm_head(hidden)
+            loss = None
+            if labels is not None:
+                flat_logits = logits.reshape(-1, logits.size(-1))
+                if chunk > 0:
+                    loss = logits_cross_entropy(flat_logits, labels.reshape(-1))
                 else:
-                    loss = chunked_linear_cross_entropy(x, self.lm_head.weight, labels,
-                                                        chunk_size=loss_chunk_size)
-            else:
-                logits = self.lm_head(x)
-                if labels is not None:
-                    loss = F.cross_entropy(logits.reshape(-1, logits.size(-1)).float(), labels.reshape(-1))
-                if not return_logits:
-                    logits = None
-        return logits, loss
+                    loss = F.cross_entropy(flat_logits.float(), labels.reshape(-1))
+        return (logits if return_logits else None), loss
 
 
 def configure_coupled_gate(model: nn.Module, *, scan_impl: str = "triton_hybrid",
@@ -452,7 +538,7 @@ def configure_coupled_gate(model: nn.Module, *, scan_impl: str = "triton_hybrid"
     backbone benchmark (benchmark_backbone_throughput.py:33-59)."""
     backbone = model.mogt if hasattr(model, "mogt") else model
     D = backbone.embedding.embedding_dim
-    n_in = {"current": 1, "current_prev": 2, "current_prev_prefix": 3}[value_gate_input]
+    n_in = len(_gate_input_parts(value_gate_input))
     dev = backbone.embedding.weight.device
     for block in backbone.blocks:
         block.scan_impl = scan_impl

@@ -992,6 +992,38 @@ def _(logits, labels, lse, scale, ignore_index):
     return None
 
 
+@torch.library.custom_op("mogt::lm_ce_grad", mutates_args=())
+def _lm_ce_grad_op(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor, scale: torch.Tensor,
+                   ignore_index: int) -> torch.Tensor:
+    lib = _lib.load()
+    labels = labels.contiguous()
+    lse = lse.contiguous()
+    rows, vocab = logits.shape
+    grad = torch.empty((rows, vocab), dtype=torch.float32, device=logits.device)
+    rc = lib.mogt_lm_ce_bwd(logits.data_ptr(), logits.stride(0), dtype_code(logits.dtype, "lm_ce_grad"),
+                            labels.data_ptr(), lse.data_ptr(), rows, vocab, int(ignore_index), scale.data_ptr(),
+                            grad.data_ptr(), vocab, _lib.MOGT_F32, _stream_handle(logits.device))
+    _lib.check(rc, "mogt_lm_ce_bwd")
+    return grad
+
+
+@_lm_ce_grad_op.register_fake
+def _(logits, labels, lse, scale, ignore_index):
+    return logits.new_empty(logits.shape, dtype=torch.float32)
+
+
+def lm_ce_grad(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor, scale: torch.Tensor, *,
+               ignore_index: int = -100) -> torch.Tensor:
+    """``scale * (softmax(logits) - onehot(labels))`` as a new fp32 block (zero
+    rows where the label is ``ignore_index``), for fp32 or bf16 logits."""
+    _check_ce_rows(logits, labels, "lm_ce_grad")
+    if lse.shape != labels.shape or lse.dtype != torch.float32:
+        raise ValueError("lm_ce_grad: lse must be float32 [rows]")
+    if scale.numel() != 1 or scale.dtype != torch.float32 or scale.device != logits.device:
+        raise ValueError("lm_ce_grad: scale must be a one-element float32 tensor on the logits' device")
+    return torch.ops.mogt.lm_ce_grad(logits, labels, lse, scale.reshape(1).contiguous(), int(ignore_index))
+
+
 def lm_ce_backward_(logits: torch.Tensor, labels: torch.Tensor, lse: torch.Tensor,
                     scale: torch.Tensor, *, ignore_index: int = -100) -> torch.Tensor:
     """Overwrite a logits block with ``scale * (softmax(logits) - onehot(labels))``

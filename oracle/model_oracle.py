@@ -98,10 +98,13 @@ def block_forward(p: dict, x: torch.Tensor, prefix: torch.Tensor | None, cfg: di
         V = V * vg.to(V.dtype)
         if cfg.get("couple_forget_to_value_gate", False):
             U = U * (1.0 - vg).to(U.dtype)
-    if ref_casts:
+    if ref_casts or (torch.is_grad_enabled() and (U.requires_grad or V.requires_grad)):
+        # the reference's bmm loop: float32 state with ref_casts; otherwise a
+        # float64 state, differentiable for autograd checks of the GPU backward
         from .torch_ref import affine_scan_sequential_torch
 
-        H = affine_scan_sequential_torch(U, V, state_dtype=torch.float32, output_dtype=U.dtype)
+        H = affine_scan_sequential_torch(U, V, state_dtype=torch.float32 if ref_casts else torch.float64,
+                                         output_dtype=U.dtype)
     else:
         H = torch.from_numpy(so.affine_scan_sequential(U.contiguous().numpy(), V.contiguous().numpy(),
                                                        state_dtype=np.float64, output_dtype=np.float64))

@@ -77,12 +77,14 @@ def test_add_rmsnorm_backward(gpu, zdt):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_silu_mul_backward(gpu, dtype):
-    announce(f"silu_mul backward {dtype}")
+@pytest.mark.parametrize("H", [512, 3072])
+def test_silu_mul_backward(gpu, dtype, H):
+    """H = 3072: configs[4]'s 4x gated MLP (a 6144-wide fused [w1; w2] row)."""
+    announce(f"silu_mul backward {dtype} H={H}")
     from mogt_amd import ops
 
     g = torch.Generator().manual_seed(4)
-    rows, H = 333, 512
+    rows = 333
     y = (torch.randn(rows, 2 * H, generator=g) * 2).to(dtype)
     d = torch.randn(rows, H, generator=g).to(dtype)
     yt = y.to(gpu).requires_grad_()
@@ -170,3 +172,53 @@ def test_silu_mul_vector_widths(gpu, dtype):
             tol = ROW_TOL if dtype == torch.float32 else BF16_TOL
             assert rel_err(to_np(out), ref.detach().numpy()) <= tol, (H, off)
             assert rel_err(to_np(y.grad), y64.grad.numpy()) <= tol, (H, off)
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_fused_training_step_vs_float64_autograd(gpu, autocast):
+    """One backward through the fused block path (2 layers, coupled gate,
+    prefix condition) against float64 autograd of the pinned model oracle on
+    the same weights: the loss and every parameter's gradient."""
+    announce(f"fused training step vs float64 autograd autocast={autocast}")
+    from mogt_amd.model_mogt import MOGTModel, configure_coupled_gate
+    from oracle import model_oracle as mo
+
+    torch.manual_seed(17)
+    model = MOGTModel(vocab_size=300, d_model=128, num_layers=2, r=16, ffn_hidden=512).to(gpu)
+    configure_coupled_gate(model, connection_damping=0.995, zero_gate_weight=False)
+    gen = torch.Generator().manual_seed(17)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape, generator=gen))
+            elif name.endswith("bias"):
+                p.copy_(-1.0 + 0.5 * torch.randn(p.shape, generator=gen))
+            else:
+                p.copy_(0.05 * torch.randn(p.shape, generator=gen))
+    model.train()
+    ids = torch.randint(0, 300, (1, 256), generator=gen)
+    target = torch.randn(1, 256, 128, generator=gen)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        assert all(b.fused_path_ok() for b in model.blocks)
+        out = model(ids.to(gpu))
+    loss = (out.float() - target.to(gpu)).square().mean()
+    loss.backward()
+    torch.cuda.synchronize()
+    st = {k: v.detach().double().cpu().requires_grad_() for k, v in model.state_dict().items()}
+    cfg = {"r": 16, "connection_impl": "identity", "connection_damping": 0.995,
+           "value_gate_input_mode": "current_prev_prefix", "couple_forget_to_value_gate": True}
+    ref_out = mo.model_forward(st, ids, 2, cfg, prefix_position=1)
+    ref = (ref_out - target.double()).square().mean()
+    names = list(st)
+    grads = torch.autograd.grad(ref, [st[n] for n in names], allow_unused=True)
+    tol = BF16_TOL if autocast else FP32_TOL
+    assert abs(float(loss.detach()) - float(ref.detach())) <= tol * abs(float(ref.detach()))
+    params = dict(model.named_parameters())
+    checked = 0
+    for n, gr in zip(names, grads):
+        if gr is None or n not in params:
+            continue
+        assert params[n].grad is not None, n
+        assert rel_err(to_np(params[n].grad), gr.numpy()) <= tol, n
+        checked += 1
+    assert checked >= 20

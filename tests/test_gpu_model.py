@@ -109,6 +109,57 @@ def test_fused_backbone_bf16_autocast(gpu):
     assert rel_err(to_np(out), ref.numpy()) <= BF16_TOL
 
 
+def _configs4_model(dev, seed):
+    """4 layers, d_model 768, a 4x gated MLP (hidden
+    3072), vocab 32000, the benchmark's identity-coupled slot-addressed wiring;
+    random weights (every projection non-zero)."""
+    from mogt_amd.model_mogt import MOGTModel, configure_coupled_gate
+
+    torch.manual_seed(seed)
+    model = MOGTModel(vocab_size=32000, d_model=768, num_layers=4, r=16, ffn_hidden=3072).to(dev)
+    configure_coupled_gate(model)
+    _randomize(model, seed=seed)
+    return model.eval()
+
+
+def test_configs4_backbone_bf16_full_length(gpu):
+    """configs[4] at its own shape: B = 1, L = 32768 under bf16 autocast (the
+    benchmark's precision) against the float64 oracle."""
+    announce("configs[4] backbone bf16 autocast L=32768")
+    model = _configs4_model(gpu, seed=41)
+    ids = torch.randint(0, 32000, (1, 32768), generator=torch.Generator().manual_seed(41))
+    with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+        assert all(b.fused_path_ok() for b in model.blocks)
+        out = model(ids.to(gpu))
+    torch.cuda.synchronize()
+    out = to_np(out)
+    state = _state64(model)
+    del model
+    torch.cuda.empty_cache()
+    with torch.no_grad():
+        ref = mo.model_forward(state, ids, 4, _coupled_cfg_of(state), prefix_position=1)
+    assert np.isfinite(out).all()
+    assert rel_err(out, ref.numpy()) <= BF16_TOL
+
+
+def test_configs4_backbone_fp32(gpu):
+    """configs[4]'s model in fp32 at L = 4096 against the float64 oracle."""
+    announce("configs[4] backbone fp32 L=4096")
+    model = _configs4_model(gpu, seed=42)
+    ids = torch.randint(0, 32000, (1, 4096), generator=torch.Generator().manual_seed(42))
+    with torch.no_grad():
+        out = model(ids.to(gpu))
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        ref = mo.model_forward(_state64(model), ids, 4, _coupled_cfg_of(_state64(model)), prefix_position=1)
+    assert rel_err(to_np(out), ref.numpy()) <= FP32_TOL
+
+
+def _coupled_cfg_of(state):
+    return {"r": 16, "connection_impl": "identity", "connection_damping": 1.0,
+            "value_gate_input_mode": "current_prev_prefix", "couple_forget_to_value_gate": True}
+
+
 @pytest.mark.parametrize("conn,tmode", [("matrix_exp", "multiply"), ("cayley", "multiply"),
                                         ("identity", "multiply"), ("matrix_exp", "residual"),
                                         ("cayley", "forget_relu")])

@@ -31,3 +31,25 @@ def test_gemm_weight_cache_reuse_and_invalidation():
     assert g1 is not g2 and g1.grad_fn is not None
     g1.sum().backward()
     assert torch.equal(a.weight.grad, torch.ones(3, 4)) and torch.equal(b.weight.grad, torch.ones(2, 4))
+
+
+def test_gemm_weight_cache_invalidation_paths():
+    """Writes through p.data bypass the version counter; invalidate_weight_cache,
+    train()/eval() and load_state_dict drop the cached operands."""
+    from mogt_amd.model_mogt import SwiGLU, MOGTBlock
+
+    blk = MOGTBlock(d_model=32, r=4, ffn_hidden=64)
+    ffn: SwiGLU = blk.ffn
+    build = lambda: torch.cat([ffn.w1.weight, ffn.w2.weight], dim=0)   # noqa: E731
+    with torch.no_grad():
+        w = _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build)
+        ffn.w1.weight.data.mul_(2.0)                     # not seen by the version counter
+        assert _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build) is w
+        blk.invalidate_weight_cache()
+        w2 = _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build)
+        assert w2 is not w and torch.equal(w2[:64], ffn.w1.weight)
+        blk.eval()
+        w3 = _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build)
+        assert w3 is not w2
+        blk.load_state_dict(blk.state_dict())
+        assert _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build) is not w3
