@@ -174,6 +174,67 @@ def test_backward_matches_oracle(gpu, R, C):
     assert rel_err(to_np(Ut.grad), gU_ref) <= FP32_TOL
 
 
+def test_core_operator_shape_full_length(gpu):
+    """The reference's core-operator benchmark shape (U [1, 32768, 16, 16],
+    V [1, 32768, 16, 48], fp32; the bench's dense_affine_r16_c48_L32768 line)
+    through triton_affine_scan_hybrid, against the oracle, with and without
+    the prefix product."""
+    announce("dense core shape R16 C48 L32768")
+    from mogt_amd import triton_scan
+
+    U, V = _stable_affine(1, 32768, 16, 48, seed=16)
+    P_ref, H_ref = so.affine_scan_sequential(U.astype(np.float64), V.astype(np.float64), return_prefix=True)
+    Ut, Vt = torch.from_numpy(U).to(gpu), torch.from_numpy(V).to(gpu)
+    H = triton_scan.triton_affine_scan_hybrid(Ut, Vt)
+    P, H2 = triton_scan.triton_affine_scan_hybrid(Ut, Vt, return_prefix=True)
+    torch.cuda.synchronize()
+    assert H.dtype == torch.float32
+    assert rel_err(to_np(H), H_ref) <= FP32_TOL
+    assert rel_err(to_np(H2), H_ref) <= FP32_TOL
+    assert rel_err(to_np(P), P_ref) <= FP32_TOL
+
+
+def test_affine_scan_dropin_names(gpu):
+    """mogt_amd.affine_scan's drop-ins for affine_scan.py:14-278, called by
+    their own names on the reference's sanity inputs (seed 42, B2 L17 R4 C3 and
+    B1 L64 R16 C8): sequential, doubling and block_reference with and without
+    return_prefix, the combine operator, and the hand backward."""
+    announce("affine_scan drop-in names")
+    from mogt_amd import affine_scan as das
+
+    for shape in ((2, 17, 4, 3), (1, 64, 16, 8)):
+        Ut, Vt = synthetic.reference_test_case(*shape)
+        U, V = Ut.float(), Vt.float()
+        P_ref, H_ref = so.affine_scan_sequential(U.double().numpy(), V.double().numpy(), return_prefix=True)
+        Ug, Vg = U.to(gpu), V.to(gpu)
+        outs = {
+            "sequential": das.affine_scan_sequential(Ug, Vg, return_prefix=True),
+            "doubling": das.affine_scan_doubling(Ug, Vg, return_prefix=True),
+            "block5": das.affine_scan_block_reference(Ug, Vg, block_size=5, return_prefix=True),
+            "block5d": das.affine_scan_block_reference(Ug, Vg, block_size=5, carry_scan="doubling",
+                                                       return_prefix=True),
+        }
+        for name, (P, H) in outs.items():
+            assert P.dtype == torch.float32 and H.dtype == torch.float32, name
+            assert rel_err(to_np(H), H_ref) <= FP32_TOL, name
+            assert rel_err(to_np(P), P_ref) <= FP32_TOL, name
+        H_only = das.affine_scan_doubling(Ug, Vg, output_dtype=torch.bfloat16)
+        assert H_only.dtype == torch.bfloat16 and rel_err(to_np(H_only), H_ref) <= BF16_TOL
+        # affine_combine: (U2, V2) o (U1, V1) = (U2 U1, U2 V1 + V2)
+        cu, cv = das.affine_combine(Ug[:, 1], Vg[:, 1], Ug[:, 0], Vg[:, 0])
+        assert rel_err(to_np(cv), H_ref[:, 1]) <= FP32_TOL and rel_err(to_np(cu), P_ref[:, 1]) <= FP32_TOL
+        G = synthetic.rng(3).standard_normal(V.shape).astype(np.float32)
+        gU_ref, gV_ref = so.affine_scan_sequential_backward(U.double().numpy(), V.double().numpy(),
+                                                            G.astype(np.float64))
+        gU, gV = das.affine_scan_sequential_backward(Ug, Vg, torch.from_numpy(G).to(gpu))
+        torch.cuda.synchronize()
+        assert rel_err(to_np(gU), gU_ref) <= FP32_TOL and rel_err(to_np(gV), gV_ref) <= FP32_TOL
+    with pytest.raises(ValueError):
+        das.affine_scan_block_reference(Ug, Vg, carry_scan="bogus")
+    with pytest.raises(ValueError):
+        das.affine_scan_block_reference(Ug, Vg, block_size=0)
+
+
 def test_cfg4_dense_cayley_full_size(gpu):
     """H=8, d_h=32, B=1, L=16384, fp32, A_t = gate * Cayley(W_t),
     B_t = v k^T; output S_t for every step."""

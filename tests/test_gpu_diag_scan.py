@@ -122,7 +122,7 @@ def test_cfg2_fp32_full_size(gpu, L):
     assert rel_err(to_np(h), ref) <= FP32_TOL
 
 
-@pytest.mark.parametrize("L", [8192, 32768])
+@pytest.mark.parametrize("L", [8192, 16384, 32768])
 def test_cfg2_bf16_io_full_size(gpu, L):
     announce(f"diag cfg2 bf16 L={L}")
     import mogt_amd
