@@ -124,6 +124,18 @@ int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                float damping, int z_dtype, int v_dtype, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
+/* mogt_coupled_rank_scan_fwd (fp32 gate logits) that also writes
+ * row_stats [B, L, ceil(R*C / 64)] fp32: the sum of squares of the fp32 state
+ * h over each group of 64 consecutive features, i.e. the statistics of the
+ * RMSNorm norm_out that reads h (model_mogt.py:236-241).  With them h can be
+ * written in the read-out GEMM's dtype and normalised after the GEMM, since
+ * theta_read(norm_out(h))_t = r_t W diag(w) h_t with r_t =
+ * rsqrt(sum(row_stats[t]) / (R*C) + eps) (mogt_add_rmsnorm_rowscale_fwd).
+ * Workspace: mogt_coupled_rank_scan_workspace_bytes.                       */
+int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, void* h, float* row_stats,
+                                     int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                     float damping, int v_dtype, int out_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream);
 /* mogt_coupled_rank_scan_fwd with an explicit tile, one of
  * mogt_diag_scan_tiles(2) whose vector divides `channels` (v and h aligned to
  * it, up to 16 bytes); for sweeps and tile coverage tests.  Workspace:
@@ -238,6 +250,16 @@ int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float
                          int z_dtype, int out_dtype, void* stream);
 int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
                       void* stream);
+/* mogt_add_rmsnorm_fwd for a read-out of an unnormalised row: z = W diag(w) h
+ * (theta_read with norm_out's weight folded in), row_stats [rows, n_stats] the
+ * partial sums of squares of h (mogt_coupled_rank_scan_stats_fwd).  With r =
+ * rsqrt(sum(row_stats[row]) / dim + stat_eps):  Z = round(r z) (the
+ * reference's theta_read(norm_out(h)) in z's dtype), x_out = x + round(scale
+ * Z), out = rmsnorm(x_out) * weight -- model_mogt.py:236-256.             */
+int mogt_add_rmsnorm_rowscale_fwd(const float* x, const void* z, const float* row_stats,
+                                  int64_t n_stats, float stat_eps, float scale, const float* weight,
+                                  float* x_out, void* out, int64_t rows, int64_t dim, float eps,
+                                  int z_dtype, int out_dtype, void* stream);
 
 /* Backward of the row kernels (the autograd of RMSNorm and SwiGLU,
  * model_mogt.py:15-20, 29-30, as torch differentiates the reference's

@@ -55,6 +55,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int,
          _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_coupled_rank_scan_stats_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_int,
+         _c_void_p, _c_size, _c_void_p],
+    ),
     "mogt_coupled_rank_scan_fwd_cfg": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_int, _c_int,
@@ -96,6 +101,10 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
          _c_int, _c_int, _c_void_p]),
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_add_rmsnorm_rowscale_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_float, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64,
+         _c_i64, _c_float, _c_int, _c_int, _c_void_p]),
     "mogt_rmsnorm_bwd": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
                  _c_int, _c_int, _c_int, _c_void_p, _c_float, _c_int, _c_void_p]),

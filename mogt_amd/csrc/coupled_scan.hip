@@ -20,6 +20,22 @@ int coupled_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
                      t.vec, t.lanes, t.steps, t.waves);
 }
 
+// Tiles of the row-statistics variant: the default tiles, all 64 features
+// wide, so the statistics have one column per 64 features whatever the pick.
+#define MOGT_COUPLED_STAT_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(2, 32, 8, 16) X(2, 32, 16, 8) X(1, 64, 8, 16) \
+    X(1, 64, 32, 16) X(1, 64, 16, 16)
+
+template <typename TV, typename TO>
+int coupled_stat_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
+#define MOGT_CASE(V_, F_, S_, W_)                                          \
+    if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) \
+        return diag_launch<MODE_COUPLED, TV, float, TO, V_, F_, S_, W_, false, true>(prm, st);
+    MOGT_COUPLED_STAT_TILES(MOGT_CASE)
+#undef MOGT_CASE
+    return set_error(MOGT_E_INVALID, "coupled scan statistics: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
+                     t.vec, t.lanes, t.steps, t.waves);
+}
+
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 
 // Default tile (measured on MI355X at r = 16, c = 48, L = 8k..32k): four
@@ -49,7 +65,7 @@ int coupled_alignment(const void* v, const void* h, int v_dtype, int out_dtype) 
 
 int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int64_t R, int64_t C,
                 float damping, int z_dtype, int v_dtype, int out_dtype, const DiagTile& t,
-                void* ws, size_t ws_bytes, void* stream) {
+                void* ws, size_t ws_bytes, void* stream, float* row_stats = nullptr) {
     const int64_t D = R * C;
     if (C % t.vec != 0)
         return set_error(MOGT_E_INVALID, "channels %lld not a multiple of vec %d", (long long)C, t.vec);
@@ -63,8 +79,16 @@ int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int
     prm.R = static_cast<int>(R);
     prm.C = static_cast<int>(C);
     prm.damping = damping;
+    prm.rowstat = row_stats;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool zb = z_dtype == MOGT_BF16, vb = v_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
+    if (row_stats) {
+        if (zb) return set_error(MOGT_E_INVALID, "coupled scan statistics: gate logits must be fp32");
+        if (t.vec * t.lanes != 64)
+            return set_error(MOGT_E_INVALID, "coupled scan statistics: tile must be 64 features wide");
+        if (vb) return ob ? coupled_stat_dispatch<bf16_t, bf16_t>(prm, t, st) : coupled_stat_dispatch<bf16_t, float>(prm, t, st);
+        return ob ? coupled_stat_dispatch<float, bf16_t>(prm, t, st) : coupled_stat_dispatch<float, float>(prm, t, st);
+    }
     if (!zb && vb && !ob) return coupled_dispatch<float, bf16_t, float>(prm, t, st);
     if (!zb && vb && ob) return coupled_dispatch<float, bf16_t, bf16_t>(prm, t, st);
     if (zb && vb && !ob) return coupled_dispatch<bf16_t, bf16_t, float>(prm, t, st);
@@ -110,6 +134,22 @@ extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h,
                                     coupled_alignment(v, h, v_dtype, out_dtype));
     return coupled_run(z, v, h, batch, length, rank, channels, damping, z_dtype, v_dtype, out_dtype,
                        t, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, void* h, float* row_stats,
+                                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                                float damping, int v_dtype, int out_dtype, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "rank and channels must be positive");
+    if (!dtype_ok(v_dtype) || !dtype_ok(out_dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!z || !v || !h || !row_stats) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    const DiagTile t = coupled_tile(batch, length, rank, channels, coupled_alignment(v, h, v_dtype, out_dtype));
+    return coupled_run(z, v, h, batch, length, rank, channels, damping, MOGT_F32, v_dtype, out_dtype, t,
+                       workspace, workspace_bytes, stream, row_stats);
 }
 
 // The same with an explicit tile (sweeps and tests): the tile must be one of

@@ -70,12 +70,32 @@ struct DiagParams {
     uint32_t* seen;     // [G * n_ch] per-chunk "epoch read" words
     uint64_t* pay;      // 2 planes of [G][n_ch][FW] words: A, H
     int64_t plane;      // words per plane
+    float* rowstat;     // COUPLED with ROWSTAT: [B, L, n_fg] sums of squares of h
 };
 
 constexpr uint32_t ST_NONE = 0u;
 
+// Sum over the lanes of one row of a chunk (FWL consecutive lanes), returned
+// in every lane of the row.  A 16-lane row is one DPP row: quad swaps, then
+// the half-row and row mirrors; wider rows add cross-row shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <int FWL>
+__device__ __forceinline__ float row_lanes_sum(float v) {
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);   // row_half_mirror
+    v += dpp_f32<0x140>(v);   // row_mirror
+    if constexpr (FWL >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (FWL >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX>
+          bool PREFIX, bool ROWSTAT = false>
 __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int NT = 64 * WT;
     constexpr int Q = 64 / FWL;       // step groups per wave (rows per vector load)
@@ -93,6 +113,10 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     // DIAG bf16 raw a and b words (two values per word); COUPLED the gate logit
     // (then the gate) and the raw v words.
     static_assert(!(PREFIX && GATED), "prefix output is a DIAG-mode option");
+    // ROWSTAT: per (row, feature group) sum of squares of the fp32 outputs, the
+    // statistics of the RMSNorm that reads h (model_mogt.py:240), so h can
+    // leave in the GEMM's dtype without a separate normalisation pass
+    static_assert(!ROWSTAT || COUPLED, "row statistics are a COUPLED-mode option");
 
     __shared__ int s_pending[2];
     __shared__ float s_cwA[VW][FW];   // level-1 summaries, then exclusive prefixes over VW
@@ -385,6 +409,17 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 if constexpr (PREFIX) Ap[v] *= av;
                 o[v] = hh[v];
             }
+            if constexpr (ROWSTAT) {
+                // features past D hold h = 0 (identity steps); every lane of the
+                // row takes part, the row's first lane (always a valid feature)
+                // stores the group's sum
+                float sq = 0.0f;
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) sq = fmaf(o[v], o[v], sq);
+                sq = row_lanes_sum<FWL>(sq);
+                if ((lane % FWL) == 0 && s < nv)
+                    p.rowstat[(row0 + t0 + s) * p.n_fg + fg] = sq;
+            }
             if (s < nv) {
                 const int off = (q * S + s) * Ds + flane;
                 store_stream<TOut, VEC>(ph + off, o);
@@ -499,10 +534,10 @@ inline int diag_prepare(DiagParams& prm, int64_t B, int64_t L, int64_t D, const 
 }
 
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX>
+          bool PREFIX, bool ROWSTAT = false>
 int diag_launch(const DiagParams& prm, hipStream_t stream) {
     const int grid = prm.G * prm.n_ch;
-    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX>), dim3(grid),
+    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX, ROWSTAT>), dim3(grid),
                        dim3(64 * WT), 0, stream, prm);
     return check_launch("diag_scan_kernel");
 }

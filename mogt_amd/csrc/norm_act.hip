@@ -24,14 +24,25 @@ template <typename T> __device__ __forceinline__ float rnd(float v) { return IO<
 constexpr int NA_WAVES = 4;   // rows per work-group
 
 // VPL = 4-element vectors per lane (row length <= 256 * VPL).
-template <typename TX, typename TZ, typename TO, int VPL, bool ADD>
+// ROWSCALE (with ADD): z is a read-out computed from an unnormalised input
+// row, zr = W diag(w_out) h; the row's RMSNorm factor r = rsqrt(sum of the
+// n_stat partial sums of squares of h / D + stat_eps) turns it into
+// Z = round(r zr) = theta_read(norm_out(h)) before the residual update.
+template <typename TX, typename TZ, typename TO, int VPL, bool ADD, bool ROWSCALE = false>
 __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
     const TX* __restrict__ x, const TZ* __restrict__ z, float scale, const float* __restrict__ w,
-    float* __restrict__ x_out, TO* __restrict__ out, int64_t rows, int D, float eps) {
+    float* __restrict__ x_out, TO* __restrict__ out, int64_t rows, int D, float eps,
+    const float* __restrict__ rowstat = nullptr, int n_stat = 0, float stat_eps = 0.0f) {
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * NA_WAVES + (threadIdx.x >> 6);
     if (row >= rows) return;
     const TX* xr = x + row * D;
+    float zscale = 1.0f;
+    if constexpr (ROWSCALE) {
+        float t = 0.0f;
+        for (int i = lane; i < n_stat; i += 64) t += rowstat[row * n_stat + i];
+        zscale = rsqrtf(wave_sum(t) / static_cast<float>(D) + stat_eps);
+    }
     float v[VPL][4];
     float ss = 0.0f;
 #pragma unroll
@@ -42,6 +53,10 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
             if constexpr (ADD) {
                 float zz[4];
                 load_vec<TZ, 4>(z + row * D + c, zz);
+                if constexpr (ROWSCALE) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) zz[e] = rnd<TZ>(zscale * zz[e]);
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[k][e] += rnd<TZ>(scale * zz[e]);
                 store_vec<float, 4>(x_out + row * D + c, v[k]);
@@ -297,20 +312,21 @@ int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* 
     return set_error(MOGT_E_INVALID, "rmsnorm_bwd: row length %d > 4096", D);
 }
 
-template <typename TX, typename TZ, typename TO, bool ADD>
+template <typename TX, typename TZ, typename TO, bool ADD, bool ROWSCALE = false>
 int launch_norm(const void* x, const void* z, float scale, const float* w, float* x_out, void* out,
-                int64_t rows, int D, float eps, hipStream_t st) {
+                int64_t rows, int D, float eps, hipStream_t st, const float* rowstat = nullptr, int n_stat = 0,
+                float stat_eps = 0.0f) {
     const int vpl = (D + 255) / 256;
     const dim3 grid(static_cast<unsigned>((rows + NA_WAVES - 1) / NA_WAVES));
     const dim3 block(64 * NA_WAVES);
     const TX* xp = static_cast<const TX*>(x);
     const TZ* zp = static_cast<const TZ*>(z);
     TO* op = static_cast<TO*>(out);
-#define MOGT_NORM_CASE(V)                                                                      \
-    if (vpl <= V) {                                                                             \
-        hipLaunchKernelGGL((rmsnorm_kernel<TX, TZ, TO, V, ADD>), grid, block, 0, st, xp, zp,    \
-                           scale, w, x_out, op, rows, D, eps);                                  \
-        return check_launch("rmsnorm_kernel");                                                  \
+#define MOGT_NORM_CASE(V)                                                                            \
+    if (vpl <= V) {                                                                                   \
+        hipLaunchKernelGGL((rmsnorm_kernel<TX, TZ, TO, V, ADD, ROWSCALE>), grid, block, 0, st, xp, zp, \
+                           scale, w, x_out, op, rows, D, eps, rowstat, n_stat, stat_eps);             \
+        return check_launch("rmsnorm_kernel");                                                        \
     }
     MOGT_NORM_CASE(1)
     MOGT_NORM_CASE(2)
@@ -371,6 +387,34 @@ extern "C" int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, 
     if (z_dtype == MOGT_BF16 && out_dtype == MOGT_F32)
         return launch_norm<float, bf16_t, float, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
     return launch_norm<float, bf16_t, bf16_t, true>(x, z, scale, weight, x_out, out, rows, D, eps, st);
+}
+
+extern "C" int mogt_add_rmsnorm_rowscale_fwd(const float* x, const void* z, const float* row_stats,
+                                             int64_t n_stats, float stat_eps, float scale, const float* weight,
+                                             float* x_out, void* out, int64_t rows, int64_t dim, float eps,
+                                             int z_dtype, int out_dtype, void* stream) {
+    clear_error();
+    int rc = check_norm_args(rows, dim);
+    if (rc) return rc;
+    if (!dt_ok(z_dtype) || !dt_ok(out_dtype)) return set_error(MOGT_E_INVALID, "add_rmsnorm_rowscale: dtype");
+    if (n_stats <= 0 || n_stats > 4096)
+        return set_error(MOGT_E_INVALID, "add_rmsnorm_rowscale: 1 <= n_stats <= 4096");
+    if (rows == 0) return MOGT_OK;
+    if (!x || !z || !row_stats || !weight || !x_out || !out)
+        return set_error(MOGT_E_INVALID, "add_rmsnorm_rowscale: null pointer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int D = static_cast<int>(dim), ns = static_cast<int>(n_stats);
+    if (z_dtype == MOGT_F32 && out_dtype == MOGT_F32)
+        return launch_norm<float, float, float, true, true>(x, z, scale, weight, x_out, out, rows, D, eps, st,
+                                                            row_stats, ns, stat_eps);
+    if (z_dtype == MOGT_F32 && out_dtype == MOGT_BF16)
+        return launch_norm<float, float, bf16_t, true, true>(x, z, scale, weight, x_out, out, rows, D, eps, st,
+                                                             row_stats, ns, stat_eps);
+    if (z_dtype == MOGT_BF16 && out_dtype == MOGT_F32)
+        return launch_norm<float, bf16_t, float, true, true>(x, z, scale, weight, x_out, out, rows, D, eps, st,
+                                                             row_stats, ns, stat_eps);
+    return launch_norm<float, bf16_t, bf16_t, true, true>(x, z, scale, weight, x_out, out, rows, D, eps, st,
+                                                          row_stats, ns, stat_eps);
 }
 
 extern "C" int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,

@@ -414,9 +414,25 @@ class MOGTBlock(_WeightCacheOwner):
         with torch.autograd.profiler.record_function("mogt.value_projection"):
             v_raw = F.linear(xn, _gemm_weight(self, "phi_val", (self.phi_val.weight,), lambda: self.phi_val.weight))
             z = self._gate_logits(xn, prefix_condition)
+        damping = float(getattr(self, "connection_damping", 0.999))
+        if not torch.is_grad_enabled():
+            # inference: norm_out folded around the read-out GEMM.  The scan
+            # writes h in the GEMM's dtype plus per-row sums of squares; the
+            # GEMM runs against theta_read * norm_out.weight; the next RMSNorm
+            # applies each row's factor rsqrt(mean(h^2) + eps) as it reads Z.
+            with torch.autograd.profiler.record_function("mogt.affine_scan"):
+                h, stats = ops.coupled_rank_scan_stats(z, v_raw, damping=damping, out_dtype=gemm_dtype)
+            with torch.autograd.profiler.record_function("mogt.readout"):
+                Zr = F.linear(h, _gemm_weight(self, "theta_read_folded", (self.theta_read.weight, self.norm_out.weight),
+                                              lambda: self.theta_read.weight * self.norm_out.weight))
+            with torch.autograd.profiler.record_function("mogt.ffn"):
+                x, xn2 = ops.add_rmsnorm_rowscale(x, Zr, stats, self._residual_scale(Zr), self.norm_ffn.weight,
+                                                  stat_eps=self.norm_out.eps, eps=self.norm_ffn.eps,
+                                                  out_dtype=gemm_dtype)
+                f = self.ffn(xn2)
+            return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
         with torch.autograd.profiler.record_function("mogt.affine_scan"):
-            h = ops.coupled_rank_scan(z, v_raw, damping=float(getattr(self, "connection_damping", 0.999)),
-                                      out_dtype=torch.float32)
+            h = ops.coupled_rank_scan(z, v_raw, damping=damping, out_dtype=torch.float32)
         with torch.autograd.profiler.record_function("mogt.readout"):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
             Z = F.linear(hn, _gemm_weight(self, "theta_read", (self.theta_read.weight,),

@@ -365,6 +365,51 @@ def _coupled_backward(ctx, grad_h):
 torch.library.register_autograd("mogt::coupled_rank_scan", _coupled_backward, setup_context=_coupled_setup)
 
 
+STAT_GROUP = 64   # features per column of the coupled scan's row statistics
+
+
+@torch.library.custom_op("mogt::coupled_rank_scan_stats", mutates_args=())
+def _coupled_rank_scan_stats_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: float,
+                                out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    z = z.contiguous().to(torch.float32)
+    v = v.contiguous()
+    B, L, D = v.shape
+    C = D // rank
+    h = torch.empty(v.shape, dtype=out_dtype, device=v.device)
+    stats = torch.empty((B, L, -(-D // STAT_GROUP)), dtype=torch.float32, device=v.device)
+    vc = dtype_code(v.dtype, "coupled_rank_scan_stats")
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, vc), v.device)
+    rc = lib.mogt_coupled_rank_scan_stats_fwd(z.data_ptr(), v.data_ptr(), h.data_ptr(), stats.data_ptr(), B, L,
+                                              rank, C, float(damping), vc,
+                                              dtype_code(out_dtype, "coupled_rank_scan_stats"), ws.data_ptr(),
+                                              ws.numel(), _stream_handle(v.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_stats_fwd")
+    _checked(ws, "mogt_coupled_rank_scan_stats_fwd")
+    return h, stats
+
+
+@_coupled_rank_scan_stats_op.register_fake
+def _(z, v, rank, damping, out_dtype):
+    B, L, D = v.shape
+    return v.new_empty(v.shape, dtype=out_dtype), v.new_empty((B, L, -(-D // STAT_GROUP)), dtype=torch.float32)
+
+
+def coupled_rank_scan_stats(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,
+                            out_dtype: torch.dtype = torch.float32) -> tuple[torch.Tensor, torch.Tensor]:
+    """``coupled_rank_scan`` that also returns the row statistics of the RMSNorm
+    reading its output: ``stats[b, t, k]`` = sum of ``h[b, t, 64k:64k+64]**2`` in
+    the fp32 state (before ``out_dtype`` rounding).  No autograd: the
+    inference read-out (``add_rmsnorm_rowscale``) consumes them."""
+    require_cuda("coupled_rank_scan_stats", gate_logits, v_raw)
+    if gate_logits.ndim != 3 or v_raw.ndim != 3:
+        raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
+    B, L, r = gate_logits.shape
+    if v_raw.shape[:2] != (B, L) or v_raw.shape[2] % r != 0:
+        raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
+    return torch.ops.mogt.coupled_rank_scan_stats(gate_logits, v_raw, r, float(damping), out_dtype)
+
+
 def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,
                       out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Fused gate + scan of the coupled write-forget MOGT mixer.
@@ -665,6 +710,50 @@ def add_rmsnorm(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Te
     if x.shape != z.shape:
         raise ValueError("x and z must have the same shape")
     return torch.ops.mogt.add_rmsnorm(x, z, float(scale), weight, float(eps), out_dtype)
+
+
+@torch.library.custom_op("mogt::add_rmsnorm_rowscale", mutates_args=())
+def _add_rmsnorm_rowscale_op(x: torch.Tensor, z: torch.Tensor, stats: torch.Tensor, stat_eps: float, scale: float,
+                             weight: torch.Tensor, eps: float, out_dtype: torch.dtype
+                             ) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    x = x.contiguous()
+    z = z.contiguous()
+    stats = stats.contiguous()
+    w = weight.contiguous().to(torch.float32)
+    D = x.shape[-1]
+    rows = x.numel() // D
+    x_out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    rc = lib.mogt_add_rmsnorm_rowscale_fwd(x.data_ptr(), z.data_ptr(), stats.data_ptr(), stats.shape[-1],
+                                           float(stat_eps), float(scale), w.data_ptr(), x_out.data_ptr(),
+                                           out.data_ptr(), rows, D, float(eps),
+                                           dtype_code(z.dtype, "add_rmsnorm_rowscale"),
+                                           dtype_code(out_dtype, "add_rmsnorm_rowscale"), _stream_handle(x.device))
+    _lib.check(rc, "mogt_add_rmsnorm_rowscale_fwd")
+    return x_out, out
+
+
+@_add_rmsnorm_rowscale_op.register_fake
+def _(x, z, stats, stat_eps, scale, weight, eps, out_dtype):
+    return x.new_empty(x.shape, dtype=torch.float32), x.new_empty(x.shape, dtype=out_dtype)
+
+
+def add_rmsnorm_rowscale(x: torch.Tensor, z: torch.Tensor, stats: torch.Tensor, scale: float,
+                         weight: torch.Tensor, *, stat_eps: float = 1e-6, eps: float = 1e-6,
+                         out_dtype: torch.dtype = torch.float32):
+    """``add_rmsnorm`` whose residual term is normalised per row first:
+    ``Z = z * rsqrt(sum(stats[row]) / D + stat_eps)`` (rounded to z's dtype),
+    ``x' = x + scale * Z``, ``out = rmsnorm(x') * weight``.  For ``z = h @ (W
+    diag(w_out))^T`` and ``stats`` from ``coupled_rank_scan_stats`` it equals
+    ``theta_read(norm_out(h))`` added to the residual stream.  No autograd."""
+    require_cuda("add_rmsnorm_rowscale", x, z, stats, weight)
+    if x.dtype != torch.float32:
+        raise ValueError("add_rmsnorm_rowscale keeps the residual stream in float32")
+    if x.shape != z.shape or stats.shape[:-1] != x.shape[:-1] or stats.dtype != torch.float32:
+        raise ValueError("x and z must have the same shape and stats must be float32 [..., n_stats]")
+    return torch.ops.mogt.add_rmsnorm_rowscale(x, z, stats, float(stat_eps), float(scale), weight, float(eps),
+                                               out_dtype)
 
 
 @torch.library.custom_op("mogt::silu_mul", mutates_args=())

@@ -199,6 +199,43 @@ def test_coupled_rank_scan(gpu, L, r, c, vdt):
     assert float(np.median(err)) <= 1e-6   # the bulk is exact to fp32 accumulation
 
 
+@pytest.mark.parametrize("B,L,r,c,vdt,odt", [(2, 1000, 16, 48, "bf16", "bf16"), (1, 32768, 16, 48, "bf16", "bf16"),
+                                              (1, 300, 4, 8, "fp32", "fp32"), (2, 517, 4, 24, "bf16", "fp32"),
+                                              (1, 77, 3, 20, "fp32", "bf16")])
+def test_coupled_rank_scan_row_statistics(gpu, B, L, r, c, vdt, odt):
+    """The statistics variant: the same h (in out_dtype), and per row and group
+    of 64 features the sum of squares of the fp32 state (groups past D hold
+    fewer features); against the oracle's float64 h."""
+    announce(f"coupled scan statistics B={B} L={L} r={r} c={c} v={vdt} out={odt}")
+    from mogt_amd import ops
+
+    z, v = synthetic.coupled_inputs(B, L, r, c, seed=L + r)
+    zt = torch.from_numpy(z).to(gpu)
+    vt = torch.from_numpy(v).to(gpu)
+    if vdt == "bf16":
+        vt = vt.bfloat16()
+    odt_t = torch.bfloat16 if odt == "bf16" else torch.float32
+    h, stats = ops.coupled_rank_scan_stats(zt, vt, damping=0.997, out_dtype=odt_t)
+    h32 = ops.coupled_rank_scan(zt, vt, damping=0.997, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = so.coupled_rank_scan(z, to_np(vt), r, damping=0.997, v_is_bf16=vdt == "bf16")
+    D = r * c
+    G = -(-D // 64)
+    assert h.dtype == odt_t and stats.shape == (B, L, G)
+    # the scan against the oracle (bf16 v: a last-bit difference of the fp32
+    # sigmoid can flip the bf16 rounding of v * g -> bf16 bar, exact bulk)
+    err = np.abs(to_np(h32).astype(np.float64) - ref) / np.max(np.abs(ref))
+    assert float(err.max()) <= (BF16_TOL if vdt == "bf16" else FP32_TOL)
+    assert float(np.median(err)) <= 1e-6
+    # the statistics variant against the same arithmetic without statistics
+    h64 = to_np(h32).astype(np.float64)
+    assert rel_err(to_np(h), h64) <= (2.0 ** -8 if odt == "bf16" else 1e-6)
+    pad = np.zeros((B, L, G * 64))
+    pad[..., :D] = h64
+    ref_stats = (pad.reshape(B, L, G, 64) ** 2).sum(-1)
+    assert rel_err(to_np(stats), ref_stats) <= 1e-5
+
+
 @pytest.mark.parametrize("vdt", ["fp32", "bf16"])
 @pytest.mark.parametrize("tile", TILES_COUPLED)
 def test_every_coupled_tile(gpu, tile, vdt):

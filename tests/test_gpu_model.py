@@ -73,6 +73,31 @@ def test_rmsnorm_add_and_silu_kernels(gpu):
     assert rel_err(to_np(sb), ref_sb.numpy()) <= BF16_TOL
 
 
+@pytest.mark.parametrize("zdt,odt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
+def test_add_rmsnorm_rowscale_kernel(gpu, zdt, odt):
+    """x' = x + s round(r z), r = rsqrt(sum(stats) / D + eps): the residual
+    update of the read-out folded around the GEMM, against float64 (z given in
+    its dtype, so only the two roundings of the product differ)."""
+    announce(f"add_rmsnorm_rowscale z={zdt} out={odt}")
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(8)
+    rows, D = 3001, 768
+    x = torch.randn(rows, D, generator=g)
+    z = (torch.randn(rows, D, generator=g) * 30).to(zdt)
+    h = torch.randn(rows, D, generator=g) * 3
+    stats = (h.double() ** 2).reshape(rows, D // 64, 64).sum(-1).float()
+    w = 1.0 + 0.1 * torch.randn(D, generator=g)
+    x_new, out = ops.add_rmsnorm_rowscale(x.to(gpu), z.to(gpu), stats.to(gpu), 0.7, w.to(gpu), stat_eps=1e-6,
+                                          eps=1e-6, out_dtype=odt)
+    torch.cuda.synchronize()
+    r = torch.rsqrt(h.double().pow(2).mean(-1, keepdim=True) + 1e-6)
+    x_ref = x.double() + 0.7 * (r * z.double())
+    tol = BF16_TOL if zdt == torch.bfloat16 else 1e-5
+    assert rel_err(to_np(x_new), x_ref.numpy()) <= tol
+    assert rel_err(to_np(out), mo.rmsnorm(x_ref, w.double()).numpy()) <= tol
+
+
 @pytest.mark.parametrize("L", [64, 1000])
 def test_fused_block_matches_oracle_fp32(gpu, L):
     announce(f"fused MOGT block fp32 L={L}")
