@@ -136,6 +136,22 @@ int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, void* h, floa
                                      int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                      float damping, int v_dtype, int out_dtype,
                                      void* workspace, size_t workspace_bytes, void* stream);
+/* mogt_coupled_rank_scan_stats_fwd fed by one projection GEMM: row t of
+ * proj [B, L, ld_proj] holds v (columns 0 .. R*C-1, phi_val's output) and, from
+ * column gate_col, the value gate's pre-logits for the current token (R
+ * columns) and, when gate_prev = 1, for the previous token (the next R
+ * columns).  The gate logit is z[t][i] = proj[t][gate_col + i] +
+ * (gate_prev && t > 0 ? proj[t-1][gate_col + R + i] : 0) + gate_const[b][i]
+ * (gate_const [B, R] fp32: bias + prefix term, nullable) -- phi_value_gate
+ * over [x_t, x_{t-1}, prefix] (model_mogt.py:104-122, 166-182) without the
+ * concatenated input.  proj and h share `dtype`; row_stats as in
+ * mogt_coupled_rank_scan_stats_fwd.  Workspace:
+ * mogt_coupled_rank_scan_workspace_bytes.                                 */
+int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj, int64_t gate_col, int gate_prev,
+                                    const float* gate_const, void* h, float* row_stats,
+                                    int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                    float damping, int dtype,
+                                    void* workspace, size_t workspace_bytes, void* stream);
 /* mogt_coupled_rank_scan_fwd with an explicit tile, one of
  * mogt_diag_scan_tiles(2) whose vector divides `channels` (v and h aligned to
  * it, up to 16 bytes); for sweeps and tile coverage tests.  Workspace:

@@ -36,6 +36,19 @@ int coupled_stat_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t 
                      t.vec, t.lanes, t.steps, t.waves);
 }
 
+// Projection-fed gates (GPROJ) with statistics: v, the gate pre-logits and h
+// share one dtype T.
+template <typename T>
+int coupled_proj_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
+#define MOGT_CASE(V_, F_, S_, W_)                                          \
+    if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) \
+        return diag_launch<MODE_COUPLED, T, T, T, V_, F_, S_, W_, false, true, true>(prm, st);
+    MOGT_COUPLED_STAT_TILES(MOGT_CASE)
+#undef MOGT_CASE
+    return set_error(MOGT_E_INVALID, "coupled scan statistics: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
+                     t.vec, t.lanes, t.steps, t.waves);
+}
+
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 
 // Default tile (measured on MI355X at r = 16, c = 48, L = 8k..32k): four
@@ -63,9 +76,19 @@ int coupled_alignment(const void* v, const void* h, int v_dtype, int out_dtype) 
 
 }  // namespace
 
+// proj: null, or the projection-fed gate (GPROJ) with z the pre-logit columns
+// of the projection, row stride ldz, and gate_prev / gconst as in DiagParams;
+// ldv: row stride of v (0: R * C).
+struct CoupledProj {
+    int64_t ldz;
+    int gate_prev;
+    const float* gconst;
+};
+
 int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int64_t R, int64_t C,
                 float damping, int z_dtype, int v_dtype, int out_dtype, const DiagTile& t,
-                void* ws, size_t ws_bytes, void* stream, float* row_stats = nullptr) {
+                void* ws, size_t ws_bytes, void* stream, float* row_stats = nullptr, int64_t ldv = 0,
+                const CoupledProj* proj = nullptr) {
     const int64_t D = R * C;
     if (C % t.vec != 0)
         return set_error(MOGT_E_INVALID, "channels %lld not a multiple of vec %d", (long long)C, t.vec);
@@ -80,8 +103,20 @@ int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int
     prm.C = static_cast<int>(C);
     prm.damping = damping;
     prm.rowstat = row_stats;
+    prm.ldz = prm.R;
+    if (ldv) prm.ldv = ldv;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool zb = z_dtype == MOGT_BF16, vb = v_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
+    if (proj) {
+        prm.ldz = proj->ldz;
+        prm.gate_prev = proj->gate_prev;
+        prm.gconst = proj->gconst;
+        if (!row_stats || zb != vb || vb != ob)
+            return set_error(MOGT_E_INVALID, "projection-fed coupled scan: one dtype and row statistics");
+        if (t.vec * t.lanes != 64)
+            return set_error(MOGT_E_INVALID, "coupled scan statistics: tile must be 64 features wide");
+        return vb ? coupled_proj_dispatch<bf16_t>(prm, t, st) : coupled_proj_dispatch<float>(prm, t, st);
+    }
     if (row_stats) {
         if (zb) return set_error(MOGT_E_INVALID, "coupled scan statistics: gate logits must be fp32");
         if (t.vec * t.lanes != 64)
@@ -150,6 +185,32 @@ extern "C" int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, vo
     const DiagTile t = coupled_tile(batch, length, rank, channels, coupled_alignment(v, h, v_dtype, out_dtype));
     return coupled_run(z, v, h, batch, length, rank, channels, damping, MOGT_F32, v_dtype, out_dtype, t,
                        workspace, workspace_bytes, stream, row_stats);
+}
+
+extern "C" int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj, int64_t gate_col, int gate_prev,
+                                               const float* gate_const, void* h, float* row_stats, int64_t batch,
+                                               int64_t length, int64_t rank, int64_t channels, float damping,
+                                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "rank and channels must be positive");
+    if (!dtype_ok(dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    const int64_t D = rank * channels;
+    if (gate_prev != 0 && gate_prev != 1) return set_error(MOGT_E_INVALID, "gate_prev must be 0 or 1");
+    if (gate_col < D || gate_col + rank * (1 + gate_prev) > ld_proj || ld_proj > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "projection row of %lld columns cannot hold v (%lld) and the gate "
+                         "pre-logits at column %lld", (long long)ld_proj, (long long)D, (long long)gate_col);
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!proj || !h || !row_stats) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    // the vector must divide the projection's row stride as well as the channels
+    const int al = coupled_alignment(proj, h, dtype, dtype);
+    const int vec_ok = ld_proj % 4 == 0 ? al : (ld_proj % 2 == 0 ? (al < 2 ? al : 2) : 1);
+    const DiagTile t = coupled_tile(batch, length, rank, channels, vec_ok);
+    const size_t esz = dtype == MOGT_BF16 ? 2 : 4;
+    const CoupledProj pj{ld_proj, gate_prev, gate_const};
+    return coupled_run(static_cast<const char*>(proj) + gate_col * esz, proj, h, batch, length, rank, channels,
+                       damping, dtype, dtype, dtype, t, workspace, workspace_bytes, stream, row_stats, ld_proj, &pj);
 }
 
 // The same with an explicit tile (sweeps and tests): the tile must be one of

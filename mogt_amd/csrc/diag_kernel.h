@@ -71,6 +71,10 @@ struct DiagParams {
     uint64_t* pay;      // 2 planes of [G][n_ch][FW] words: A, H
     int64_t plane;      // words per plane
     float* rowstat;     // COUPLED with ROWSTAT: [B, L, n_fg] sums of squares of h
+    int64_t ldv;        // COUPLED: row stride of v in elements (D, or wider inside a projection)
+    int64_t ldz;        // GATED: row stride of the gate logits (R), or of the projection (GPROJ)
+    int gate_prev;      // GPROJ: add the previous step's pre-logit (column R + i) when 1
+    const float* gconst;   // GPROJ: [B, R] per-sequence logit term (bias + prefix), or null
 };
 
 constexpr uint32_t ST_NONE = 0u;
@@ -95,7 +99,7 @@ __device__ __forceinline__ float row_lanes_sum(float v) {
 }
 
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX, bool ROWSTAT = false>
+          bool PREFIX, bool ROWSTAT = false, bool GPROJ = false>
 __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int NT = 64 * WT;
     constexpr int Q = 64 / FWL;       // step groups per wave (rows per vector load)
@@ -117,6 +121,12 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     // statistics of the RMSNorm that reads h (model_mogt.py:240), so h can
     // leave in the GEMM's dtype without a separate normalisation pass
     static_assert(!ROWSTAT || COUPLED, "row statistics are a COUPLED-mode option");
+    // GPROJ: the gate logit of rank i at step t is assembled from a projection
+    // row (the phi_value_gate pre-logits next to phi_val's output in one GEMM):
+    // z = P[t][i] + (gate_prev && t > 0 ? P[t-1][R + i] : 0) + gconst[b][i], the
+    // gate over [x_t, x_{t-1}, prefix] (model_mogt.py:104-122, 170-171) without
+    // the concatenated input or a separate logit tensor
+    static_assert(!GPROJ || COUPLED, "projection-fed gates are a COUPLED-mode option");
 
     __shared__ int s_pending[2];
     __shared__ float s_cwA[VW][FW];   // level-1 summaries, then exclusive prefixes over VW
@@ -184,36 +194,47 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     constexpr int NA = GATED ? 1 : (BF16_IN ? NWB : VEC);
     float ra[S][NA];      // DIAG fp32: a; DIAG bf16: raw a words; GATED: raw z, then decay
     uint32_t rb[S][NWB];  // raw words of b (DIAG) or v (COUPLED)
+    uint32_t rp[GPROJ ? S : 1];   // GPROJ: raw previous-step pre-logit
     int nv;               // valid steps of this lane (0 .. S)
+    int gi = 0;           // GATED: rank (gate index) of this lane's features
     {
         const int64_t r = p.L - t0;
         nv = !fvalid || r <= 0 ? 0 : (r >= S ? S : static_cast<int>(r));
         const int lastrel = static_cast<int>(p.L - 1 - tw);   // last row of the problem, from tw
         const int flc = fvalid ? flane : 0;
         const int64_t wbase = (rbase + (REV ? -tw : tw)) * p.D + fbase;
+        // v of the forward coupled scan may sit inside a wider projection row
+        const int64_t ldb = MODE == MODE_COUPLED ? p.ldv : p.D;
+        const int Dsb = MODE == MODE_COUPLED ? static_cast<int>(p.ldv) : Ds;
         // REV reads a one row later in memory (a_{t+1}), except for logical
         // step 0, whose a_L does not exist: it reads row L - 1 and uses a = 0
         // (step_a); clamped rows past the end map to step 0 too when L = 1
         const TIn* pa = static_cast<const TIn*>(p.a) + wbase;
-        const TIn* pb = static_cast<const TIn*>(p.b) + wbase;
+        const TIn* pb = static_cast<const TIn*>(p.b) + (rbase + (REV ? -tw : tw)) * ldb + fbase;
         const TZ* pz = nullptr;
-        int gi = 0;
         if constexpr (GATED) {
             // forward: the gate row of step tw + rel; REV: the row after it in
             // memory (a_{t+1}), row L - 1 for logical step 0 (decay unused)
-            pz = static_cast<const TZ*>(p.a) + (REV ? rbase - tw : row0 + tw) * p.R;
+            pz = static_cast<const TZ*>(p.a) + (REV ? rbase - tw : row0 + tw) * p.ldz;
             gi = static_cast<int>((fbase + flc) / p.C);
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int rel = min(q * S + s, lastrel);
             const int off = rel * Ds + flc;
-            load_raw<sizeof(TIn) * VEC>(pb + off, rb[s]);
+            load_raw<sizeof(TIn) * VEC>(pb + rel * Dsb + flc, rb[s]);
             if constexpr (GATED) {
                 uint32_t zw[1];
                 const int zrel = REV ? ((tw + rel != 0) ? 1 - rel : -rel) : rel;
-                load_raw_cached<sizeof(TZ)>(pz + zrel * p.R + gi, zw);
+                load_raw_cached<sizeof(TZ)>(pz + zrel * p.ldz + gi, zw);
                 ra[s][0] = __uint_as_float(zw[0]);
+                if constexpr (GPROJ) {
+                    // the previous step's row; step 0 of the sequence reads its
+                    // own row (in bounds) and drops the value
+                    const int prel = (tw + rel > 0) ? rel - 1 : rel;
+                    load_raw_cached<sizeof(TZ)>(pz + prel * p.ldz + p.R + gi, zw);
+                    rp[s] = zw[0];
+                }
             } else {
                 uint32_t aw[NA];
                 load_raw<sizeof(TIn) * VEC>(pa + off + ((REV && tw + rel != 0) ? Di : 0), aw);
@@ -230,10 +251,20 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
     // Steps outside the problem become the identity (a = 1, b = 0).  The
     // reverse mode only forms the decay (b is the incoming gradient).
     if constexpr (GATED) {
+        float zc = 0.0f;   // GPROJ: per-sequence logit term
+        if constexpr (GPROJ) {
+            if (p.gconst) zc = p.gconst[static_cast<int64_t>(bi) * p.R + gi];
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const uint32_t zb = __float_as_uint(ra[s][0]);
-            const float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
+            float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
+            if constexpr (GPROJ) {
+                const uint32_t pb = rp[s];
+                const float zp = std::is_same<TZ, bf16_t>::value ? __uint_as_float(pb << 16) : __uint_as_float(pb);
+                const bool has_prev = p.gate_prev && (tw + min(q * S + s, static_cast<int>(p.L - 1 - tw)) > 0);
+                z = (z + (has_prev ? zp : 0.0f)) + zc;
+            }
             const bool ok = s < nv;
             const float gg = sigmoidf_(z);
             ra[s][0] = ok ? p.damping * (1.0f - gg) : 1.0f;
@@ -522,6 +553,8 @@ inline int diag_prepare(DiagParams& prm, int64_t B, int64_t L, int64_t D, const 
                          ws_bytes);
     prm.L = L;
     prm.D = D;
+    prm.ldv = D;
+    prm.ldz = 1;
     prm.n_fg = geo.n_fg;
     prm.n_ch = geo.n_ch;
     prm.G = geo.G;
@@ -534,11 +567,11 @@ inline int diag_prepare(DiagParams& prm, int64_t B, int64_t L, int64_t D, const 
 }
 
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX, bool ROWSTAT = false>
+          bool PREFIX, bool ROWSTAT = false, bool GPROJ = false>
 int diag_launch(const DiagParams& prm, hipStream_t stream) {
     const int grid = prm.G * prm.n_ch;
-    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX, ROWSTAT>), dim3(grid),
-                       dim3(64 * WT), 0, stream, prm);
+    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX, ROWSTAT, GPROJ>),
+                       dim3(grid), dim3(64 * WT), 0, stream, prm);
     return check_launch("diag_scan_kernel");
 }
 

@@ -64,6 +64,7 @@ extern "C" int mogt_coupled_rank_scan_rev_fwd(const void* z, const float* dh, fl
     prm.h = G;
     prm.aprefix = nullptr;
     prm.R = static_cast<int>(rank);
+    prm.ldz = prm.R;
     prm.C = static_cast<int>(channels);
     prm.damping = damping;
     hipStream_t st = static_cast<hipStream_t>(stream);

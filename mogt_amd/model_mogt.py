@@ -398,48 +398,76 @@ class MOGTBlock(_WeightCacheOwner):
             const = pt if const is None else const + pt
         return (z if const is None else z + const).contiguous()
 
-    def forward_fused(self, x: torch.Tensor, prefix_condition, pending):
-        """Fused forward (differentiable: every kernel has its backward).  ``pending = (z, scale)`` is the previous
-        block's last residual term (added here inside the first RMSNorm).
-        Returns ``(x_after_mixer, (ffn_out, ffn_scale))``: the caller adds the
-        FFN term (or hands it to the next block)."""
-        ad = _autocast_dtype()
-        gemm_dtype = ad or x.dtype
-        eps = self.norm_mogt.eps
-        if pending is None:
-            xn = ops.rmsnorm(x, self.norm_mogt.weight, eps, out_dtype=gemm_dtype)
-        else:
-            x, xn = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_mogt.weight, eps,
-                                    out_dtype=gemm_dtype)
+    def _value_and_gate_projection(self, xn: torch.Tensor, prefix_condition: torch.Tensor | None):
+        """One GEMM of x against [phi_val; W_cur; W_prev]: v and the value gate's
+        pre-logits for the current and the previous token side by side, plus
+        the per-sequence logit term (bias + prefix term, fp32 [B, r] or [r]).
+        Returns (proj, has_prev, const)."""
+        gate: nn.Linear = self.phi_value_gate
+        parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
+        D = self.d_model
+        W = gate.weight
+        if W.shape[1] != len(parts) * D:
+            raise RuntimeError(f"phi_value_gate takes {W.shape[1]} inputs, the gate input mode builds "
+                               f"{len(parts) * D}")
+        cols = {name: W[:, i * D:(i + 1) * D] for i, name in enumerate(parts)}
+        stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
+        W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W), lambda: torch.cat(stacked, dim=0))
+        proj = F.linear(xn, W_all)
+        const = gate.bias.float() if gate.bias is not None else None
+        if "prefix" in cols and prefix_condition is not None:
+            pref = prefix_condition.to(dtype=xn.dtype).view(xn.size(0), D)
+            pt = F.linear(pref, cols["prefix"]).float()
+            const = pt if const is None else pt + const
+        return proj, "prev" in cols, const
+
+    def _mixer_inference(self, x, xn, prefix_condition, damping: float, gemm_dtype):
+        """Mixer of the fused path without autograd.  One GEMM gives phi_val's
+        output and the gate's pre-logits, which the scan combines into the
+        logits itself.  norm_out is folded around the read-out GEMM: the scan
+        writes h in the GEMM's dtype plus per-row sums of squares, the GEMM runs
+        against theta_read * norm_out.weight, and the next RMSNorm applies each
+        row's factor rsqrt(mean(h^2) + eps) as it reads Z."""
+        with torch.autograd.profiler.record_function("mogt.affine_scan"):
+            proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition)
+            h, stats = ops.coupled_rank_scan_proj(proj, self.d_model, rank=self.r, gate_prev=gate_prev,
+                                                  gate_const=gconst, damping=damping)
+        with torch.autograd.profiler.record_function("mogt.readout"):
+            Zr = F.linear(h, _gemm_weight(self, "theta_read_folded", (self.theta_read.weight, self.norm_out.weight),
+                                          lambda: self.theta_read.weight * self.norm_out.weight))
+        return ops.add_rmsnorm_rowscale(x, Zr, stats, self._residual_scale(Zr), self.norm_ffn.weight,
+                                        stat_eps=self.norm_out.eps, eps=self.norm_ffn.eps, out_dtype=gemm_dtype)
+
+    def _mixer_training(self, x, xn, prefix_condition, damping: float, gemm_dtype):
+        """Mixer of the fused path under autograd: every kernel has its backward
+        (gate logits, coupled scan, RMSNorm, residual update)."""
         with torch.autograd.profiler.record_function("mogt.value_projection"):
             v_raw = F.linear(xn, _gemm_weight(self, "phi_val", (self.phi_val.weight,), lambda: self.phi_val.weight))
             z = self._gate_logits(xn, prefix_condition)
-        damping = float(getattr(self, "connection_damping", 0.999))
-        if not torch.is_grad_enabled():
-            # inference: norm_out folded around the read-out GEMM.  The scan
-            # writes h in the GEMM's dtype plus per-row sums of squares; the
-            # GEMM runs against theta_read * norm_out.weight; the next RMSNorm
-            # applies each row's factor rsqrt(mean(h^2) + eps) as it reads Z.
-            with torch.autograd.profiler.record_function("mogt.affine_scan"):
-                h, stats = ops.coupled_rank_scan_stats(z, v_raw, damping=damping, out_dtype=gemm_dtype)
-            with torch.autograd.profiler.record_function("mogt.readout"):
-                Zr = F.linear(h, _gemm_weight(self, "theta_read_folded", (self.theta_read.weight, self.norm_out.weight),
-                                              lambda: self.theta_read.weight * self.norm_out.weight))
-            with torch.autograd.profiler.record_function("mogt.ffn"):
-                x, xn2 = ops.add_rmsnorm_rowscale(x, Zr, stats, self._residual_scale(Zr), self.norm_ffn.weight,
-                                                  stat_eps=self.norm_out.eps, eps=self.norm_ffn.eps,
-                                                  out_dtype=gemm_dtype)
-                f = self.ffn(xn2)
-            return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
         with torch.autograd.profiler.record_function("mogt.affine_scan"):
             h = ops.coupled_rank_scan(z, v_raw, damping=damping, out_dtype=torch.float32)
         with torch.autograd.profiler.record_function("mogt.readout"):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
             Z = F.linear(hn, _gemm_weight(self, "theta_read", (self.theta_read.weight,),
                                           lambda: self.theta_read.weight))
+        return ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight, self.norm_ffn.eps,
+                               out_dtype=gemm_dtype)
+
+    def forward_fused(self, x: torch.Tensor, prefix_condition, pending):
+        """Fused forward.  ``pending = (z, scale)`` is the previous block's last
+        residual term (added here inside the first RMSNorm).  Returns
+        ``(x_after_mixer, (ffn_out, ffn_scale))``: the caller adds the FFN term
+        (or hands it to the next block)."""
+        gemm_dtype = _autocast_dtype() or x.dtype
+        eps = self.norm_mogt.eps
+        if pending is None:
+            xn = ops.rmsnorm(x, self.norm_mogt.weight, eps, out_dtype=gemm_dtype)
+        else:
+            x, xn = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_mogt.weight, eps, out_dtype=gemm_dtype)
+        damping = float(getattr(self, "connection_damping", 0.999))
+        mixer = self._mixer_training if torch.is_grad_enabled() else self._mixer_inference
+        x, xn2 = mixer(x, xn, prefix_condition, damping, gemm_dtype)
         with torch.autograd.profiler.record_function("mogt.ffn"):
-            x, xn2 = ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight,
-                                     self.norm_ffn.eps, out_dtype=gemm_dtype)
             f = self.ffn(xn2)
         return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
 

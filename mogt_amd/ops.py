@@ -410,6 +410,56 @@ def coupled_rank_scan_stats(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, d
     return torch.ops.mogt.coupled_rank_scan_stats(gate_logits, v_raw, r, float(damping), out_dtype)
 
 
+@torch.library.custom_op("mogt::coupled_rank_scan_proj", mutates_args=())
+def _coupled_rank_scan_proj_op(proj: torch.Tensor, features: int, gate_prev: bool, gate_const: torch.Tensor | None,
+                               rank: int, damping: float) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    proj = proj.contiguous()
+    B, L, ld = proj.shape
+    D = int(features)
+    C = D // rank
+    h = torch.empty((B, L, D), dtype=proj.dtype, device=proj.device)
+    stats = torch.empty((B, L, -(-D // STAT_GROUP)), dtype=torch.float32, device=proj.device)
+    code = dtype_code(proj.dtype, "coupled_rank_scan_proj")
+    gc = None
+    if gate_const is not None:
+        gc = gate_const.to(torch.float32).expand(B, rank).contiguous()
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device)
+    rc = lib.mogt_coupled_rank_scan_proj_fwd(proj.data_ptr(), ld, D, int(bool(gate_prev)),
+                                             gc.data_ptr() if gc is not None else None, h.data_ptr(),
+                                             stats.data_ptr(), B, L, rank, C, float(damping), code, ws.data_ptr(),
+                                             ws.numel(), _stream_handle(proj.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_proj_fwd")
+    _checked(ws, "mogt_coupled_rank_scan_proj_fwd")
+    return h, stats
+
+
+@_coupled_rank_scan_proj_op.register_fake
+def _(proj, features, gate_prev, gate_const, rank, damping):
+    B, L, _ = proj.shape
+    return (proj.new_empty((B, L, features)),
+            proj.new_empty((B, L, -(-features // STAT_GROUP)), dtype=torch.float32))
+
+
+def coupled_rank_scan_proj(proj: torch.Tensor, features: int, *, rank: int, gate_prev: bool,
+                           gate_const: torch.Tensor | None = None,
+                           damping: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
+    """The coupled scan fed by one projection ``proj [B, L, features + rank *
+    (1 + gate_prev)]``: ``v = proj[..., :features]`` and the value gate's logit
+    ``z_t = proj_t[features + i] + proj_{t-1}[features + rank + i] (if
+    gate_prev, t > 0) + gate_const[b, i]``.  Returns ``h`` in proj's dtype and
+    the row statistics of ``coupled_rank_scan_stats``.  No autograd."""
+    require_cuda("coupled_rank_scan_proj", proj)
+    if proj.ndim != 3 or features % rank != 0 or proj.shape[-1] < features + rank * (1 + int(gate_prev)):
+        raise ValueError("proj must be [B, L, features + rank * (1 + gate_prev)]")
+    if gate_const is not None:
+        require_cuda("coupled_rank_scan_proj", gate_const)
+        if gate_const.shape[-1] != rank or gate_const.ndim > 2:
+            raise ValueError("gate_const must be [rank] or [B, rank]")
+    return torch.ops.mogt.coupled_rank_scan_proj(proj, int(features), bool(gate_prev), gate_const, int(rank),
+                                                 float(damping))
+
+
 def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,
                       out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Fused gate + scan of the coupled write-forget MOGT mixer.

@@ -236,6 +236,48 @@ def test_coupled_rank_scan_row_statistics(gpu, B, L, r, c, vdt, odt):
     assert rel_err(to_np(stats), ref_stats) <= 1e-5
 
 
+@pytest.mark.parametrize("B,L,r,c,dt,prev,const", [(2, 1000, 16, 48, "bf16", True, "batch"),
+                                                   (1, 32768, 16, 48, "bf16", True, "batch"),
+                                                   (1, 300, 4, 24, "fp32", False, None),
+                                                   (2, 77, 3, 20, "fp32", False, "rank"),
+                                                   (1, 129, 4, 8, "bf16", True, None)])
+def test_coupled_rank_scan_projection_fed(gpu, B, L, r, c, dt, prev, const):
+    """The scan fed by one projection row [v | gate pre-logits (current) |
+    (previous)]: against the statistics scan on logits assembled by torch from
+    the same projection, and against the oracle.  Row strides not a multiple of
+    the vector fall back to narrower tiles."""
+    announce(f"coupled scan projection-fed B={B} L={L} r={r} c={c} {dt} prev={prev} const={const}")
+    from mogt_amd import ops
+
+    D = r * c
+    ld = D + r * (2 if prev else 1)
+    g = torch.Generator().manual_seed(L + r)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    proj = torch.randn(B, L, ld, generator=g)
+    proj[..., D:] = proj[..., D:] * 1.5 - 1.0
+    proj = proj.to(tdt).to(gpu)
+    gc = None
+    if const == "batch":
+        gc = (torch.randn(B, r, generator=g) - 1.0).to(gpu)
+    elif const == "rank":
+        gc = (torch.randn(r, generator=g) - 1.0).to(gpu)
+    h, stats = ops.coupled_rank_scan_proj(proj, D, rank=r, gate_prev=prev, gate_const=gc, damping=0.995)
+    z = proj[..., D:D + r].float()
+    if prev:
+        z = torch.cat([z[:, :1], z[:, 1:] + proj[:, :-1, D + r:D + 2 * r].float()], dim=1)
+    if gc is not None:
+        z = z + gc.expand(B, r)[:, None, :]
+    v = proj[..., :D]
+    h2, stats2 = ops.coupled_rank_scan_stats(z.contiguous(), v.contiguous(), damping=0.995, out_dtype=tdt)
+    torch.cuda.synchronize()
+    assert h.shape == (B, L, D) and h.dtype == tdt
+    assert rel_err(to_np(h), to_np(h2)) <= (2.0 ** -8 if dt == "bf16" else 1e-6)
+    assert rel_err(to_np(stats), to_np(stats2)) <= 1e-5
+    ref = so.coupled_rank_scan(to_np(z), to_np(v), r, damping=0.995, v_is_bf16=dt == "bf16")
+    err = np.abs(to_np(h).astype(np.float64) - ref) / np.max(np.abs(ref))
+    assert float(err.max()) <= (BF16_TOL if dt == "bf16" else FP32_TOL)
+
+
 @pytest.mark.parametrize("vdt", ["fp32", "bf16"])
 @pytest.mark.parametrize("tile", TILES_COUPLED)
 def test_every_coupled_tile(gpu, tile, vdt):
