@@ -482,6 +482,22 @@ def measure_backbone(torch, layers, ffn_hidden, vocab, L, iters, warmup):
             "params": params}
 
 
+def backbone_lengths(torch, layers, ffn_hidden, vocab, lengths=(8192, 16384, 32768), iters=10, warmup=3):
+    """The reference harness's length sweep (benchmark_backbone_throughput.py:92-131):
+    per length a status ("ok" or "oom" when the forward runs out of device
+    memory), ms, tokens/s and peak memory."""
+    rows = {}
+    for L in lengths:
+        torch.cuda.empty_cache()
+        try:
+            r = measure_backbone(torch, layers, ffn_hidden, vocab, L, iters, warmup)
+            rows[str(L)] = dict(status="ok", **{k: r[k] for k in ("ms", "tokens_per_s", "peak_mem_mb")})
+        except torch.cuda.OutOfMemoryError as exc:
+            torch.cuda.empty_cache()
+            rows[str(L)] = {"status": "oom", "ms": None, "tokens_per_s": None, "error": str(exc)[:200]}
+    return rows
+
+
 def measure_backbone_train(torch, layers, ffn_hidden, vocab, L, iters, warmup, fused=True):
     """One training step of the backbone (forward + backward of a mean-square
     loss on its output, bf16 autocast, no optimizer): through the fused block
@@ -728,6 +744,12 @@ def main():
             extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
                 r, ffn_hidden=2048, vocab=4096,
                 note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
+            extras["mogt_backbone_length_sweep"] = {
+                "4layer_ffn3072_vocab32000": backbone_lengths(torch, 4, 3072, 32000),
+                "2layer_refffn_vocab4096": backbone_lengths(torch, 2, None, 4096),
+                "reference_2layer_L4_ms": {"8192": 14.07, "16384": 37.88, "32768": 77.56},
+                "note": "forward, bf16 autocast, inference mode, B = 1; status 'oom' where the forward "
+                        "runs out of device memory (benchmark_backbone_throughput.py:92-131)"}
             # 10 warm-up steps: the first training steps of a process run slow for
             # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
             # with 10-20), independent of which path runs first
@@ -744,6 +766,14 @@ def main():
         log("cpu baseline (reference sequential torch scan restated, host cores)")
         cpu = cpu_baseline()
         log(f"cpu baseline: {cpu['ms']:.0f} ms ({cpu['value']:.3f} GB/s)")
+
+    # every single-pass scan above ran on a cached workspace: a look-back wait
+    # that gave up would have poisoned its outputs with NaN; refuse the numbers
+    give_ups = ops.workspace_faults()
+    if give_ups:
+        print(f"bench.py: {give_ups} look-back wait(s) gave up; the measured scans are invalid",
+              file=sys.stderr)
+        sys.exit(3)
 
     traffic = read_traffic("diag_scan_d768_l32768_fp32_traffic.txt")
     achieved = head["gbs"]
@@ -778,6 +808,7 @@ def main():
         "cpu_baseline": ({k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")}
                          if cpu else None),
         "scan_core_us": round(head["ms"] * 1e3, 3),
+        "lookback_give_ups": give_ups,
         "reference_triton_core_ms_L4": REF_TRITON_CORE_MS_L4,
         "extras": extras,
     }
