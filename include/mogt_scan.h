@@ -144,14 +144,28 @@ int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, void* h, floa
  * (gate_prev && t > 0 ? proj[t-1][gate_col + R + i] : 0) + gate_const[b][i]
  * (gate_const [B, R] fp32: bias + prefix term, nullable) -- phi_value_gate
  * over [x_t, x_{t-1}, prefix] (model_mogt.py:104-122, 166-182) without the
- * concatenated input.  proj and h share `dtype`; row_stats as in
- * mogt_coupled_rank_scan_stats_fwd.  Workspace:
+ * concatenated input.  With row_stats (as in mogt_coupled_rank_scan_stats_fwd)
+ * h is written in proj's `dtype`; without (nullable), out_dtype must be fp32
+ * (the training path, which normalises h separately).  z_out (nullable, fp32
+ * [B, L, R]) receives the assembled logits.  Workspace:
  * mogt_coupled_rank_scan_workspace_bytes.                                 */
 int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj, int64_t gate_col, int gate_prev,
-                                    const float* gate_const, void* h, float* row_stats,
+                                    const float* gate_const, void* h, float* row_stats, float* z_out,
                                     int64_t batch, int64_t length, int64_t rank, int64_t channels,
-                                    float damping, int dtype,
+                                    float damping, int dtype, int out_dtype,
                                     void* workspace, size_t workspace_bytes, void* stream);
+/* Gradient epilogue of the projection-fed scan (training): like
+ * mogt_coupled_rank_scan_grad with v read from proj (gate_col = R*C, ld_proj =
+ * R*C + R*(1 + gate_prev)) and z the logits the forward kept (z_out), written
+ * into dproj, the gradient of the projection: dv in columns 0 .. R*C-1, the
+ * logit gradient dz[t] in row t's current-token gate columns and in row
+ * t-1's previous-token columns (zero in row L-1's), so one GEMM maps it back
+ * to x and to [phi_val; W_cur; W_prev].  dz (fp32 [B, L, R], nullable) also
+ * receives the logit gradient (for the bias and prefix terms).             */
+int mogt_coupled_rank_scan_proj_grad(const float* G, const float* z, const void* proj, int64_t ld_proj,
+                                     int gate_prev, const float* h, void* dproj, float* dz,
+                                     int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                     float damping, int dtype, void* stream);
 /* mogt_coupled_rank_scan_fwd with an explicit tile, one of
  * mogt_diag_scan_tiles(2) whose vector divides `channels` (v and h aligned to
  * it, up to 16 bytes); for sweeps and tile coverage tests.  Workspace:

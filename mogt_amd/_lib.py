@@ -62,8 +62,13 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "mogt_coupled_rank_scan_proj_fwd": (
         _c_int,
-        [_c_void_p, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64,
-         _c_float, _c_int, _c_void_p, _c_size, _c_void_p],
+        [_c_void_p, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_float, _c_int, _c_int, _c_void_p, _c_size, _c_void_p],
+    ),
+    "mogt_coupled_rank_scan_proj_grad": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
+         _c_i64, _c_float, _c_int, _c_void_p],
     ),
     "mogt_coupled_rank_scan_fwd_cfg": (
         _c_int,

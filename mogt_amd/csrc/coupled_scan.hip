@@ -36,13 +36,13 @@ int coupled_stat_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t 
                      t.vec, t.lanes, t.steps, t.waves);
 }
 
-// Projection-fed gates (GPROJ) with statistics: v, the gate pre-logits and h
-// share one dtype T.
-template <typename T>
+// Projection-fed gates (GPROJ): v and the gate pre-logits share one dtype T;
+// h in TO; with or without row statistics.
+template <typename T, typename TO, bool STATS>
 int coupled_proj_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
 #define MOGT_CASE(V_, F_, S_, W_)                                          \
     if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) \
-        return diag_launch<MODE_COUPLED, T, T, T, V_, F_, S_, W_, false, true, true>(prm, st);
+        return diag_launch<MODE_COUPLED, T, T, TO, V_, F_, S_, W_, false, STATS, true>(prm, st);
     MOGT_COUPLED_STAT_TILES(MOGT_CASE)
 #undef MOGT_CASE
     return set_error(MOGT_E_INVALID, "coupled scan statistics: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
@@ -83,6 +83,7 @@ struct CoupledProj {
     int64_t ldz;
     int gate_prev;
     const float* gconst;
+    float* zout;
 };
 
 int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int64_t R, int64_t C,
@@ -111,11 +112,18 @@ int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int
         prm.ldz = proj->ldz;
         prm.gate_prev = proj->gate_prev;
         prm.gconst = proj->gconst;
-        if (!row_stats || zb != vb || vb != ob)
-            return set_error(MOGT_E_INVALID, "projection-fed coupled scan: one dtype and row statistics");
+        prm.zout = proj->zout;
+        if (zb != vb) return set_error(MOGT_E_INVALID, "projection-fed coupled scan: v and gates share a dtype");
         if (t.vec * t.lanes != 64)
-            return set_error(MOGT_E_INVALID, "coupled scan statistics: tile must be 64 features wide");
-        return vb ? coupled_proj_dispatch<bf16_t>(prm, t, st) : coupled_proj_dispatch<float>(prm, t, st);
+            return set_error(MOGT_E_INVALID, "projection-fed coupled scan: tile must be 64 features wide");
+        if (row_stats) {
+            if (vb != ob) return set_error(MOGT_E_INVALID, "projection-fed scan with statistics: h in proj's dtype");
+            return vb ? coupled_proj_dispatch<bf16_t, bf16_t, true>(prm, t, st)
+                      : coupled_proj_dispatch<float, float, true>(prm, t, st);
+        }
+        if (ob) return set_error(MOGT_E_INVALID, "projection-fed scan without statistics: h in fp32");
+        return vb ? coupled_proj_dispatch<bf16_t, float, false>(prm, t, st)
+                  : coupled_proj_dispatch<float, float, false>(prm, t, st);
     }
     if (row_stats) {
         if (zb) return set_error(MOGT_E_INVALID, "coupled scan statistics: gate logits must be fp32");
@@ -188,29 +196,34 @@ extern "C" int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, vo
 }
 
 extern "C" int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj, int64_t gate_col, int gate_prev,
-                                               const float* gate_const, void* h, float* row_stats, int64_t batch,
-                                               int64_t length, int64_t rank, int64_t channels, float damping,
-                                               int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+                                               const float* gate_const, void* h, float* row_stats, float* z_out,
+                                               int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                               float damping, int dtype, int out_dtype, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
     clear_error();
     if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
     if (rank <= 0 || channels <= 0 || rank > 0x7fffffff || channels > 0x7fffffff)
         return set_error(MOGT_E_INVALID, "rank and channels must be positive");
-    if (!dtype_ok(dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (row_stats ? out_dtype != dtype : out_dtype != MOGT_F32)
+        return set_error(MOGT_E_INVALID, "projection-fed scan: h in proj's dtype with row statistics, "
+                                         "else fp32");
     const int64_t D = rank * channels;
     if (gate_prev != 0 && gate_prev != 1) return set_error(MOGT_E_INVALID, "gate_prev must be 0 or 1");
     if (gate_col < D || gate_col + rank * (1 + gate_prev) > ld_proj || ld_proj > 0x7fffffff)
         return set_error(MOGT_E_INVALID, "projection row of %lld columns cannot hold v (%lld) and the gate "
                          "pre-logits at column %lld", (long long)ld_proj, (long long)D, (long long)gate_col);
     if (batch == 0 || length == 0) return MOGT_OK;
-    if (!proj || !h || !row_stats) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    if (!proj || !h) return set_error(MOGT_E_INVALID, "null tensor pointer");
     // the vector must divide the projection's row stride as well as the channels
-    const int al = coupled_alignment(proj, h, dtype, dtype);
+    const int al = coupled_alignment(proj, h, dtype, out_dtype);
     const int vec_ok = ld_proj % 4 == 0 ? al : (ld_proj % 2 == 0 ? (al < 2 ? al : 2) : 1);
     const DiagTile t = coupled_tile(batch, length, rank, channels, vec_ok);
     const size_t esz = dtype == MOGT_BF16 ? 2 : 4;
-    const CoupledProj pj{ld_proj, gate_prev, gate_const};
+    const CoupledProj pj{ld_proj, gate_prev, gate_const, z_out};
     return coupled_run(static_cast<const char*>(proj) + gate_col * esz, proj, h, batch, length, rank, channels,
-                       damping, dtype, dtype, dtype, t, workspace, workspace_bytes, stream, row_stats, ld_proj, &pj);
+                       damping, dtype, dtype, out_dtype, t, workspace, workspace_bytes, stream, row_stats, ld_proj,
+                       &pj);
 }
 
 // The same with an explicit tile (sweeps and tests): the tile must be one of
@@ -262,17 +275,25 @@ constexpr int CG_THREADS = 256;
 constexpr int CG_ROWS = 8;
 constexpr int CG_MAX_VEC = 1024;   // D <= 4096
 
-template <typename TV>
+// ldv: row stride of v and dv.  PROJ: v and dv live in projection rows of
+// ldv elements whose gate columns (from D: R current, then R previous when
+// gate_prev) receive the logit gradient -- dz[t] in row t's current columns
+// and in row t - 1's previous columns (the previous-token term of step t is a
+// term of row t - 1), zero in row L - 1's previous columns; dz (fp32
+// [B, L, R]) may then be null.
+template <typename TV, bool PROJ = false>
 __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* __restrict__ G,
                                                                   const float* __restrict__ z,
                                                                   const TV* __restrict__ v,
                                                                   const float* __restrict__ h,
                                                                   TV* __restrict__ dv, float* __restrict__ dz,
                                                                   int64_t nrows, int64_t L, int R, int C,
-                                                                  float damping) {
+                                                                  float damping, int64_t ldv = 0,
+                                                                  int gate_prev = 0) {
     __shared__ float s_v[CG_MAX_VEC], s_h[CG_MAX_VEC];
     const int tid = threadIdx.x;
     const int D = R * C, nvec = D / 4, vpr = C / 4;
+    const int64_t ld = PROJ ? ldv : D;
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * CG_ROWS;
     const int64_t r1 = r0 + CG_ROWS < nrows ? r0 + CG_ROWS : nrows;
     for (int64_t row = r0; row < r1; ++row) {
@@ -283,7 +304,7 @@ __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* _
             const float g_io = IO<TV>::ld(IO<TV>::st(sigmoidf_(z[row * R + i])));
             float gv[4], vv[4], hv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o[4];
             load_vec<float, 4>(G + base + 4 * f, gv);
-            load_vec<TV, 4>(v + base + 4 * f, vv);
+            load_vec<TV, 4>(v + row * ld + 4 * f, vv);
             if (has_prev) load_vec<float, 4>(h + base - D + 4 * f, hv);
             float sv = 0.0f, sh = 0.0f;
 #pragma unroll
@@ -292,7 +313,7 @@ __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* _
                 sh = fmaf(gv[e], hv[e], sh);
                 o[e] = gv[e] * g_io;
             }
-            store_vec<TV, 4>(dv + base + 4 * f, o);
+            store_vec<TV, 4>(dv + row * ld + 4 * f, o);
             s_v[f] = sv;
             s_h[f] = sh;
         }
@@ -304,7 +325,15 @@ __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* _
                 sh += s_h[k];
             }
             const float gg = sigmoidf_(z[row * R + i]);
-            dz[row * R + i] = (sv - damping * sh) * gg * (1.0f - gg);
+            const float g = (sv - damping * sh) * gg * (1.0f - gg);
+            if (dz) dz[row * R + i] = g;
+            if constexpr (PROJ) {
+                dv[row * ld + D + i] = IO<TV>::st(g);
+                if (gate_prev) {
+                    if (has_prev) dv[(row - 1) * ld + D + R + i] = IO<TV>::st(g);
+                    if (row % L == L - 1) dv[row * ld + D + R + i] = IO<TV>::st(0.0f);
+                }
+            }
         }
         __syncthreads();
     }
@@ -336,5 +365,37 @@ extern "C" int mogt_coupled_rank_scan_grad(const void* G, const float* z, const 
         hipLaunchKernelGGL((coupled_grad_kernel<bf16_t>), dim3(static_cast<unsigned>(blocks)), dim3(CG_THREADS), 0,
                            st, static_cast<const float*>(G), z, static_cast<const bf16_t*>(v), h,
                            static_cast<bf16_t*>(dv), dz, nrows, length, R, C, damping);
+    return check_launch("coupled_grad_kernel");
+}
+
+extern "C" int mogt_coupled_rank_scan_proj_grad(const float* G, const float* z, const void* proj, int64_t ld_proj,
+                                                int gate_prev, const float* h, void* dproj, float* dz,
+                                                int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                                float damping, int dtype, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0) return set_error(MOGT_E_INVALID, "negative size");
+    if (rank <= 0 || channels <= 0 || channels % 4 != 0 || rank * channels > 4 * CG_MAX_VEC)
+        return set_error(MOGT_E_INVALID,
+                         "coupled grad: channels a positive multiple of 4 and rank * channels <= 4096");
+    if (!dtype_ok(dtype)) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (gate_prev != 0 && gate_prev != 1) return set_error(MOGT_E_INVALID, "gate_prev must be 0 or 1");
+    const int64_t D = rank * channels;
+    if (ld_proj != D + rank * (1 + gate_prev) || ld_proj % 4 != 0)
+        return set_error(MOGT_E_INVALID, "projection rows must be D + R * (1 + gate_prev) elements, a multiple of 4");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!G || !z || !proj || !h || !dproj) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    const int64_t nrows = batch * length;
+    const int64_t blocks = (nrows + CG_ROWS - 1) / CG_ROWS;
+    if (blocks > 0x7fffffffLL) return set_error(MOGT_E_INVALID, "coupled grad: problem too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int R = static_cast<int>(rank), C = static_cast<int>(channels);
+    if (dtype == MOGT_F32)
+        hipLaunchKernelGGL((coupled_grad_kernel<float, true>), dim3(static_cast<unsigned>(blocks)), dim3(CG_THREADS),
+                           0, st, G, z, static_cast<const float*>(proj), h, static_cast<float*>(dproj), dz, nrows,
+                           length, R, C, damping, ld_proj, gate_prev);
+    else
+        hipLaunchKernelGGL((coupled_grad_kernel<bf16_t, true>), dim3(static_cast<unsigned>(blocks)),
+                           dim3(CG_THREADS), 0, st, G, z, static_cast<const bf16_t*>(proj), h,
+                           static_cast<bf16_t*>(dproj), dz, nrows, length, R, C, damping, ld_proj, gate_prev);
     return check_launch("coupled_grad_kernel");
 }

@@ -75,6 +75,7 @@ struct DiagParams {
     int64_t ldz;        // GATED: row stride of the gate logits (R), or of the projection (GPROJ)
     int gate_prev;      // GPROJ: add the previous step's pre-logit (column R + i) when 1
     const float* gconst;   // GPROJ: [B, R] per-sequence logit term (bias + prefix), or null
+    float* zout;           // GPROJ: [B, L, R] fp32 gate logits as assembled (for the backward), or null
 };
 
 constexpr uint32_t ST_NONE = 0u;
@@ -264,6 +265,9 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                 const float zp = std::is_same<TZ, bf16_t>::value ? __uint_as_float(pb << 16) : __uint_as_float(pb);
                 const bool has_prev = p.gate_prev && (tw + min(q * S + s, static_cast<int>(p.L - 1 - tw)) > 0);
                 z = (z + (has_prev ? zp : 0.0f)) + zc;
+                // the lane holding a gate's first channel keeps the logit
+                if (p.zout && s < nv && (fbase + flane) % p.C == 0)
+                    p.zout[(row0 + t0 + s) * p.R + gi] = z;
             }
             const bool ok = s < nv;
             const float gg = sigmoidf_(z);

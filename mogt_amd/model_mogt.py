@@ -439,13 +439,26 @@ class MOGTBlock(_WeightCacheOwner):
                                         stat_eps=self.norm_out.eps, eps=self.norm_ffn.eps, out_dtype=gemm_dtype)
 
     def _mixer_training(self, x, xn, prefix_condition, damping: float, gemm_dtype):
-        """Mixer of the fused path under autograd: every kernel has its backward
-        (gate logits, coupled scan, RMSNorm, residual update)."""
-        with torch.autograd.profiler.record_function("mogt.value_projection"):
-            v_raw = F.linear(xn, _gemm_weight(self, "phi_val", (self.phi_val.weight,), lambda: self.phi_val.weight))
-            z = self._gate_logits(xn, prefix_condition)
-        with torch.autograd.profiler.record_function("mogt.affine_scan"):
-            h = ops.coupled_rank_scan(z, v_raw, damping=damping, out_dtype=torch.float32)
+        """Mixer of the fused path under autograd: every kernel has its backward.
+        Where the row layout allows, the scan is fed by the one projection GEMM
+        of the inference path, so the backward's epilogue writes the
+        projection's gradient directly (one GEMM back to x and to the stacked
+        weights); otherwise by separately computed gate logits."""
+        parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
+        if ops.coupled_proj_scan_supported(self.d_model, self.r, "prev" in parts):
+            with torch.autograd.profiler.record_function("mogt.affine_scan"):
+                proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition)
+                if gconst is not None:
+                    gconst = gconst.expand(xn.size(0), self.r).contiguous()
+                h = ops.coupled_proj_scan(proj, self.d_model, rank=self.r, gate_prev=gate_prev, gate_const=gconst,
+                                          damping=damping)
+        else:
+            with torch.autograd.profiler.record_function("mogt.value_projection"):
+                v_raw = F.linear(xn, _gemm_weight(self, "phi_val", (self.phi_val.weight,),
+                                                  lambda: self.phi_val.weight))
+                z = self._gate_logits(xn, prefix_condition)
+            with torch.autograd.profiler.record_function("mogt.affine_scan"):
+                h = ops.coupled_rank_scan(z, v_raw, damping=damping, out_dtype=torch.float32)
         with torch.autograd.profiler.record_function("mogt.readout"):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
             Z = F.linear(hn, _gemm_weight(self, "theta_read", (self.theta_read.weight,),

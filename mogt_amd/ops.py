@@ -427,8 +427,8 @@ def _coupled_rank_scan_proj_op(proj: torch.Tensor, features: int, gate_prev: boo
     ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device)
     rc = lib.mogt_coupled_rank_scan_proj_fwd(proj.data_ptr(), ld, D, int(bool(gate_prev)),
                                              gc.data_ptr() if gc is not None else None, h.data_ptr(),
-                                             stats.data_ptr(), B, L, rank, C, float(damping), code, ws.data_ptr(),
-                                             ws.numel(), _stream_handle(proj.device))
+                                             stats.data_ptr(), None, B, L, rank, C, float(damping), code, code,
+                                             ws.data_ptr(), ws.numel(), _stream_handle(proj.device))
     _lib.check(rc, "mogt_coupled_rank_scan_proj_fwd")
     _checked(ws, "mogt_coupled_rank_scan_proj_fwd")
     return h, stats
@@ -458,6 +458,107 @@ def coupled_rank_scan_proj(proj: torch.Tensor, features: int, *, rank: int, gate
             raise ValueError("gate_const must be [rank] or [B, rank]")
     return torch.ops.mogt.coupled_rank_scan_proj(proj, int(features), bool(gate_prev), gate_const, int(rank),
                                                  float(damping))
+
+
+@torch.library.custom_op("mogt::coupled_proj_scan", mutates_args=())
+def _coupled_proj_scan_op(proj: torch.Tensor, gate_const: torch.Tensor | None, features: int, rank: int,
+                          gate_prev: bool, damping: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Training form of the projection-fed scan: fp32 h and the assembled
+    fp32 logits z (kept for the backward)."""
+    lib = _lib.load()
+    proj = proj.contiguous()
+    B, L, ld = proj.shape
+    D = int(features)
+    C = D // rank
+    h = torch.empty((B, L, D), dtype=torch.float32, device=proj.device)
+    z = torch.empty((B, L, rank), dtype=torch.float32, device=proj.device)
+    code = dtype_code(proj.dtype, "coupled_proj_scan")
+    gc = gate_const.to(torch.float32).contiguous() if gate_const is not None else None
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device)
+    rc = lib.mogt_coupled_rank_scan_proj_fwd(proj.data_ptr(), ld, D, int(bool(gate_prev)),
+                                             gc.data_ptr() if gc is not None else None, h.data_ptr(), None,
+                                             z.data_ptr(), B, L, rank, C, float(damping), code, _lib.MOGT_F32,
+                                             ws.data_ptr(), ws.numel(), _stream_handle(proj.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_proj_fwd")
+    _checked(ws, "mogt_coupled_rank_scan_proj_fwd")
+    return h, z
+
+
+@_coupled_proj_scan_op.register_fake
+def _(proj, gate_const, features, rank, gate_prev, damping):
+    B, L, _ = proj.shape
+    return (proj.new_empty((B, L, features), dtype=torch.float32),
+            proj.new_empty((B, L, rank), dtype=torch.float32))
+
+
+@torch.library.custom_op("mogt::coupled_proj_grad", mutates_args=())
+def _coupled_proj_grad_op(G: torch.Tensor, z: torch.Tensor, proj: torch.Tensor, h: torch.Tensor, features: int,
+                          rank: int, gate_prev: bool, damping: float) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    G, z, proj, h = G.contiguous(), z.contiguous(), proj.contiguous(), h.contiguous()
+    B, L, ld = proj.shape
+    D = int(features)
+    dproj = torch.empty_like(proj)
+    dz = torch.empty((B, L, rank), dtype=torch.float32, device=proj.device)
+    rc = lib.mogt_coupled_rank_scan_proj_grad(G.data_ptr(), z.data_ptr(), proj.data_ptr(), ld, int(bool(gate_prev)),
+                                              h.data_ptr(), dproj.data_ptr(), dz.data_ptr(), B, L, rank, D // rank,
+                                              float(damping), dtype_code(proj.dtype, "coupled_proj_grad"),
+                                              _stream_handle(proj.device))
+    _lib.check(rc, "mogt_coupled_rank_scan_proj_grad")
+    return dproj, dz
+
+
+@_coupled_proj_grad_op.register_fake
+def _(G, z, proj, h, features, rank, gate_prev, damping):
+    B, L, _ = proj.shape
+    return torch.empty_like(proj), proj.new_empty((B, L, rank), dtype=torch.float32)
+
+
+def _coupled_proj_setup(ctx, inputs, output):
+    proj, gate_const, features, rank, gate_prev, damping = inputs
+    h, z = output
+    ctx.save_for_backward(proj, z, h)
+    ctx.args = (int(features), int(rank), bool(gate_prev), float(damping))
+
+
+def _coupled_proj_backward(ctx, grad_h, grad_z):
+    """G = dH + a_{t+1} G_{t+1} (reverse scan, decay from the saved logits),
+    then one epilogue writes the projection's gradient (dv and the logit
+    gradient in the current / previous-token gate columns); the per-sequence
+    logit term gets the logit gradient summed over time."""
+    proj, z, h = ctx.saved_tensors
+    features, rank, gate_prev, damping = ctx.args
+    G = torch.ops.mogt.coupled_scan_rev(z, grad_h, rank, damping)
+    dproj, dz = torch.ops.mogt.coupled_proj_grad(G, z, proj, h, features, rank, gate_prev, damping)
+    dconst = dz.sum(1) if ctx.needs_input_grad[1] else None
+    return dproj, dconst, None, None, None, None
+
+
+torch.library.register_autograd("mogt::coupled_proj_scan", _coupled_proj_backward, setup_context=_coupled_proj_setup)
+
+
+def coupled_proj_scan(proj: torch.Tensor, features: int, *, rank: int, gate_prev: bool,
+                      gate_const: torch.Tensor | None = None, damping: float = 1.0) -> torch.Tensor:
+    """Differentiable projection-fed coupled scan: ``v = proj[..., :features]``,
+    logits ``z_t = proj_t[features + i] + proj_{t-1}[features + rank + i]`` (if
+    ``gate_prev``, t > 0) ``+ gate_const[b, i]`` (``[B, rank]`` fp32 or None);
+    returns the fp32 state ``h [B, L, features]``.  Needs ``features / rank``
+    and the projection's row length to be multiples of 4."""
+    require_cuda("coupled_proj_scan", proj)
+    B, L, ld = proj.shape
+    if features % rank != 0 or ld != features + rank * (1 + int(gate_prev)):
+        raise ValueError("proj must be [B, L, features + rank * (1 + gate_prev)]")
+    if gate_const is not None and tuple(gate_const.shape) != (B, rank):
+        raise ValueError("gate_const must be [B, rank]")
+    h, _ = torch.ops.mogt.coupled_proj_scan(proj, gate_const, int(features), int(rank), bool(gate_prev),
+                                            float(damping))
+    return h
+
+
+def coupled_proj_scan_supported(features: int, rank: int, gate_prev: bool) -> bool:
+    c = features // rank
+    return (features % rank == 0 and c % 4 == 0 and features <= 4096
+            and (features + rank * (1 + int(gate_prev))) % 4 == 0)
 
 
 def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping: float = 1.0,

@@ -171,3 +171,60 @@ def test_coupled_reverse_scan(gpu, B, L, r, c, zdt):
     ref = _coupled_rev64(to_np(zt).astype(np.float64), dh, r, 0.995)
     assert G.dtype == torch.float32 and G.shape == (B, L, r * c)
     assert rel_err(to_np(G), ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("B,L,r,c,dt,prev,with_const", [(2, 200, 4, 8, "fp32", True, True),
+                                                        (1, 300, 16, 48, "fp32", True, True),
+                                                        (2, 150, 4, 12, "fp32", False, False),
+                                                        (1, 256, 16, 48, "bf16", True, True)])
+def test_projection_fed_scan_gradients(gpu, B, L, r, c, dt, prev, with_const):
+    """The differentiable projection-fed coupled scan (the training mixer):
+    gradients of the projection -- v columns, current-token gate columns and
+    the previous-token gate columns (shifted by one step) -- and of the
+    per-sequence logit term, against float64 autograd of z = P[t][D+i] +
+    P[t-1][D+r+i] + const, g = sigmoid(z), h_t = d (1-g) h_{t-1} + v g."""
+    announce(f"projection-fed scan gradients B={B} L={L} r={r} c={c} {dt} prev={prev}")
+    from mogt_amd import ops
+
+    D = r * c
+    ld = D + r * (2 if prev else 1)
+    g = torch.Generator().manual_seed(L + c)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    proj = torch.randn(B, L, ld, generator=g)
+    proj[..., D:] = proj[..., D:] - 0.5
+    proj = proj.to(tdt)
+    gc = (torch.randn(B, r, generator=g) - 1.0) if with_const else None
+    w = torch.randn(B, L, D, generator=g)
+    pt = proj.to(gpu).requires_grad_()
+    gct = gc.to(gpu).requires_grad_() if gc is not None else None
+    h = ops.coupled_proj_scan(pt, D, rank=r, gate_prev=prev, gate_const=gct, damping=0.99)
+    (h * w.to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    p64 = proj.double().requires_grad_()
+    g64 = gc.double().requires_grad_() if gc is not None else None
+    z = p64[..., D:D + r]
+    if prev:
+        z = torch.cat([z[:, :1], z[:, 1:] + p64[:, :-1, D + r:D + 2 * r]], dim=1)
+    if g64 is not None:
+        z = z + g64[:, None, :]
+    gate = torch.sigmoid(z)
+    # the gate as multiplied into bf16 v (the cast passes gradients through)
+    gio = gate.to(tdt).double() if dt == "bf16" else gate
+    a = (0.99 * (1.0 - gate)).repeat_interleave(c, dim=-1)
+    bv = p64[..., :D] * gio.repeat_interleave(c, dim=-1)
+    hh = torch.zeros(B, D, dtype=torch.float64)
+    outs = []
+    for t in range(L):
+        hh = a[:, t] * hh + bv[:, t]
+        outs.append(hh)
+    ref = (torch.stack(outs, 1) * w.double()).sum()
+    ref.backward()
+    tol = FP32_TOL if dt == "fp32" else BF16_TOL
+    assert rel_err(to_np(h), torch.stack(outs, 1).detach().numpy()) <= tol
+    gp = to_np(pt.grad)
+    assert rel_err(gp[..., :D], p64.grad[..., :D].numpy()) <= tol
+    assert rel_err(gp[..., D:], p64.grad[..., D:].numpy()) <= tol
+    if prev:
+        assert np.all(gp[:, -1, D + r:] == 0)
+    if gc is not None:
+        assert rel_err(to_np(gct.grad), g64.grad.numpy()) <= tol
