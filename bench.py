@@ -736,29 +736,46 @@ def main():
                         "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
                         "torch ops on the same GPU"}
         if full or args.only == "backbone":
-            r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
+            from mogt_amd import gemm_tuning
+
+            # the libraries' default GEMM choice first, then the tuned table
+            # (mogt_amd/tuning/gemm_gfx950.csv); both are reported
+            d4 = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
+            d2 = measure_backbone(torch, 2, None, 4096, 32768, 10, 3)
+            dt = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
+            tuned = gemm_tuning.use_tuned_gemms()
+            r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3) if tuned else d4
             extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
-                r, ffn_hidden=3072, vocab=32000,
-                note="BASELINE configs[4]: 4 layers, 4x gated MLP, bf16 autocast; target < 77.56 ms")
-            r = measure_backbone(torch, 2, None, 4096, 32768, 10, 3)
+                r, ffn_hidden=3072, vocab=32000, default_gemms_ms=d4["ms"], tuned_gemm_table=tuned,
+                mfma_frac=round(2.174e12 / (r["ms"] * 1e-3) / 2.5e15, 4),
+                note="BASELINE configs[4]: 4 layers, 4x gated MLP, bf16 autocast; target < 77.56 ms; "
+                     "ms with the tuned GEMM table, default_gemms_ms with the libraries' own choice; "
+                     "mfma_frac = 2.174 TFLOP of GEMMs / time / 2.5 PFLOP/s")
+            r = measure_backbone(torch, 2, None, 4096, 32768, 10, 3) if tuned else d2
             extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
-                r, ffn_hidden=2048, vocab=4096,
+                r, ffn_hidden=2048, vocab=4096, default_gemms_ms=d2["ms"], tuned_gemm_table=tuned,
                 note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
             extras["mogt_backbone_length_sweep"] = {
                 "4layer_ffn3072_vocab32000": backbone_lengths(torch, 4, 3072, 32000),
                 "2layer_refffn_vocab4096": backbone_lengths(torch, 2, None, 4096),
                 "reference_2layer_L4_ms": {"8192": 14.07, "16384": 37.88, "32768": 77.56},
-                "note": "forward, bf16 autocast, inference mode, B = 1; status 'oom' where the forward "
-                        "runs out of device memory (benchmark_backbone_throughput.py:92-131)"}
+                "tuned_gemm_table": tuned,
+                "note": "forward, bf16 autocast, inference mode, B = 1, tuned GEMM table when accepted; "
+                        "status 'oom' where the forward runs out of device memory "
+                        "(benchmark_backbone_throughput.py:92-131)"}
             # 10 warm-up steps: the first training steps of a process run slow for
             # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
             # with 10-20), independent of which path runs first
-            rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
+            rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True) if tuned else dt
             rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=False)
             extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(
-                rf, generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
+                rf, default_gemms_ms=dt["ms"], tuned_gemm_table=tuned,
+                generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
                 note="forward + backward (mean-square loss on the backbone output, no optimizer), "
-                     "bf16 autocast; fused block path vs the generic op-by-op path on the same weights")
+                     "bf16 autocast; fused block path (default_gemms_ms: the libraries' own GEMM choice) "
+                     "vs the generic op-by-op path on the same weights")
+            if tuned:
+                gemm_tuning.default_gemms()
         log(f"extras: {json.dumps(extras)}")
 
     cpu = None

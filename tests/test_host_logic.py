@@ -53,3 +53,17 @@ def test_gemm_weight_cache_invalidation_paths():
         assert w3 is not w2
         blk.load_state_dict(blk.state_dict())
         assert _gemm_weight(ffn, "w12", (ffn.w1.weight, ffn.w2.weight), build) is not w3
+
+
+def test_gemm_table_is_well_formed():
+    """The tuned GEMM table: TunableOp's validator header for gfx950 and one
+    solution per backbone GEMM shape (bf16, the d_model 768 projections)."""
+    from mogt_amd import gemm_tuning
+
+    lines = gemm_tuning.TABLE.read_text().splitlines()
+    head = {ln.split(",")[1]: ln.split(",")[2] for ln in lines if ln.startswith("Validator,")}
+    assert head["GCN_ARCH_NAME"].startswith("gfx950") and "PT_VERSION" in head
+    rows = [ln.split(",") for ln in lines if ln.startswith("GemmTunableOp_")]
+    assert len(rows) >= 40 and all(len(r) == 4 and float(r[3]) > 0 for r in rows)
+    shapes = {r[1] for r in rows}
+    assert any(s.startswith("tn_6144_32768_768") for s in shapes)   # the fused [w1; w2] projection
