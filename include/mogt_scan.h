@@ -269,7 +269,8 @@ int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, con
  *   -- RMSNorm.forward, model_mogt.py:9-20 (statistics in fp32).
  * mogt_add_rmsnorm_fwd: x_out = x + (scale * z) [the product rounded to z's
  *   dtype], out = rmsnorm(x_out) -- the residual update followed by the next
- *   RMSNorm (model_mogt.py:243-256), x and x_out fp32.
+ *   RMSNorm (model_mogt.py:243-256), x and x_out fp32; x_out may be null when
+ *   only the normalised row is needed (the backbone's final norm_f).
  * mogt_silu_mul_fwd: y = [rows, 2*hidden] (w1 | w2 outputs), out = silu(y1) *
  *   y2 [rows, hidden] -- SwiGLU.forward, model_mogt.py:29-30 (silu result
  *   rounded to the tensor dtype before the product, as torch does).          */

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[k][e] += rnd<TZ>(scale * zz[e]);
-                store_vec<float, 4>(x_out + row * D + c, v[k]);
+                if (x_out) store_vec<float, 4>(x_out + row * D + c, v[k]);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) ss = fmaf(v[k][e], v[k][e], ss);
@@ -377,7 +377,7 @@ extern "C" int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, 
     if (rc) return rc;
     if (!dt_ok(z_dtype) || !dt_ok(out_dtype)) return set_error(MOGT_E_INVALID, "add_rmsnorm: dtype");
     if (rows == 0) return MOGT_OK;
-    if (!x || !z || !weight || !x_out || !out) return set_error(MOGT_E_INVALID, "add_rmsnorm: null pointer");
+    if (!x || !z || !weight || !out) return set_error(MOGT_E_INVALID, "add_rmsnorm: null pointer");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int D = static_cast<int>(dim);
     if (z_dtype == MOGT_F32 && out_dtype == MOGT_F32)

@@ -398,11 +398,23 @@ class MOGTBlock(_WeightCacheOwner):
             const = pt if const is None else const + pt
         return (z if const is None else z + const).contiguous()
 
-    def _value_and_gate_projection(self, xn: torch.Tensor, prefix_condition: torch.Tensor | None):
+    def _gate_const_weights(self):
+        """(W_pref or None, bias or None) of the value gate: the weights of its
+        per-sequence logit term."""
+        gate: nn.Linear = self.phi_value_gate
+        parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
+        D = self.d_model
+        w_pref = gate.weight[:, parts.index("prefix") * D:(parts.index("prefix") + 1) * D] if "prefix" in parts \
+            else None
+        return w_pref, gate.bias
+
+    def _value_and_gate_projection(self, xn: torch.Tensor, prefix_condition: torch.Tensor | None,
+                                   const: torch.Tensor | None = None, const_given: bool = False):
         """One GEMM of x against [phi_val; W_cur; W_prev]: v and the value gate's
         pre-logits for the current and the previous token side by side, plus
-        the per-sequence logit term (bias + prefix term, fp32 [B, r] or [r]).
-        Returns (proj, has_prev, const)."""
+        the per-sequence logit term (bias + prefix term, fp32 [B, r] or [r]),
+        unless the caller passes it (``const_given``).  Returns (proj,
+        has_prev, const)."""
         gate: nn.Linear = self.phi_value_gate
         parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
         D = self.d_model
@@ -414,6 +426,8 @@ class MOGTBlock(_WeightCacheOwner):
         stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
         W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W), lambda: torch.cat(stacked, dim=0))
         proj = F.linear(xn, W_all)
+        if const_given:
+            return proj, "prev" in cols, const
         const = gate.bias.float() if gate.bias is not None else None
         if "prefix" in cols and prefix_condition is not None:
             pref = prefix_condition.to(dtype=xn.dtype).view(xn.size(0), D)
@@ -421,7 +435,7 @@ class MOGTBlock(_WeightCacheOwner):
             const = pt if const is None else pt + const
         return proj, "prev" in cols, const
 
-    def _mixer_inference(self, x, xn, prefix_condition, damping: float, gemm_dtype):
+    def _mixer_inference(self, x, xn, prefix_condition, damping: float, gemm_dtype, gate_const=None):
         """Mixer of the fused path without autograd.  One GEMM gives phi_val's
         output and the gate's pre-logits, which the scan combines into the
         logits itself.  norm_out is folded around the read-out GEMM: the scan
@@ -429,7 +443,8 @@ class MOGTBlock(_WeightCacheOwner):
         against theta_read * norm_out.weight, and the next RMSNorm applies each
         row's factor rsqrt(mean(h^2) + eps) as it reads Z."""
         with torch.autograd.profiler.record_function("mogt.affine_scan"):
-            proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition)
+            proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition, gate_const,
+                                                                      const_given=gate_const is not None)
             h, stats = ops.coupled_rank_scan_proj(proj, self.d_model, rank=self.r, gate_prev=gate_prev,
                                                   gate_const=gconst, damping=damping)
         with torch.autograd.profiler.record_function("mogt.readout"):
@@ -466,11 +481,12 @@ class MOGTBlock(_WeightCacheOwner):
         return ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight, self.norm_ffn.eps,
                                out_dtype=gemm_dtype)
 
-    def forward_fused(self, x: torch.Tensor, prefix_condition, pending):
+    def forward_fused(self, x: torch.Tensor, prefix_condition, pending, gate_const=None):
         """Fused forward.  ``pending = (z, scale)`` is the previous block's last
-        residual term (added here inside the first RMSNorm).  Returns
-        ``(x_after_mixer, (ffn_out, ffn_scale))``: the caller adds the FFN term
-        (or hands it to the next block)."""
+        residual term (added here inside the first RMSNorm).  ``gate_const``
+        (inference only): this block's per-sequence gate-logit term when the
+        caller computed it.  Returns ``(x_after_mixer, (ffn_out, ffn_scale))``:
+        the caller adds the FFN term (or hands it to the next block)."""
         gemm_dtype = _autocast_dtype() or x.dtype
         eps = self.norm_mogt.eps
         if pending is None:
@@ -478,8 +494,10 @@ class MOGTBlock(_WeightCacheOwner):
         else:
             x, xn = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_mogt.weight, eps, out_dtype=gemm_dtype)
         damping = float(getattr(self, "connection_damping", 0.999))
-        mixer = self._mixer_training if torch.is_grad_enabled() else self._mixer_inference
-        x, xn2 = mixer(x, xn, prefix_condition, damping, gemm_dtype)
+        if torch.is_grad_enabled():
+            x, xn2 = self._mixer_training(x, xn, prefix_condition, damping, gemm_dtype)
+        else:
+            x, xn2 = self._mixer_inference(x, xn, prefix_condition, damping, gemm_dtype, gate_const)
         with torch.autograd.profiler.record_function("mogt.ffn"):
             f = self.ffn(xn2)
         return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
@@ -507,6 +525,31 @@ class MOGTModel(_WeightCacheOwner):
         pos = int(pos)
         return h[:, pos, :] if -h.size(1) <= pos < h.size(1) else None
 
+    def _gate_consts(self, cond: torch.Tensor | None) -> list:
+        """Every block's per-sequence gate-logit term (bias + prefix term) in
+        one fp32 GEMV over the stacked prefix weights (inference); entries are
+        fp32 [B, r], or None for a gate without either."""
+        specs = [blk._gate_const_weights() for blk in self.blocks]
+        if all(wp is None and b is None for wp, b in specs):
+            return [None] * len(self.blocks)
+        r = self.blocks[0].r
+        params = tuple(t for wp, b in specs for t in (wp, b) if t is not None)
+        D = self.embedding.embedding_dim
+
+        def build():
+            ws = [wp if wp is not None else torch.zeros(r, D, device=params[0].device) for wp, _ in specs]
+            bs = [b if b is not None else torch.zeros(r, device=params[0].device) for _, b in specs]
+            return torch.cat([torch.cat(ws, 0).float(), torch.cat(bs, 0).float()[:, None]], dim=1)
+
+        with torch.autocast("cuda", enabled=False):
+            Wb = _gemm_weight(self, "gate_consts", params, build)   # [n * r, D + 1] fp32
+            if cond is None:
+                allc = Wb[:, D].expand(1, -1)
+            else:
+                allc = torch.addmm(Wb[:, D], cond.float(), Wb[:, :D].t())
+        B = cond.size(0) if cond is not None else 1
+        return [allc[:, i * r:(i + 1) * r].expand(B, r) for i in range(len(self.blocks))]
+
     def _checkpointed(self, index: int) -> bool:
         if not (self.training and getattr(self, "gradient_checkpointing", False)):
             return False
@@ -520,9 +563,12 @@ class MOGTModel(_WeightCacheOwner):
         if chain_fused:
             # each block hands its FFN term to the next block's first RMSNorm;
             # the last one is added inside norm_f
+            consts = self._gate_consts(cond) if not torch.is_grad_enabled() else [None] * len(self.blocks)
             pending = None
-            for blk in self.blocks:
-                h, pending = blk.forward_fused(h, cond, pending)
+            for blk, gc in zip(self.blocks, consts):
+                h, pending = blk.forward_fused(h, cond, pending, gc)
+            if not torch.is_grad_enabled():
+                return ops.add_rmsnorm_final(h, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps)
             return ops.add_rmsnorm(h, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps,
                                    out_dtype=torch.float32)[1]
         for i, blk in enumerate(self.blocks):

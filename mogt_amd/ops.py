@@ -863,6 +863,37 @@ def add_rmsnorm(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Te
     return torch.ops.mogt.add_rmsnorm(x, z, float(scale), weight, float(eps), out_dtype)
 
 
+@torch.library.custom_op("mogt::add_rmsnorm_final", mutates_args=())
+def _add_rmsnorm_final_op(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Tensor, eps: float,
+                          out_dtype: torch.dtype) -> torch.Tensor:
+    lib = _lib.load()
+    x = x.contiguous()
+    z = z.contiguous()
+    w = weight.contiguous().to(torch.float32)
+    D = x.shape[-1]
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    rc = lib.mogt_add_rmsnorm_fwd(x.data_ptr(), z.data_ptr(), float(scale), w.data_ptr(), None, out.data_ptr(),
+                                  x.numel() // D, D, float(eps), dtype_code(z.dtype, "add_rmsnorm_final"),
+                                  dtype_code(out_dtype, "add_rmsnorm_final"), _stream_handle(x.device))
+    _lib.check(rc, "mogt_add_rmsnorm_fwd")
+    return out
+
+
+@_add_rmsnorm_final_op.register_fake
+def _(x, z, scale, weight, eps, out_dtype):
+    return x.new_empty(x.shape, dtype=out_dtype)
+
+
+def add_rmsnorm_final(x: torch.Tensor, z: torch.Tensor, scale: float, weight: torch.Tensor, eps: float = 1e-6,
+                      out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``rmsnorm(x + scale * z) * weight`` without writing the updated residual
+    stream (the last norm of the backbone).  No autograd."""
+    require_cuda("add_rmsnorm_final", x, z, weight)
+    if x.dtype != torch.float32 or x.shape != z.shape:
+        raise ValueError("add_rmsnorm_final: x float32 and z of the same shape")
+    return torch.ops.mogt.add_rmsnorm_final(x, z, float(scale), weight, float(eps), out_dtype)
+
+
 @torch.library.custom_op("mogt::add_rmsnorm_rowscale", mutates_args=())
 def _add_rmsnorm_rowscale_op(x: torch.Tensor, z: torch.Tensor, stats: torch.Tensor, stat_eps: float, scale: float,
                              weight: torch.Tensor, eps: float, out_dtype: torch.dtype
