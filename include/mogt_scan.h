@@ -281,6 +281,16 @@ int mogt_add_rmsnorm_fwd(const float* x, const void* z, float scale, const float
                          int z_dtype, int out_dtype, void* stream);
 int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, int dtype,
                       void* stream);
+/* mogt_swiglu_gate_fwd: y = silu(x w_gate^T) * (x w_up^T) as one bf16 GEMM
+ *   with the gate in its epilogue -- SwiGLU.forward's silu(w1(x)) * w2(x),
+ *   model_mogt.py:29-30, without the [rows, 2*hidden] pre-activations.  x
+ *   [rows, d_in] (row stride ldx), w_gate / w_up [hidden, d_in] (nn.Linear
+ *   weights, contiguous), y [rows, hidden] (row stride ldy); dtype MOGT_BF16
+ *   only; fp32 accumulation, each linear output and the silu rounded to bf16
+ *   as in the unfused path.  d_in % 32 == 0, hidden % 128 == 0, ldx % 8 == 0,
+ *   ldy % 4 == 0; x and weights 16-byte aligned, y 8-byte aligned.           */
+int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
+                         int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, void* stream);
 /* mogt_add_rmsnorm_fwd for a read-out of an unnormalised row: z = W diag(w) h
  * (theta_read with norm_out's weight folded in), row_stats [rows, n_stats] the
  * partial sums of squares of h (mogt_coupled_rank_scan_stats_fwd).  With r =

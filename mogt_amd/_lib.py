@@ -111,6 +111,9 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
          _c_int, _c_int, _c_void_p]),
     "mogt_silu_mul_fwd": (_c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_swiglu_gate_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                 _c_void_p]),
     "mogt_add_rmsnorm_rowscale_fwd": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_float, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64,

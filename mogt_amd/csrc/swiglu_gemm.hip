@@ -1,0 +1,339 @@
+// The SwiGLU gate of the feed-forward block as one bf16 GEMM with the gate in
+// its epilogue (SwiGLU.forward, model_mogt.py:29-30, first half):
+//   y[m][n] = silu(x[m] . w_gate[n]) * (x[m] . w_up[n])
+// x [rows, K] (row stride ldx), w_gate / w_up [H, K] (nn.Linear weights), y
+// [rows, H] (row stride ldy), all bf16; fp32 accumulation.  The [rows, 2H]
+// pre-activations are never written.  The epilogue rounds like the unfused
+// path it replaces: each linear output to bf16, silu of it to bf16, then the
+// product to bf16.
+//
+// Tiling (v_mfma_f32_32x32x16_bf16, 4 waves, one work-group per CU):
+//   work-group  256 rows of x  x  128 outputs (128 w_gate rows + the same 128
+//               w_up rows)
+//   wave        128 rows of x x 64 outputs: 4 x 4 accumulator tiles of
+//               D[w][x] (weight row, x row) -- tiles 0, 1 gate, 2, 3 up, so a
+//               gate value and its up value sit in the same lane and register
+// With weight rows as the MFMA's A operand, a lane's 16 results are 4 groups
+// of 4 consecutive outputs of one x row: the gate is applied in registers and
+// each group leaves as one 8-byte store, no LDS round trip.
+//
+// Operands reach LDS by direct buffer-to-LDS loads (no staging registers) in
+// stages of 32 along K, four stages in flight (128 KB): stage s is multiplied
+// while stages s + 1 .. s + 3 load.  A stage holds 256 rows of x then 256 rows
+// of weights, 64 B per row; the 16-byte chunk c of row r sits at chunk
+// c ^ ((r / 2 ^ r / 4) % 4), so an MFMA operand read (consecutive rows, one
+// chunk) is free of bank conflicts whether the LDS serves 8 lanes x 16 B or
+// 16 lanes x 16 B per cycle.  One wave load instruction fills 1 KB of
+// LDS (16 rows) in lane order, so the swizzle is applied to the global
+// addresses.  These loads are issued from inline assembly and their
+// completion is awaited with explicit vmcnt waits: the compiler's own waits
+// for LDS-bound loads drain all of them before any LDS read.  Rows of x past
+// `rows` are loaded as the last valid row (their outputs are dropped by the
+// store descriptor's range).
+//
+// Work-group order is XCD-aware: the hardware deals work-groups round-robin
+// over the 8 XCDs, so block b is renumbered to give each XCD a contiguous run
+// of tiles, walked 8 row blocks at a time, so that one XCD's L2 keeps the x
+// rows of those 8 blocks while it sweeps the weight blocks.
+#include "common.h"
+
+namespace mogt {
+namespace {
+
+typedef __bf16 sg_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float sg_f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t sg_u32x2 __attribute__((ext_vector_type(2)));
+typedef int sg_i32x4 __attribute__((ext_vector_type(4)));
+typedef float sg_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 sg_bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int SG_BM = 256;                   // x rows per work-group
+constexpr int SG_BN = 128;                   // outputs per work-group
+constexpr int SG_BK = 32;                    // contraction per stage
+constexpr int SG_NST = 4;                    // stages in LDS
+constexpr int SG_THREADS = 256;              // 4 waves
+constexpr int SG_ROWB = SG_BK * 2;           // bytes per LDS row
+constexpr int SG_OPB = 256 * SG_ROWB;        // one operand of a stage (16 KB)
+constexpr int SG_STB = 2 * SG_OPB;           // one stage (32 KB)
+constexpr int SG_GROUP_M = 8;                // row blocks walked together per XCD
+
+struct SwigluParams {
+    const bf16_t* x;
+    const bf16_t* wg;
+    const bf16_t* wu;
+    bf16_t* y;
+    int64_t rows;
+    int64_t ldx, ldy;    // elements
+    int K, H;
+    int n_mb, n_nb;      // row blocks, output blocks
+};
+
+__device__ __forceinline__ float sg_silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+// two fp32 values as one word of two bf16 (round to nearest even)
+__device__ __forceinline__ uint32_t sg_pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((sg_f32x2{lo, hi}), sg_bf16x2));
+}
+
+// 64 lanes x 16 bytes from (rsrc, voff + soff) into LDS at lds .. lds + 1023
+__device__ __forceinline__ void sg_dma16(sg_i32x4 rsrc, int voff, int soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
+// wait until at most N vector memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void sg_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ sg_i32x4 sg_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    sg_i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));   // stride 0
+    r[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+    r[3] = 0x00020000;
+    return r;
+}
+
+// block id -> (row block, output block)
+__device__ __forceinline__ void sg_tile(const SwigluParams& p, int& mb, int& nb) {
+    const int n = p.n_mb * p.n_nb;
+    const int bid = blockIdx.x;
+    const int q = n >> 3, rem = n & 7;
+    const int xcd = bid & 7, loc = bid >> 3;
+    const int v = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
+    const int group = SG_GROUP_M * p.n_nb;
+    const int g = v / group, first = g * SG_GROUP_M;
+    const int gm = min(p.n_mb - first, SG_GROUP_M);
+    const int w = v - g * group;
+    mb = first + w % gm;
+    nb = w / gm;
+}
+
+__global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p) {
+    __shared__ __attribute__((aligned(1024))) char smem[SG_NST * SG_STB];   // [stage][x | w][256][64 B]
+    int mb, nb;
+    sg_tile(p, mb, nb);
+    const int64_t m0 = static_cast<int64_t>(mb) * SG_BM;
+    const int n0 = nb * SG_BN;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, hb = lane >> 5;
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+        (__attribute__((address_space(3))) char*)smem));
+
+    // loads: wave w fills rows 64 w .. 64 w + 63 of each operand, 16 rows
+    // (1 KB) per instruction; lane L takes row 16 i + L / 4 of its block and
+    // the global chunk that lands in LDS slot L % 4 under the swizzle
+    const int64_t mrows = p.rows - m0 < SG_BM ? p.rows - m0 : SG_BM;
+    const sg_i32x4 rx = sg_rsrc(p.x + m0 * p.ldx, static_cast<uint32_t>(mrows * p.ldx * 2));
+    const sg_i32x4 rw = sg_rsrc((wave < 2 ? p.wg : p.wu) + static_cast<int64_t>(n0) * p.K,
+                                static_cast<uint32_t>(SG_BN * p.K * 2));
+    const int lc = (lane & 3) ^ (((lane >> 3) ^ (lane >> 4)) & 3);
+    int vx[4], vw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 64 * wave + 16 * i + (lane >> 2);
+        const int rc = r < mrows ? r : static_cast<int>(mrows) - 1;
+        vx[i] = static_cast<int>(rc * p.ldx * 2) + lc * 16;
+        vw[i] = ((r & 127) * p.K) * 2 + lc * 16;
+    }
+    const uint32_t ldx_dst = lds0 + wave * 4096, ldw_dst = lds0 + SG_OPB + wave * 4096;
+    const int nk = p.K / SG_BK;
+    auto issue = [&](int s) {
+        const uint32_t st = (s & (SG_NST - 1)) * SG_STB;
+        const int kb = s * SG_ROWB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sg_dma16(rx, vx[i], kb, ldx_dst + st + i * 1024);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sg_dma16(rw, vw[i], kb, ldw_dst + st + i * 1024);
+    };
+
+    // fragment rows: x rows wm*128 + 32 i + l32; weight rows (gate) 64 wn + 32 j
+    // + l32, (up) 128 + 64 wn + 32 j + l32; every one has row % 16 == l32 % 16
+    const int xrow0 = (wm * 128 + l32) * SG_ROWB;
+    const int wrow0 = SG_OPB + (wn * 64 + l32) * SG_ROWB;
+    const int swz = ((l32 >> 1) ^ (l32 >> 2)) & 3;
+
+    sg_f32x16 acc[4][4];   // [weight tile][x tile]
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    // Fragments of a whole stage (2 K-steps: 4 x and 4 weight fragments each)
+    // are read into registers one stage ahead, so the MFMAs never wait on LDS.
+    // Stage s + 1 is awaited (this wave's loads, then the barrier for every
+    // wave's) between the two K-steps of stage s, its fragments read, and the
+    // loads of stage s + 3 issued into the buffer of stage s - 1, whose
+    // fragments every wave has consumed before that barrier.
+    // a: the stage's first K-step; b: its second; c: the next stage's second
+    // K-step, read during this stage.  b and c swap roles from stage to stage
+    // (the loop is unrolled by two), so no fragment is ever copied.
+    sg_bf16x8 a[8], b[8], c[8];   // x 0..3 | w 0..3
+    auto frag_ptr = [&](const char* st, int ks, int f) {
+        const int cb = ((2 * ks + hb) ^ swz) << 4;
+        const int row = f < 4 ? xrow0 + f * 32 * SG_ROWB : wrow0 + (((f - 4) >> 1) * 128 + ((f - 4) & 1) * 32) * SG_ROWB;
+        return reinterpret_cast<const sg_bf16x8*>(st + row + cb);
+    };
+    auto read_stage = [&](int s, sg_bf16x8 (&f0)[8], sg_bf16x8 (&f1)[8]) {
+        const char* st = smem + (s & (SG_NST - 1)) * SG_STB;
+#pragma unroll
+        for (int f = 0; f < 8; ++f) f0[f] = *frag_ptr(st, 0, f);
+#pragma unroll
+        for (int f = 0; f < 8; ++f) f1[f] = *frag_ptr(st, 1, f);
+    };
+    auto mfma_half = [&](const sg_bf16x8 (&f)[8]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[4 + j], f[i], acc[j][i], 0, 0, 0);
+    };
+    // One stage with every later stage present: the second K-step's 16 MFMAs
+    // (fragments `cur`) are interleaved one to one with the 8 loads of stage
+    // s + 3 and the 16 fragment reads of stage s + 1 (first K-step into a,
+    // free since the first half, then the second K-step into `next`).
+    auto steady = [&](int s, const sg_bf16x8 (&cur)[8], sg_bf16x8 (&next)[8]) {
+        mfma_half(a);
+        __builtin_amdgcn_sched_barrier(0);
+        sg_wait_vm<8>();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t dst = ((s + 3) & (SG_NST - 1)) * SG_STB;
+        const int kb = (s + 3) * SG_ROWB;
+        const char* stn = smem + ((s + 1) & (SG_NST - 1)) * SG_STB;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int j = t >> 2, i = t & 3;
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[4 + j], cur[i], acc[j][i], 0, 0, 0);
+            if (t < 4)
+                sg_dma16(rx, vx[t], kb, ldx_dst + dst + t * 1024);
+            else if (t < 8)
+                sg_dma16(rw, vw[t - 4], kb, ldw_dst + dst + (t - 4) * 1024);
+            if (t < 8)
+                a[t] = *frag_ptr(stn, 0, t);
+            else
+                next[t - 8] = *frag_ptr(stn, 1, t - 8);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    issue(0);
+    if (nk > 1) issue(1);
+    if (nk > 2) issue(2);
+    if (nk > 2)
+        sg_wait_vm<16>();
+    else if (nk > 1)
+        sg_wait_vm<8>();
+    else
+        sg_wait_vm<0>();
+    __syncthreads();
+    read_stage(0, a, b);
+    int s = 0;
+    for (; s + 4 < nk; s += 2) {
+        steady(s, b, c);
+        steady(s + 1, c, b);
+    }
+    if (s + 3 < nk) {
+        steady(s, b, c);
+#pragma unroll
+        for (int f = 0; f < 8; ++f) b[f] = c[f];
+        ++s;
+    }
+    // the last (up to) three stages
+    for (; s < nk; ++s) {
+        mfma_half(a);
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < nk) {
+            if (s + 2 < nk)
+                sg_wait_vm<8>();
+            else
+                sg_wait_vm<0>();
+            __syncthreads();
+            read_stage(s + 1, a, c);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half(b);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < 8; ++f) b[f] = c[f];
+    }
+
+    // epilogue: lane (l32, hb), register group q: x row 32 i + l32, outputs
+    // 32 j + 8 q + 4 hb .. + 3 of the wave's 64
+    const auto ry = __builtin_amdgcn_make_buffer_rsrc(p.y + m0 * p.ldy, 0, static_cast<int>(mrows * p.ldy * 2),
+                                                      0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row_off = static_cast<int>((wm * 128 + 32 * i + l32) * p.ldy * 2);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float g = round_bf16(acc[j][i][4 * q + e]);
+                    const float u = round_bf16(acc[j + 2][i][4 * q + e]);
+                    o[e] = round_bf16(sg_silu(g)) * u;
+                }
+                const sg_u32x2 w = {sg_pack(o[0], o[1]), sg_pack(o[2], o[3])};
+                const int col = n0 + wn * 64 + 32 * j + 8 * q + 4 * hb;
+                __builtin_amdgcn_raw_buffer_store_b64(w, ry, row_off + col * 2, 0, 0);
+            }
+        }
+    }
+}
+
+}  // namespace
+}  // namespace mogt
+
+using namespace mogt;
+
+extern "C" int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
+                                    int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype,
+                                    void* stream) {
+    clear_error();
+    if (dtype != MOGT_BF16) return set_error(MOGT_E_INVALID, "swiglu_gate: bf16 operands only");
+    if (rows < 0 || d_in <= 0 || hidden <= 0) return set_error(MOGT_E_INVALID, "swiglu_gate: bad shape");
+    if (d_in % SG_BK != 0 || hidden % SG_BN != 0)
+        return set_error(MOGT_E_INVALID, "swiglu_gate: d_in must be a multiple of %d and hidden of %d", SG_BK, SG_BN);
+    if (ldx < d_in || ldy < hidden || ldx % 8 != 0 || ldy % 4 != 0)
+        return set_error(MOGT_E_INVALID, "swiglu_gate: row strides must cover the rows (ldx %% 8 == 0, ldy %% 4 == 0)");
+    if (rows == 0) return MOGT_OK;
+    if (!x || !w_gate || !w_up || !y) return set_error(MOGT_E_INVALID, "swiglu_gate: null pointer");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_gate) | reinterpret_cast<uintptr_t>(w_up)) & 15 ||
+        reinterpret_cast<uintptr_t>(y) & 7)
+        return set_error(MOGT_E_INVALID, "swiglu_gate: x and weights need 16-byte, y 8-byte alignment");
+    // per-block byte ranges and offsets are 32-bit
+    if (static_cast<int64_t>(SG_BM) * (ldx > ldy ? ldx : ldy) * 2 >= (int64_t(1) << 31) ||
+        static_cast<int64_t>(SG_BN) * d_in * 2 >= (int64_t(1) << 31))
+        return set_error(MOGT_E_INVALID, "swiglu_gate: row strides too large");
+    const int64_t n_mb = (rows + SG_BM - 1) / SG_BM;
+    const int64_t n_nb = hidden / SG_BN;
+    if (n_mb * n_nb > 0x7fffffff) return set_error(MOGT_E_INVALID, "swiglu_gate: too many tiles");
+    SwigluParams prm{};
+    prm.x = static_cast<const bf16_t*>(x);
+    prm.wg = static_cast<const bf16_t*>(w_gate);
+    prm.wu = static_cast<const bf16_t*>(w_up);
+    prm.y = static_cast<bf16_t*>(y);
+    prm.rows = rows;
+    prm.ldx = ldx;
+    prm.ldy = ldy;
+    prm.K = static_cast<int>(d_in);
+    prm.H = static_cast<int>(hidden);
+    prm.n_mb = static_cast<int>(n_mb);
+    prm.n_nb = static_cast<int>(n_nb);
+    hipLaunchKernelGGL(swiglu_gemm_kernel, dim3(static_cast<unsigned>(n_mb * n_nb)), dim3(SG_THREADS), 0,
+                       static_cast<hipStream_t>(stream), prm);
+    return check_launch("swiglu_gemm_kernel");
+}

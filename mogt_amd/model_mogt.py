@@ -112,11 +112,19 @@ class SwiGLU(nn.Module):
         self.w3 = nn.Linear(hidden_dim, d_model, bias=False)
 
     def forward(self, x):
+        w3 = _gemm_weight(self, "w3", (self.w3.weight,), lambda: self.w3.weight)
+        if not torch.is_grad_enabled() and x.is_cuda:
+            # bf16 without gradients: silu(w1 x) * w2 x is one GEMM whose
+            # epilogue applies the gate (csrc/swiglu_gemm.hip)
+            w1 = _gemm_weight(self, "w1", (self.w1.weight,), lambda: self.w1.weight)
+            w2 = _gemm_weight(self, "w2", (self.w2.weight,), lambda: self.w2.weight)
+            xb = x.to(w1.dtype) if _autocast_dtype() is not None else x
+            if ops.swiglu_gate_supported(xb, w1, w2):
+                return F.linear(ops.swiglu_gate(xb, w1, w2), w3)
         # one GEMM against [w1; w2], then the fused gate (autograd through the
         # silu_mul backward kernel and torch.cat back to w1, w2)
         w12 = _gemm_weight(self, "w12", (self.w1.weight, self.w2.weight),
                            lambda: torch.cat([self.w1.weight, self.w2.weight], dim=0))
-        w3 = _gemm_weight(self, "w3", (self.w3.weight,), lambda: self.w3.weight)
         return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
 
 

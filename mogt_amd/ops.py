@@ -955,6 +955,52 @@ def _(y):
     return y.new_empty((*y.shape[:-1], y.shape[-1] // 2))
 
 
+@torch.library.custom_op("mogt::swiglu_gate", mutates_args=())
+def _swiglu_gate_op(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    lib = _lib.load()
+    x = x if x.stride(-1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 else x.contiguous()
+    w_gate = w_gate.contiguous()
+    w_up = w_up.contiguous()
+    H, K = w_gate.shape
+    y = torch.empty((x.shape[0], H), dtype=x.dtype, device=x.device)
+    rc = lib.mogt_swiglu_gate_fwd(x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), y.data_ptr(), x.shape[0], K, H,
+                                  x.stride(0), y.stride(0), dtype_code(x.dtype, "swiglu_gate"),
+                                  _stream_handle(x.device))
+    _lib.check(rc, "mogt_swiglu_gate_fwd")
+    return y
+
+
+@_swiglu_gate_op.register_fake
+def _(x, w_gate, w_up):
+    return x.new_empty((x.shape[0], w_gate.shape[0]))
+
+
+SWIGLU_GATE_K_MULTIPLE = 32
+SWIGLU_GATE_H_MULTIPLE = 128
+
+
+def swiglu_gate_supported(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> bool:
+    """Whether ``swiglu_gate`` takes these operands: bf16 CUDA tensors, the
+    input dimension a multiple of 32 and the hidden size of 128."""
+    return (x.is_cuda and x.dtype == torch.bfloat16 and w_gate.dtype == torch.bfloat16
+            and w_up.dtype == torch.bfloat16 and w_gate.shape == w_up.shape and w_gate.ndim == 2
+            and x.shape[-1] == w_gate.shape[1] and w_gate.shape[1] % SWIGLU_GATE_K_MULTIPLE == 0
+            and w_gate.shape[0] % SWIGLU_GATE_H_MULTIPLE == 0)
+
+
+def swiglu_gate(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """``silu(x @ w_gate.T) * (x @ w_up.T)`` in bf16 as one GEMM whose
+    epilogue applies the gate (model_mogt.py:29-30); each linear output and
+    the silu are rounded to bf16 as in the unfused expression.  x ``[..., K]``,
+    weights ``[H, K]``.  No autograd."""
+    require_cuda("swiglu_gate", x, w_gate, w_up)
+    if not swiglu_gate_supported(x, w_gate, w_up):
+        raise ValueError("swiglu_gate needs bf16 x [..., K] and weights [H, K] with K % 32 == 0, H % 128 == 0")
+    lead = x.shape[:-1]
+    y = torch.ops.mogt.swiglu_gate(x.reshape(-1, x.shape[-1]), w_gate, w_up)
+    return y.reshape(*lead, w_gate.shape[0])
+
+
 # backward of the row kernels -------------------------------------------------
 def _rows_per_wave(rows: int) -> int:
     # about 2048 waves, at least 4 rows each: the dw partials stay a few MB

@@ -66,6 +66,17 @@ def test_argument_errors_without_device(lib):
     rc = lib.mogt_lm_ce_bwd(8, 32, 0, 1, 1, 4, 32, -100, 1, 8, 40, 0, None)
     assert rc == -1 and b"in place" in lib.mogt_last_error()
     assert lib.mogt_lm_ce_fwd(None, 32, 0, None, 0, 32, -100, None, None, None) == 0
+    # fused SwiGLU gate: bf16 only, d_in % 32, hidden % 128, strides covering
+    # the rows
+    assert lib.mogt_swiglu_gate_fwd(16, 16, 16, 16, 8, 64, 128, 64, 128, 0, None) == -1
+    rc = lib.mogt_swiglu_gate_fwd(16, 16, 16, 16, 8, 48, 128, 48, 128, 1, None)
+    assert rc == -1 and b"multiple" in lib.mogt_last_error()
+    assert lib.mogt_swiglu_gate_fwd(16, 16, 16, 16, 8, 64, 96, 64, 96, 1, None) == -1
+    rc = lib.mogt_swiglu_gate_fwd(16, 16, 16, 16, 8, 64, 128, 32, 128, 1, None)
+    assert rc == -1 and b"stride" in lib.mogt_last_error()
+    rc = lib.mogt_swiglu_gate_fwd(8, 16, 16, 16, 8, 64, 128, 64, 128, 1, None)
+    assert rc == -1 and b"align" in lib.mogt_last_error()
+    assert lib.mogt_swiglu_gate_fwd(None, None, None, None, 0, 64, 128, 64, 128, 1, None) == 0
 
 
 def test_empty_problems_are_noops_without_device(lib):
