@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "scan core ms + HBM GB/s at D768 L=32768; MOGT 4-layer fwd ms"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 REF_TRITON_CORE_MS_L4 = 5.48   # reference hybrid core @ L=32768 (R=16, C=48, NVIDIA L4)
 
 
@@ -42,7 +43,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--only", choices=["diag", "coupled", "rank1", "dense", "backbone", "all"], default="all",
+    p.add_argument("--only", choices=["diag", "coupled", "rank1", "dense", "swiglu", "backbone", "all"],
+                   default="all",
                    help="after the headline: every extra (all), none (diag), or only the coupled "
                         "mixer scan, rank-1 (configs[2]), dense (core shape and configs[3]) or "
                         "backbone (configs[4] forward and training step) lines")
@@ -254,6 +256,34 @@ def _reference_chunked_ce_torch(torch, hidden, weight, labels, chunk):
             gh[s:e] = probs.matmul(wf).to(hidden.dtype)
             gw = gw + probs.t().matmul(hc.float())
     return loss / T, gh, gw
+
+
+def measure_swiglu(torch, steps, warmup, rows=32768, d_in=768, hidden=3072):
+    """The FFN's gate (model_mogt.py:29-30) at configs[4]'s shape: the fused
+    SwiGLU GEMM (csrc/swiglu_gemm.hip) against the unfused path (one library
+    GEMM against [w1; w2], then the silu_mul row kernel), bf16."""
+    import torch.nn.functional as F
+    from mogt_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    x = torch.randn(rows, d_in, generator=gen, device=dev).bfloat16()
+    wg = (torch.randn(hidden, d_in, generator=gen, device=dev) / d_in ** 0.5).bfloat16()
+    wu = (torch.randn(hidden, d_in, generator=gen, device=dev) / d_in ** 0.5).bfloat16()
+    w12 = torch.cat([wg, wu], 0)
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    runs = {"fused": lambda i: ops.swiglu_gate(x, wg, wu), "unfused": lambda i: ops.silu_mul(F.linear(x, w12)),
+            "gemm": lambda i: F.linear(x, w12)}
+    # the three are timed in turn, three rounds, best of each: the first
+    # kernels of a process otherwise run before the clocks have settled
+    best = {k: float("inf") for k in runs}
+    for _ in range(3):
+        for k, f in runs.items():
+            best[k] = min(best[k], timer.time(f, steps, warmup))
+    ms_fused, ms_unfused, ms_gemm = best["fused"], best["unfused"], best["gemm"]
+    flop = 2.0 * rows * d_in * 2 * hidden
+    return {"ms": ms_fused, "ms_unfused": ms_unfused, "ms_gemm_only": ms_gemm, "tflops": flop / ms_fused / 1e9}
 
 
 def measure_lm_ce(torch, lib, steps, warmup, rows=4096, vocab=32000, L=32768, D=768, chunk=4096):
@@ -735,6 +765,14 @@ def main():
                 "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
                         "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
                         "torch ops on the same GPU"}
+        if full or args.only == "swiglu":
+            r = measure_swiglu(torch, args.steps, args.warmup)
+            extras["swiglu_gate_gemm_32768x768_to_3072_bf16"] = {
+                "us": round(r["ms"] * 1e3, 2), "TFLOP/s": round(r["tflops"], 1),
+                "frac_bf16_mfma_peak": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                "unfused_us": round(r["ms_unfused"] * 1e3, 2), "library_gemm_only_us": round(r["ms_gemm_only"] * 1e3, 2),
+                "note": "FFN gate silu(x w1^T) * (x w2^T) as one GEMM with the gate in its epilogue vs the "
+                        "library GEMM against [w1; w2] + the silu_mul row kernel (model_mogt.py:29-30)"}
         if full or args.only == "backbone":
             from mogt_amd import gemm_tuning
 
@@ -747,7 +785,7 @@ def main():
             r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3) if tuned else d4
             extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
                 r, ffn_hidden=3072, vocab=32000, default_gemms_ms=d4["ms"], tuned_gemm_table=tuned,
-                mfma_frac=round(2.174e12 / (r["ms"] * 1e-3) / 2.5e15, 4),
+                mfma_frac=round(2.174e12 / (r["ms"] * 1e-3) / (MFMA_BF16_PEAK_TFLOPS * 1e12), 4),
                 note="BASELINE configs[4]: 4 layers, 4x gated MLP, bf16 autocast; target < 77.56 ms; "
                      "ms with the tuned GEMM table, default_gemms_ms with the libraries' own choice; "
                      "mfma_frac = 2.174 TFLOP of GEMMs / time / 2.5 PFLOP/s")
