@@ -149,11 +149,12 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
     const TX* __restrict__ x, const float* __restrict__ w, const TG* __restrict__ dy,
     const float* __restrict__ dres, TX* __restrict__ dx, float* __restrict__ dw_part, int64_t rows, int D,
     float eps, int rows_per_wave, void* __restrict__ dz, float dz_scale, int dz_bf16) {
-    const int lane = threadIdx.x & 63;
-    const int64_t gw = static_cast<int64_t>(blockIdx.x) * NA_WAVES + (threadIdx.x >> 6);
+    extern __shared__ float dw_lds[];   // [NA_WAVES][D]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * NA_WAVES + wave;
     const int64_t r0 = gw * rows_per_wave;
-    if (r0 >= rows) return;
-    const int64_t r1 = r0 + rows_per_wave < rows ? r0 + rows_per_wave : rows;
+    // a wave past the last row has no rows but still joins the group's dw sum
+    const int64_t r1 = r0 >= rows ? r0 : (r0 + rows_per_wave < rows ? r0 + rows_per_wave : rows);
     float ww[VPL][4], acc[VPL][4];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
         }
     };
     float v[VPL][4], g[VPL][4], rr[VPL][4];
-    load_row(r0, v, g, rr);
+    if (r0 < r1) load_row(r0, v, g, rr);
     for (int64_t row = r0; row < r1; ++row) {
         float vn[VPL][4], gn[VPL][4], rn[VPL][4];
         if (row + 1 < r1) load_row(row + 1, vn, gn, rn);
@@ -230,10 +231,19 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
                 }
         }
     }
+    // the group's waves' dw partials summed in wave order (deterministic):
+    // one partial row per work-group
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int c = (k * 64 + lane) * 4;
-        if (c < D) store_vec<float, 4>(dw_part + gw * D + c, acc[k]);
+        if (c < D) store_vec<float, 4>(dw_lds + wave * D + c, acc[k]);
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < D; c += 64 * NA_WAVES) {
+        float t = dw_lds[c];
+#pragma unroll
+        for (int q = 1; q < NA_WAVES; ++q) t += dw_lds[q * D + c];
+        dw_part[static_cast<int64_t>(blockIdx.x) * D + c] = t;
     }
 }
 
@@ -293,12 +303,13 @@ int launch_norm_bwd(const void* x, const float* w, const void* dy, const float* 
     const int64_t waves = (rows + rpw - 1) / rpw;
     const dim3 grid(static_cast<unsigned>((waves + NA_WAVES - 1) / NA_WAVES));
     const dim3 block(64 * NA_WAVES);
+    const size_t lds = static_cast<size_t>(NA_WAVES) * D * sizeof(float);
     const TX* xp = static_cast<const TX*>(x);
     const TG* gp = static_cast<const TG*>(dy);
     TX* dxp = static_cast<TX*>(dx);
 #define MOGT_NORM_BWD_CASE(V)                                                                     \
     if (vpl <= V) {                                                                                \
-        hipLaunchKernelGGL((rmsnorm_bwd_kernel<TX, TG, V>), grid, block, 0, st, xp, w, gp, dres, dxp, \
+        hipLaunchKernelGGL((rmsnorm_bwd_kernel<TX, TG, V>), grid, block, lds, st, xp, w, gp, dres, dxp, \
                            dw_part, rows, D, eps, rpw, dz, dz_scale, dz_bf16);                      \
         return check_launch("rmsnorm_bwd_kernel");                                                 \
     }

@@ -430,7 +430,9 @@ class MOGTBlock(_WeightCacheOwner):
         if W.shape[1] != len(parts) * D:
             raise RuntimeError(f"phi_value_gate takes {W.shape[1]} inputs, the gate input mode builds "
                                f"{len(parts) * D}")
-        cols = {name: W[:, i * D:(i + 1) * D] for i, name in enumerate(parts)}
+        # column blocks as views whose backward is one stack (not one zero
+        # fill and copy per sliced block)
+        cols = dict(zip(parts, W.view(W.shape[0], len(parts), D).unbind(1)))
         stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
         W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W), lambda: torch.cat(stacked, dim=0))
         proj = F.linear(xn, W_all)
@@ -565,9 +567,13 @@ class MOGTModel(_WeightCacheOwner):
 
     def forward(self, input_ids):
         h = self.embedding(input_ids)
-        cond = self._prefix_condition(h)
         chain_fused = (h.dtype == torch.float32 and len(self.blocks) > 0 and not self._checkpointed(0)
                        and all(blk.fused_path_ok() for blk in self.blocks))
+        cond = self._prefix_condition(h)
+        if chain_fused and cond is not None and torch.is_grad_enabled():
+            # the same row looked up again: its gradient goes to the embedding
+            # table directly instead of through a full-size slice of h
+            cond = self.embedding(input_ids[:, int(self.prefix_condition_position)])
         if chain_fused:
             # each block hands its FFN term to the next block's first RMSNorm;
             # the last one is added inside norm_f

@@ -1002,6 +1002,9 @@ def swiglu_gate(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> to
 
 
 # backward of the row kernels -------------------------------------------------
+RMSNORM_BWD_WAVES_PER_GROUP = 4   # mogt_rmsnorm_bwd writes one dw partial row per 4-wave work-group
+
+
 def _rows_per_wave(rows: int) -> int:
     # about 2048 waves, at least 4 rows each: the dw partials stay a few MB
     return max(4, -(-rows // 2048))
@@ -1017,7 +1020,8 @@ def _rmsnorm_bwd_launch(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
     rows = x.numel() // D
     rpw = _rows_per_wave(rows)
     dx = torch.empty_like(x)
-    parts = torch.empty((max(1, -(-rows // rpw)), D), dtype=torch.float32, device=x.device)
+    groups = -(-(-(-rows // rpw)) // RMSNORM_BWD_WAVES_PER_GROUP)
+    parts = torch.empty((max(1, groups), D), dtype=torch.float32, device=x.device)
     if dres is not None:
         dres = dres.contiguous().to(torch.float32)
     rc = lib.mogt_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
