@@ -22,7 +22,7 @@ int coupled_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
 
 // Tiles of the row-statistics variant: the default tiles, all 64 features
 // wide, so the statistics have one column per 64 features whatever the pick.
-#define MOGT_COUPLED_STAT_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(2, 32, 8, 16) X(2, 32, 16, 8) X(1, 64, 8, 16) \
+#define MOGT_COUPLED_STAT_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(4, 16, 16, 8) X(2, 32, 8, 16) X(2, 32, 16, 8) X(1, 64, 8, 16) \
     X(1, 64, 32, 16) X(1, 64, 16, 16)
 
 template <typename TV, typename TO>
@@ -56,7 +56,7 @@ bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
 // lanes of one vector must share a gate, so the vector must divide the channel
 // count), 512-step chunks; short problems fall back to shorter chunks.
 DiagTile coupled_tile(int64_t B, int64_t L, int64_t R, int64_t C, int align_elems) {
-    static const TileChoice v4[] = {{{4, 16, 8, 16}, 512}, {{4, 16, 8, 8}, 128}, {{2, 32, 8, 16}, 128},
+    static const TileChoice v4[] = {{{4, 16, 16, 8}, 512}, {{4, 16, 8, 8}, 128}, {{2, 32, 8, 16}, 128},
                                     {{1, 64, 8, 16}, 0}};
     static const TileChoice v2[] = {{{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
     static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};

@@ -585,7 +585,7 @@ int diag_launch(const DiagParams& prm, hipStream_t stream) {
 // efficiency) and at most 64 stash registers per lane.
 #define MOGT_DIAG_F32_TILES(X) X(2, 32, 32, 8) X(2, 32, 16, 16) X(2, 32, 16, 8) X(2, 32, 32, 4) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 #define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 8) X(4, 16, 16, 16) X(4, 16, 8, 8) X(4, 32, 16, 8) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
-#define MOGT_COUPLED_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(4, 16, 16, 16) X(4, 32, 8, 16) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+#define MOGT_COUPLED_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(4, 16, 16, 8) X(4, 16, 16, 16) X(4, 32, 8, 16) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 
 // Per-family launchers (diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
 int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,

@@ -24,8 +24,8 @@ TILES_F32 = [(2, 32, 32, 8), (2, 32, 16, 16), (2, 32, 16, 8), (2, 32, 32, 4), (2
              (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
 TILES_BF16 = [(4, 16, 16, 8), (4, 16, 16, 16), (4, 16, 8, 8), (4, 32, 16, 8), (2, 32, 16, 8),
               (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
-TILES_COUPLED = [(4, 16, 8, 16), (4, 16, 8, 8), (4, 16, 16, 16), (4, 32, 8, 16), (2, 32, 16, 8), (2, 32, 16, 16),
-                 (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
+TILES_COUPLED = [(4, 16, 8, 16), (4, 16, 8, 8), (4, 16, 16, 8), (4, 16, 16, 16), (4, 32, 8, 16), (2, 32, 16, 8),
+                 (2, 32, 16, 16), (2, 32, 8, 16), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
 
 
 def _run_cfg(a, b, out_dtype, cfg, prefix=False):
