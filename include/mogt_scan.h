@@ -323,6 +323,19 @@ int mogt_rmsnorm_bwd(const void* x, const float* weight, const void* dy, const f
 int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, int64_t hidden,
                       int dtype, void* stream);
 
+/* Backward of the token embedding (nn.Embedding in MOGTModel.forward,
+ * model_mogt.py:262, 270, which torch differentiates by sorting the ids):
+ * dweight[v] = the sum of the grad rows of every position holding token v,
+ * summed in position order (deterministic).  The caller sorts the
+ * n token ids stably (sorted_ids, int64) with the positions in that order
+ * (positions, int64), zero-fills dweight (fp32 [vocab, dim]) and passes
+ * partials: fp32 [ceil(n / 16) * 2, dim] scratch.  grad: [n, dim] rows with
+ * stride ld_grad, fp32 or bf16; dim % 4 == 0, <= 4096.  Ids outside
+ * [0, vocab) are skipped.                                                    */
+int mogt_embedding_bwd(const void* grad, int64_t ld_grad, int grad_dtype, const int64_t* sorted_ids,
+                       const int64_t* positions, int64_t n, int64_t dim, int64_t vocab, float* dweight,
+                       float* partials, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Connection map of the transport, U = damping * f(scale * A) for a batch of
  * skew-symmetric r x r generators A (fp32 [count, r, r], r <= 32), replacing

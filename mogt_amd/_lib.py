@@ -122,6 +122,9 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_float,
                  _c_int, _c_int, _c_int, _c_void_p, _c_float, _c_int, _c_void_p]),
     "mogt_silu_mul_bwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
+    "mogt_embedding_bwd": (
+        _c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_void_p,
+                 _c_void_p]),
     "mogt_connection_map_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
     "mogt_lm_ce_fwd": (

@@ -566,14 +566,14 @@ class MOGTModel(_WeightCacheOwner):
         return index % max(1, int(getattr(self, "checkpoint_every_n", 1))) == 0
 
     def forward(self, input_ids):
-        h = self.embedding(input_ids)
+        h = ops.embedding(input_ids, self.embedding)
         chain_fused = (h.dtype == torch.float32 and len(self.blocks) > 0 and not self._checkpointed(0)
                        and all(blk.fused_path_ok() for blk in self.blocks))
         cond = self._prefix_condition(h)
         if chain_fused and cond is not None and torch.is_grad_enabled():
             # the same row looked up again: its gradient goes to the embedding
             # table directly instead of through a full-size slice of h
-            cond = self.embedding(input_ids[:, int(self.prefix_condition_position)])
+            cond = ops.embedding(input_ids[:, int(self.prefix_condition_position)], self.embedding)
         if chain_fused:
             # each block hands its FFN term to the next block's first RMSNorm;
             # the last one is added inside norm_f

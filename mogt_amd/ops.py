@@ -13,6 +13,7 @@ import os
 import threading
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -999,6 +1000,65 @@ def swiglu_gate(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> to
     lead = x.shape[:-1]
     y = torch.ops.mogt.swiglu_gate(x.reshape(-1, x.shape[-1]), w_gate, w_up)
     return y.reshape(*lead, w_gate.shape[0])
+
+
+# token embedding with a deterministic HIP backward -------------------------
+EMBEDDING_BLOCK = 16   # sorted positions per block of mogt_embedding_bwd
+
+
+@torch.library.custom_op("mogt::embedding_bwd", mutates_args=())
+def _embedding_bwd_op(grad: torch.Tensor, ids: torch.Tensor, vocab: int) -> torch.Tensor:
+    lib = _lib.load()
+    D = grad.shape[-1]
+    g = grad.reshape(-1, D)
+    if g.stride(-1) != 1 or g.stride(0) % 4 != 0 or g.data_ptr() % 16 != 0:
+        g = g.contiguous()
+    flat = ids.reshape(-1).to(torch.int64)
+    sorted_ids, positions = torch.sort(flat, stable=True)
+    n = flat.numel()
+    dw = torch.zeros((int(vocab), D), dtype=torch.float32, device=grad.device)
+    parts = torch.empty((max(1, -(-n // EMBEDDING_BLOCK)) * 2, D), dtype=torch.float32, device=grad.device)
+    rc = lib.mogt_embedding_bwd(g.data_ptr(), g.stride(0), dtype_code(g.dtype, "embedding_bwd"),
+                                sorted_ids.data_ptr(), positions.data_ptr(), n, D, int(vocab), dw.data_ptr(),
+                                parts.data_ptr(), _stream_handle(grad.device))
+    _lib.check(rc, "mogt_embedding_bwd")
+    return dw
+
+
+@_embedding_bwd_op.register_fake
+def _(grad, ids, vocab):
+    return grad.new_empty((int(vocab), grad.shape[-1]), dtype=torch.float32)
+
+
+class _Embedding(torch.autograd.Function):
+    """F.embedding forward; the weight's gradient from mogt_embedding_bwd."""
+
+    @staticmethod
+    def forward(ctx, weight, ids):
+        ctx.save_for_backward(ids)
+        ctx.vocab = weight.shape[0]
+        ctx.wdtype = weight.dtype
+        return F.embedding(ids, weight)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (ids,) = ctx.saved_tensors
+        dw = torch.ops.mogt.embedding_bwd(grad_out, ids, ctx.vocab)
+        return dw.to(ctx.wdtype), None
+
+
+def embedding(ids: torch.Tensor, module: torch.nn.Embedding) -> torch.Tensor:
+    """``module(ids)`` with the weight's gradient summed by the HIP kernel in
+    position order (deterministic, one pass over the gradient rows).  Plain
+    embeddings only (no padding index, norm clipping, frequency scaling or
+    sparse gradients); others go through ``module`` itself."""
+    w = module.weight
+    plain = (module.padding_idx is None and module.max_norm is None and not module.scale_grad_by_freq
+             and not module.sparse)
+    if not (plain and w.is_cuda and w.dim() == 2 and w.shape[1] % 4 == 0 and w.shape[1] <= 4096
+            and w.dtype in (torch.float32, torch.bfloat16)):
+        return module(ids)
+    return _Embedding.apply(w, ids)
 
 
 # backward of the row kernels -------------------------------------------------
