@@ -520,6 +520,8 @@ def _coupled_proj_setup(ctx, inputs, output):
     h, z = output
     ctx.save_for_backward(proj, z, h)
     ctx.args = (int(features), int(rank), bool(gate_prev), float(damping))
+    # the logits output is saved for the backward, not differentiated
+    ctx.set_materialize_grads(False)
 
 
 def _coupled_proj_backward(ctx, grad_h, grad_z):
@@ -529,6 +531,8 @@ def _coupled_proj_backward(ctx, grad_h, grad_z):
     logit term gets the logit gradient summed over time."""
     proj, z, h = ctx.saved_tensors
     features, rank, gate_prev, damping = ctx.args
+    if grad_h is None:
+        return None, None, None, None, None, None
     G = torch.ops.mogt.coupled_scan_rev(z, grad_h, rank, damping)
     dproj, dz = torch.ops.mogt.coupled_proj_grad(G, z, proj, h, features, rank, gate_prev, damping)
     dconst = dz.sum(1) if ctx.needs_input_grad[1] else None
@@ -1144,12 +1148,20 @@ def _add_rmsnorm_setup(ctx, inputs, output):
     ctx.scale = scale
     ctx.eps = eps
     ctx.z_dtype = z.dtype
+    # an unused output gets no gradient tensor (not a materialised zero one)
+    ctx.set_materialize_grads(False)
 
 
 def _add_rmsnorm_backward(ctx, g_xout, g_out):
     x_out, weight = ctx.saved_tensors
     if g_out is None:
-        g_out = torch.zeros_like(x_out)
+        if g_xout is None:
+            return None, None, None, None, None, None
+        # only the residual stream's own gradient: the norm adds nothing
+        dx = g_xout.to(x_out.dtype)
+        dz = (dx * float(ctx.scale)).to(ctx.z_dtype)
+        dw = torch.zeros(x_out.shape[-1], dtype=weight.dtype, device=x_out.device)
+        return dx, dz, None, dw, None, None
     dx, dz, dw = torch.ops.mogt.add_rmsnorm_bwd(x_out, weight, g_out, g_xout, ctx.eps, float(ctx.scale),
                                                 ctx.z_dtype)
     return dx, dz, None, dw.to(weight.dtype), None, None

@@ -76,6 +76,35 @@ def test_add_rmsnorm_backward(gpu, zdt):
     assert max(errs) <= tol, errs
 
 
+@pytest.mark.parametrize("used", ["residual_only", "norm_only"])
+def test_add_rmsnorm_backward_one_output_used(gpu, used):
+    """Only one of (x_out, out) reaches the loss: the other output has no
+    gradient tensor at all (none is materialised), and the gradients still
+    match float64 autograd."""
+    announce(f"add_rmsnorm backward, {used}")
+    from mogt_amd import ops
+
+    g = torch.Generator().manual_seed(19)
+    B, L, D = 1, 200, 768
+    x = torch.randn(B, L, D, generator=g)
+    z = torch.randn(B, L, D, generator=g)
+    w = 1 + 0.2 * torch.randn(D, generator=g)
+    c = torch.randn(B, L, D, generator=g)
+    xt, zt, wt = (t.to(gpu).requires_grad_() for t in (x, z, w))
+    x_out, out = ops.add_rmsnorm(xt, zt, 0.7, wt, 1e-6, out_dtype=torch.float32)
+    ((x_out if used == "residual_only" else out) * c.to(gpu)).sum().backward()
+    torch.cuda.synchronize()
+    x64, z64, w64 = (t.double().requires_grad_() for t in (x, z, w))
+    xo = x64 + 0.7 * z64
+    ((xo if used == "residual_only" else _rms64(xo, w64)) * c.double()).sum().backward()
+    assert rel_err(to_np(xt.grad), x64.grad.numpy()) <= FP32_TOL
+    assert rel_err(to_np(zt.grad), z64.grad.numpy()) <= FP32_TOL
+    if used == "residual_only":
+        assert float(wt.grad.abs().max()) == 0.0
+    else:
+        assert rel_err(to_np(wt.grad), w64.grad.numpy()) <= FP32_TOL
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H", [512, 3072])
 def test_silu_mul_backward(gpu, dtype, H):
