@@ -66,7 +66,11 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, const float (&in)[N
     *reinterpret_cast<Pack<T, N>*>(p) = pk;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// sigmoid(a) = 1 / (1 + 2^(-a log2 e)) on the hardware exponential and
+// reciprocal (v_exp_f32, v_rcp_f32; about 2 ulp): a = -inf gives 0, +inf 1.
+__device__ __forceinline__ float sigmoid_hw(float a) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
+}
 
 // ---------------------------------------------------------------------------
 // Decoupled look-back workspace protocol (shared by every single-pass scan).

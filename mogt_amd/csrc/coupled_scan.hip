@@ -301,7 +301,7 @@ __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* _
         const int64_t base = row * D;
         for (int f = tid; f < nvec; f += CG_THREADS) {
             const int i = f / vpr;
-            const float g_io = IO<TV>::ld(IO<TV>::st(sigmoidf_(z[row * R + i])));
+            const float g_io = IO<TV>::ld(IO<TV>::st(sigmoid_hw(z[row * R + i])));
             float gv[4], vv[4], hv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, o[4];
             load_vec<float, 4>(G + base + 4 * f, gv);
             load_vec<TV, 4>(v + row * ld + 4 * f, vv);
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(CG_THREADS) void coupled_grad_kernel(const float* _
                 sv += s_v[k];
                 sh += s_h[k];
             }
-            const float gg = sigmoidf_(z[row * R + i]);
+            const float gg = sigmoid_hw(z[row * R + i]);
             const float g = (sv - damping * sh) * gg * (1.0f - gg);
             if (dz) dz[row * R + i] = g;
             if constexpr (PROJ) {

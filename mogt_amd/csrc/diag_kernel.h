@@ -99,9 +99,22 @@ __device__ __forceinline__ float row_lanes_sum(float v) {
     return v;
 }
 
+// Waves per SIMD the register allocation must leave room for.  A 768-chunk
+// launch (L = 32768, D = 768 in 512-step, 64-feature chunks) of the 8-wave,
+// 16-step coupled tile with bf16 v is one full generation at three
+// work-groups per CU (six waves per SIMD, <= 80 VGPRs); at the unconstrained
+// 96 VGPRs two fit, and the last third of the chunks runs as a second,
+// half-empty generation.  The larger stashes (bf16 diagonal a and b words;
+// fp32 v; row statistics; projection-fed pre-logits) spill at that budget and
+// measured no faster, so those keep the compiler's choice.
+constexpr int diag_waves_per_simd(int MODE, int S, int WT, bool GPROJ, bool BF16_IN, bool ROWSTAT) {
+    return (MODE == MODE_COUPLED && S == 16 && WT == 8 && BF16_IN && !GPROJ && !ROWSTAT) ? 6 : 1;
+}
+
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
           bool PREFIX, bool ROWSTAT = false, bool GPROJ = false>
-__global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
+__global__ __launch_bounds__(64 * WT) __attribute__((amdgpu_waves_per_eu(diag_waves_per_simd(MODE, S, WT, GPROJ, std::is_same<TIn, bf16_t>::value, ROWSTAT))))
+void diag_scan_kernel(DiagParams p) {
     constexpr int NT = 64 * WT;
     constexpr int Q = 64 / FWL;       // step groups per wave (rows per vector load)
     constexpr int VW = WT * Q;        // "virtual waves": groups of S consecutive steps
@@ -270,7 +283,7 @@ __global__ __launch_bounds__(64 * WT) void diag_scan_kernel(DiagParams p) {
                     p.zout[(row0 + t0 + s) * p.R + gi] = z;
             }
             const bool ok = s < nv;
-            const float gg = sigmoidf_(z);
+            const float gg = sigmoid_hw(z);
             ra[s][0] = ok ? p.damping * (1.0f - gg) : 1.0f;
             if constexpr (COUPLED) {
                 // reference: V_t_raw * value_gate.to(V_t_raw.dtype), U * (1 - value_gate)

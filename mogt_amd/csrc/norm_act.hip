@@ -87,12 +87,6 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_kernel(
     }
 }
 
-// sigmoid(a) = 1 / (1 + 2^(-a log2 e)) on the hardware exponential and
-// reciprocal (v_exp_f32, v_rcp_f32; about 2 ulp): a = -inf gives 0, +inf 1.
-__device__ __forceinline__ float sigmoid_hw(float a) {
-    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a * -1.4426950408889634f));
-}
-
 // The SwiGLU row kernels walk the flattened [rows, H / VEC] vector index with a
 // grid stride; a thread's first (row, column) is one division and later ones
 // advance by the stride's quotient and remainder (no 64-bit division per
