@@ -147,8 +147,9 @@ int mogt_coupled_rank_scan_stats_fwd(const void* z, const void* v, void* h, floa
  * concatenated input.  With row_stats (as in mogt_coupled_rank_scan_stats_fwd)
  * h is written in proj's `dtype`; without (nullable), out_dtype must be fp32
  * (the training path, which normalises h separately).  z_out (nullable, fp32
- * [B, L, R]) receives the assembled logits.  Workspace:
- * mogt_coupled_rank_scan_workspace_bytes.                                 */
+ * [B, L, R]) receives the assembled logits; without it they are kept in the
+ * workspace's last 256-byte-aligned B*L*R*4 bytes.  Workspace:
+ * mogt_coupled_rank_scan_workspace_bytes (which includes that room).      */
 int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj, int64_t gate_col, int gate_prev,
                                     const float* gate_const, void* h, float* row_stats, float* z_out,
                                     int64_t batch, int64_t length, int64_t rank, int64_t channels,

@@ -36,17 +36,54 @@ int coupled_stat_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t 
                      t.vec, t.lanes, t.steps, t.waves);
 }
 
-// Projection-fed gates (GPROJ): v and the gate pre-logits share one dtype T;
-// h in TO; with or without row statistics.
-template <typename T, typename TO, bool STATS>
-int coupled_proj_dispatch(const DiagParams& prm, const DiagTile& t, hipStream_t st) {
-#define MOGT_CASE(V_, F_, S_, W_)                                          \
-    if (t.vec == V_ && t.lanes == F_ && t.steps == S_ && t.waves == W_) \
-        return diag_launch<MODE_COUPLED, T, T, TO, V_, F_, S_, W_, false, STATS, true>(prm, st);
-    MOGT_COUPLED_STAT_TILES(MOGT_CASE)
-#undef MOGT_CASE
-    return set_error(MOGT_E_INVALID, "coupled scan statistics: tile (vec=%d, lanes=%d, steps=%d, waves=%d) not compiled",
-                     t.vec, t.lanes, t.steps, t.waves);
+// Gate logits of the projection-fed scan: row t of the projection P holds the
+// current token's pre-logits from column gate_col (R columns; `pre` points
+// there) and, with gate_prev, the previous-token pre-logits in the next R
+// columns, which belong to step t + 1:
+//   z[b][t][i] = (P[t][gate_col + i] + (gate_prev && t > 0 ? P[t-1][gate_col + R + i] : 0))
+//                + gconst[b][i]
+// (phi_value_gate over [x_t, x_{t-1}, prefix], model_mogt.py:104-122, 170-171,
+// with the bias and prefix terms folded into gconst).  Thread = (row, group of
+// four consecutive logits), 32-bit indexing (the host bounds the count).
+template <typename T>
+__global__ __launch_bounds__(256) void coupled_gate_logits_kernel(const T* __restrict__ pre, int64_t ld,
+                                                                  int gate_prev, const float* __restrict__ gconst,
+                                                                  float* __restrict__ z, uint32_t L, int R,
+                                                                  uint32_t n) {
+    const uint32_t k = blockIdx.x * 256u + threadIdx.x;
+    if (k >= n) return;
+    const uint32_t nq = (static_cast<uint32_t>(R) + 3u) / 4u;
+    const uint32_t row = k / nq;
+    const int i0 = static_cast<int>(k - row * nq) * 4;
+    const uint32_t b = row / L;
+    const bool prev = gate_prev && row - b * L > 0;
+    const T* cur = pre + static_cast<int64_t>(row) * ld;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int i = i0 + e;
+        if (i < R) {
+            float v = IO<T>::ld(cur[i]);
+            if (prev) v = v + IO<T>::ld(cur[R + i - ld]);
+            if (gconst) v = v + gconst[static_cast<int64_t>(b) * R + i];
+            z[static_cast<int64_t>(row) * R + i] = v;
+        }
+    }
+}
+
+template <typename T>
+int coupled_gate_logits(const T* pre, int64_t ld, int gate_prev, const float* gconst, float* z, int64_t B,
+                        int64_t L, int R, hipStream_t st) {
+    const int64_t n = B * L * ((R + 3) / 4);
+    if (n > 0xffffff00LL) return set_error(MOGT_E_INVALID, "projection-fed scan: too many gate logits");
+    const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
+    hipLaunchKernelGGL((coupled_gate_logits_kernel<T>), dim3(blocks), dim3(256), 0, st, pre, ld, gate_prev, gconst,
+                       z, static_cast<uint32_t>(L), R, static_cast<uint32_t>(n));
+    return check_launch("coupled_gate_logits_kernel");
+}
+
+// Workspace bytes of the fp32 gate logits [B, L, R], rounded up to 256.
+size_t coupled_logit_bytes(int64_t B, int64_t L, int64_t R) {
+    return (static_cast<size_t>(B * L * R) * sizeof(float) + 255) & ~static_cast<size_t>(255);
 }
 
 bool dtype_ok(int d) { return d == MOGT_F32 || d == MOGT_BF16; }
@@ -76,20 +113,10 @@ int coupled_alignment(const void* v, const void* h, int v_dtype, int out_dtype) 
 
 }  // namespace
 
-// proj: null, or the projection-fed gate (GPROJ) with z the pre-logit columns
-// of the projection, row stride ldz, and gate_prev / gconst as in DiagParams;
 // ldv: row stride of v (0: R * C).
-struct CoupledProj {
-    int64_t ldz;
-    int gate_prev;
-    const float* gconst;
-    float* zout;
-};
-
 int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int64_t R, int64_t C,
                 float damping, int z_dtype, int v_dtype, int out_dtype, const DiagTile& t,
-                void* ws, size_t ws_bytes, void* stream, float* row_stats = nullptr, int64_t ldv = 0,
-                const CoupledProj* proj = nullptr) {
+                void* ws, size_t ws_bytes, void* stream, float* row_stats = nullptr, int64_t ldv = 0) {
     const int64_t D = R * C;
     if (C % t.vec != 0)
         return set_error(MOGT_E_INVALID, "channels %lld not a multiple of vec %d", (long long)C, t.vec);
@@ -108,23 +135,6 @@ int coupled_run(const void* z, const void* v, void* h, int64_t B, int64_t L, int
     if (ldv) prm.ldv = ldv;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool zb = z_dtype == MOGT_BF16, vb = v_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
-    if (proj) {
-        prm.ldz = proj->ldz;
-        prm.gate_prev = proj->gate_prev;
-        prm.gconst = proj->gconst;
-        prm.zout = proj->zout;
-        if (zb != vb) return set_error(MOGT_E_INVALID, "projection-fed coupled scan: v and gates share a dtype");
-        if (t.vec * t.lanes != 64)
-            return set_error(MOGT_E_INVALID, "projection-fed coupled scan: tile must be 64 features wide");
-        if (row_stats) {
-            if (vb != ob) return set_error(MOGT_E_INVALID, "projection-fed scan with statistics: h in proj's dtype");
-            return vb ? coupled_proj_dispatch<bf16_t, bf16_t, true>(prm, t, st)
-                      : coupled_proj_dispatch<float, float, true>(prm, t, st);
-        }
-        if (ob) return set_error(MOGT_E_INVALID, "projection-fed scan without statistics: h in fp32");
-        return vb ? coupled_proj_dispatch<bf16_t, float, false>(prm, t, st)
-                  : coupled_proj_dispatch<float, float, false>(prm, t, st);
-    }
     if (row_stats) {
         if (zb) return set_error(MOGT_E_INVALID, "coupled scan statistics: gate logits must be fp32");
         if (t.vec * t.lanes != 64)
@@ -158,7 +168,8 @@ extern "C" size_t mogt_coupled_rank_scan_workspace_bytes(int64_t batch, int64_t 
                                        coupled_tile(batch, length, rank, channels, al)).bytes;
         best = n > best ? n : best;
     }
-    return best;
+    // + the projection-fed entry point's assembled gate logits
+    return ((best + 255) & ~static_cast<size_t>(255)) + coupled_logit_bytes(batch, length, rank);
 }
 
 extern "C" int mogt_coupled_rank_scan_fwd(const void* z, const void* v, void* h, int64_t batch,
@@ -219,11 +230,29 @@ extern "C" int mogt_coupled_rank_scan_proj_fwd(const void* proj, int64_t ld_proj
     const int al = coupled_alignment(proj, h, dtype, out_dtype);
     const int vec_ok = ld_proj % 4 == 0 ? al : (ld_proj % 2 == 0 ? (al < 2 ? al : 2) : 1);
     const DiagTile t = coupled_tile(batch, length, rank, channels, vec_ok);
+    // the logits go to z_out, or to the workspace's tail
+    size_t scan_bytes = workspace_bytes;
+    float* z = z_out;
+    if (!z) {
+        const size_t zbytes = coupled_logit_bytes(batch, length, rank);
+        if (!workspace || workspace_bytes < zbytes)
+            return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes cannot hold the %zu bytes of gate logits",
+                             workspace_bytes, zbytes);
+        scan_bytes = (workspace_bytes - zbytes) & ~static_cast<size_t>(255);
+        z = reinterpret_cast<float*>(static_cast<char*>(workspace) + scan_bytes);
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
     const size_t esz = dtype == MOGT_BF16 ? 2 : 4;
-    const CoupledProj pj{ld_proj, gate_prev, gate_const, z_out};
-    return coupled_run(static_cast<const char*>(proj) + gate_col * esz, proj, h, batch, length, rank, channels,
-                       damping, dtype, dtype, out_dtype, t, workspace, workspace_bytes, stream, row_stats, ld_proj,
-                       &pj);
+    const void* pre = static_cast<const char*>(proj) + gate_col * esz;
+    const int R = static_cast<int>(rank);
+    int rc = dtype == MOGT_BF16
+                 ? coupled_gate_logits(static_cast<const bf16_t*>(pre), ld_proj, gate_prev, gate_const, z, batch,
+                                       length, R, st)
+                 : coupled_gate_logits(static_cast<const float*>(pre), ld_proj, gate_prev, gate_const, z, batch,
+                                       length, R, st);
+    if (rc) return rc;
+    return coupled_run(z, proj, h, batch, length, rank, channels, damping, MOGT_F32, dtype, out_dtype, t, workspace,
+                       scan_bytes, stream, row_stats, ld_proj);
 }
 
 // The same with an explicit tile (sweeps and tests): the tile must be one of

@@ -72,10 +72,7 @@ struct DiagParams {
     int64_t plane;      // words per plane
     float* rowstat;     // COUPLED with ROWSTAT: [B, L, n_fg] sums of squares of h
     int64_t ldv;        // COUPLED: row stride of v in elements (D, or wider inside a projection)
-    int64_t ldz;        // GATED: row stride of the gate logits (R), or of the projection (GPROJ)
-    int gate_prev;      // GPROJ: add the previous step's pre-logit (column R + i) when 1
-    const float* gconst;   // GPROJ: [B, R] per-sequence logit term (bias + prefix), or null
-    float* zout;           // GPROJ: [B, L, R] fp32 gate logits as assembled (for the backward), or null
+    int64_t ldz;        // GATED: row stride of the gate logits (R)
 };
 
 constexpr uint32_t ST_NONE = 0u;
@@ -105,15 +102,15 @@ __device__ __forceinline__ float row_lanes_sum(float v) {
 // work-groups per CU (six waves per SIMD, <= 80 VGPRs); at the unconstrained
 // 96 VGPRs two fit, and the last third of the chunks runs as a second,
 // half-empty generation.  The larger stashes (bf16 diagonal a and b words;
-// fp32 v; row statistics; projection-fed pre-logits) spill at that budget and
-// measured no faster, so those keep the compiler's choice.
-constexpr int diag_waves_per_simd(int MODE, int S, int WT, bool GPROJ, bool BF16_IN, bool ROWSTAT) {
-    return (MODE == MODE_COUPLED && S == 16 && WT == 8 && BF16_IN && !GPROJ && !ROWSTAT) ? 6 : 1;
+// fp32 v; row statistics) spill at that budget and measured no faster, so
+// those keep the compiler's choice.
+constexpr int diag_waves_per_simd(int MODE, int S, int WT, bool BF16_IN, bool ROWSTAT) {
+    return (MODE == MODE_COUPLED && S == 16 && WT == 8 && BF16_IN && !ROWSTAT) ? 6 : 1;
 }
 
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX, bool ROWSTAT = false, bool GPROJ = false>
-__global__ __launch_bounds__(64 * WT) __attribute__((amdgpu_waves_per_eu(diag_waves_per_simd(MODE, S, WT, GPROJ, std::is_same<TIn, bf16_t>::value, ROWSTAT))))
+          bool PREFIX, bool ROWSTAT = false>
+__global__ __launch_bounds__(64 * WT) __attribute__((amdgpu_waves_per_eu(diag_waves_per_simd(MODE, S, WT, std::is_same<TIn, bf16_t>::value, ROWSTAT))))
 void diag_scan_kernel(DiagParams p) {
     constexpr int NT = 64 * WT;
     constexpr int Q = 64 / FWL;       // step groups per wave (rows per vector load)
@@ -135,12 +132,6 @@ void diag_scan_kernel(DiagParams p) {
     // statistics of the RMSNorm that reads h (model_mogt.py:240), so h can
     // leave in the GEMM's dtype without a separate normalisation pass
     static_assert(!ROWSTAT || COUPLED, "row statistics are a COUPLED-mode option");
-    // GPROJ: the gate logit of rank i at step t is assembled from a projection
-    // row (the phi_value_gate pre-logits next to phi_val's output in one GEMM):
-    // z = P[t][i] + (gate_prev && t > 0 ? P[t-1][R + i] : 0) + gconst[b][i], the
-    // gate over [x_t, x_{t-1}, prefix] (model_mogt.py:104-122, 170-171) without
-    // the concatenated input or a separate logit tensor
-    static_assert(!GPROJ || COUPLED, "projection-fed gates are a COUPLED-mode option");
 
     __shared__ int s_pending[2];
     __shared__ float s_cwA[VW][FW];   // level-1 summaries, then exclusive prefixes over VW
@@ -208,7 +199,6 @@ void diag_scan_kernel(DiagParams p) {
     constexpr int NA = GATED ? 1 : (BF16_IN ? NWB : VEC);
     float ra[S][NA];      // DIAG fp32: a; DIAG bf16: raw a words; GATED: raw z, then decay
     uint32_t rb[S][NWB];  // raw words of b (DIAG) or v (COUPLED)
-    uint32_t rp[GPROJ ? S : 1];   // GPROJ: raw previous-step pre-logit
     int nv;               // valid steps of this lane (0 .. S)
     int gi = 0;           // GATED: rank (gate index) of this lane's features
     {
@@ -242,13 +232,6 @@ void diag_scan_kernel(DiagParams p) {
                 const int zrel = REV ? ((tw + rel != 0) ? 1 - rel : -rel) : rel;
                 load_raw_cached<sizeof(TZ)>(pz + zrel * p.ldz + gi, zw);
                 ra[s][0] = __uint_as_float(zw[0]);
-                if constexpr (GPROJ) {
-                    // the previous step's row; step 0 of the sequence reads its
-                    // own row (in bounds) and drops the value
-                    const int prel = (tw + rel > 0) ? rel - 1 : rel;
-                    load_raw_cached<sizeof(TZ)>(pz + prel * p.ldz + p.R + gi, zw);
-                    rp[s] = zw[0];
-                }
             } else {
                 uint32_t aw[NA];
                 load_raw<sizeof(TIn) * VEC>(pa + off + ((REV && tw + rel != 0) ? Di : 0), aw);
@@ -265,23 +248,10 @@ void diag_scan_kernel(DiagParams p) {
     // Steps outside the problem become the identity (a = 1, b = 0).  The
     // reverse mode only forms the decay (b is the incoming gradient).
     if constexpr (GATED) {
-        float zc = 0.0f;   // GPROJ: per-sequence logit term
-        if constexpr (GPROJ) {
-            if (p.gconst) zc = p.gconst[static_cast<int64_t>(bi) * p.R + gi];
-        }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const uint32_t zb = __float_as_uint(ra[s][0]);
-            float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
-            if constexpr (GPROJ) {
-                const uint32_t pb = rp[s];
-                const float zp = std::is_same<TZ, bf16_t>::value ? __uint_as_float(pb << 16) : __uint_as_float(pb);
-                const bool has_prev = p.gate_prev && (tw + min(q * S + s, static_cast<int>(p.L - 1 - tw)) > 0);
-                z = (z + (has_prev ? zp : 0.0f)) + zc;
-                // the lane holding a gate's first channel keeps the logit
-                if (p.zout && s < nv && (fbase + flane) % p.C == 0)
-                    p.zout[(row0 + t0 + s) * p.R + gi] = z;
-            }
+            const float z = std::is_same<TZ, bf16_t>::value ? __uint_as_float(zb << 16) : __uint_as_float(zb);
             const bool ok = s < nv;
             const float gg = sigmoid_hw(z);
             ra[s][0] = ok ? p.damping * (1.0f - gg) : 1.0f;
@@ -584,10 +554,10 @@ inline int diag_prepare(DiagParams& prm, int64_t B, int64_t L, int64_t D, const 
 }
 
 template <int MODE, typename TIn, typename TZ, typename TOut, int VEC, int FWL, int S, int WT,
-          bool PREFIX, bool ROWSTAT = false, bool GPROJ = false>
+          bool PREFIX, bool ROWSTAT = false>
 int diag_launch(const DiagParams& prm, hipStream_t stream) {
     const int grid = prm.G * prm.n_ch;
-    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX, ROWSTAT, GPROJ>),
+    hipLaunchKernelGGL((diag_scan_kernel<MODE, TIn, TZ, TOut, VEC, FWL, S, WT, PREFIX, ROWSTAT>),
                        dim3(grid), dim3(64 * WT), 0, stream, prm);
     return check_launch("diag_scan_kernel");
 }
