@@ -276,6 +276,17 @@ def test_coupled_rank_scan_projection_fed(gpu, B, L, r, c, dt, prev, const):
     ref = so.coupled_rank_scan(to_np(z), to_np(v), r, damping=0.995, v_is_bf16=dt == "bf16")
     err = np.abs(to_np(h).astype(np.float64) - ref) / np.max(np.abs(ref))
     assert float(err.max()) <= (BF16_TOL if dt == "bf16" else FP32_TOL)
+    # the training form returns the logits it assembled: the same fp32 sums
+    # in the same order ((current + previous) + constant)
+    # and h is the plain coupled scan of exactly those logits (v read in place
+    # from the projection rows instead of a contiguous copy; the row stride can
+    # select a narrower tile, whose chunking rounds differently)
+    if gc is None or gc.ndim == 2:
+        h3, z3 = torch.ops.mogt.coupled_proj_scan(proj, gc, D, r, prev, 0.995)
+        h4 = ops.coupled_rank_scan(z.contiguous(), v.contiguous(), damping=0.995)
+        torch.cuda.synchronize()
+        assert torch.equal(z3, z)
+        assert rel_err(to_np(h3), to_np(h4)) <= 1e-6
 
 
 @pytest.mark.parametrize("vdt", ["fp32", "bf16"])
