@@ -76,7 +76,8 @@ int mogt_diag_scan_fwd(const void* a, const void* b, void* h, void* a_prefix,
  * per lane, `waves` waves per work-group.  A chunk covers lanes*vec features
  * and steps*waves*64/lanes steps.  The workspace query takes the same tile.
  * mogt_diag_scan_tiles lists the compiled tiles of a family (0: fp32 input,
- * 1: bf16 input, 2: coupled scan) as 4 ints each and returns their count.   */
+ * 1: bf16 input, 2: coupled scan, 3: coupled reverse scan) as 4 ints each and
+ * returns their count.                                                      */
 size_t mogt_diag_scan_workspace_bytes_cfg(int64_t batch, int64_t length, int64_t features,
                                           int vec, int lanes, int steps, int waves);
 int mogt_diag_scan_fwd_cfg(const void* a, const void* b, void* h, void* a_prefix,
@@ -184,11 +185,21 @@ int mogt_coupled_rank_scan_fwd_cfg(const void* z, const void* v, void* h,
  * affine_scan_sequential_backward, affine_scan.py:65-124) for the diagonal
  * U_t = damping (1 - g_t) I of the coupled identity connection
  * (model_mogt.py:166-203).  Workspace:
- * mogt_diag_scan_workspace_bytes(batch, length, rank * channels, MOGT_F32). */
+ * mogt_coupled_rank_scan_rev_workspace_bytes.                             */
+size_t mogt_coupled_rank_scan_rev_workspace_bytes(int64_t batch, int64_t length, int64_t rank,
+                                                  int64_t channels);
 int mogt_coupled_rank_scan_rev_fwd(const void* z, const float* dh, float* G,
                                    int64_t batch, int64_t length, int64_t rank, int64_t channels,
                                    float damping, int z_dtype,
                                    void* workspace, size_t workspace_bytes, void* stream);
+/* mogt_coupled_rank_scan_rev_fwd with an explicit tile, one of
+ * mogt_diag_scan_tiles(3) whose vector divides `channels` (dh and G aligned to
+ * it, up to 16 bytes); for sweeps and tile coverage tests.  Workspace:
+ * mogt_diag_scan_workspace_bytes_cfg(batch, length, rank * channels, tile). */
+int mogt_coupled_rank_scan_rev_fwd_cfg(const void* z, const float* dh, float* G,
+                                       int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                       float damping, int z_dtype, int vec, int lanes, int steps, int waves,
+                                       void* workspace, size_t workspace_bytes, void* stream);
 /* Gradient epilogue of the coupled scan's backward (the autograd of the
  * fused gate + scan; the reference differentiates model_mogt.py:166-203
  * through torch ops): given G (fp32 [B, L, R*C], the reverse scan

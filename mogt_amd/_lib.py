@@ -16,7 +16,7 @@ MOGT_F32 = 0
 MOGT_BF16 = 1
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -80,6 +80,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_void_p, _c_size,
          _c_void_p],
     ),
+    "mogt_coupled_rank_scan_rev_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "mogt_coupled_rank_scan_rev_fwd_cfg": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_void_p, _c_size, _c_void_p]),
     "mogt_coupled_rank_scan_grad": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
                  _c_i64, _c_float, _c_int, _c_void_p]),

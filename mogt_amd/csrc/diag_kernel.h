@@ -569,13 +569,16 @@ int diag_launch(const DiagParams& prm, hipStream_t stream) {
 #define MOGT_DIAG_F32_TILES(X) X(2, 32, 32, 8) X(2, 32, 16, 16) X(2, 32, 16, 8) X(2, 32, 32, 4) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 #define MOGT_DIAG_BF16_TILES(X) X(4, 16, 16, 8) X(4, 16, 16, 16) X(4, 16, 8, 8) X(4, 32, 16, 8) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 #define MOGT_COUPLED_TILES(X) X(4, 16, 8, 16) X(4, 16, 8, 8) X(4, 16, 16, 8) X(4, 16, 16, 16) X(4, 32, 8, 16) X(2, 32, 16, 8) X(2, 32, 16, 16) X(2, 32, 8, 16) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
+// Reverse coupled scan (fp32 dh in, G out): the fp32 reverse tiles plus four
+// channels per lane (the stash is one logit and the dh words per step)
+#define MOGT_COUPLED_REV_TILES(X) X(2, 32, 32, 8) X(2, 32, 32, 4) X(2, 32, 16, 8) X(2, 32, 8, 16) X(4, 16, 16, 8) X(4, 16, 8, 16) X(4, 16, 8, 8) X(1, 64, 32, 16) X(1, 64, 16, 16) X(1, 64, 8, 16)
 
 // Per-family launchers (diag_f32.hip, diag_bf16.hip, coupled_scan.hip).
 int diag_run_f32in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,
                    hipStream_t stream);
 int diag_run_bf16in(const DiagParams& prm, const DiagTile& t, int out_dtype, bool prefix,
                     hipStream_t stream);
-bool diag_tile_compiled(int family, const DiagTile& t);   // family: 0 f32, 1 bf16, 2 coupled
+bool diag_tile_compiled(int family, const DiagTile& t);   // family: 0 f32, 1 bf16, 2 coupled, 3 coupled reverse
 int diag_run_rev(const DiagParams& prm, const DiagTile& t, hipStream_t stream);   // diag_rev.hip
 
 }  // namespace mogt

@@ -12,6 +12,7 @@ bool diag_tile_compiled(int family, const DiagTile& t) {
     if (family == 0) { MOGT_DIAG_F32_TILES(MOGT_MATCH) }
     if (family == 1) { MOGT_DIAG_BF16_TILES(MOGT_MATCH) }
     if (family == 2) { MOGT_COUPLED_TILES(MOGT_MATCH) }
+    if (family == 3) { MOGT_COUPLED_REV_TILES(MOGT_MATCH) }
 #undef MOGT_MATCH
     return false;
 }
@@ -199,11 +200,13 @@ extern "C" int mogt_diag_scan_tiles(int family, int* out, int max_tiles) {
     };
     static const DiagTile b16[] = {MOGT_DIAG_BF16_TILES(MOGT_T)};
     static const DiagTile cpl[] = {MOGT_COUPLED_TILES(MOGT_T)};
+    static const DiagTile crev[] = {MOGT_COUPLED_REV_TILES(MOGT_T)};
 #undef MOGT_T
-    const DiagTile* list = family == 0 ? f32 : family == 1 ? b16 : family == 2 ? cpl : nullptr;
+    const DiagTile* list = family == 0 ? f32 : family == 1 ? b16 : family == 2 ? cpl : family == 3 ? crev : nullptr;
     const int n = family == 0   ? static_cast<int>(sizeof(f32) / sizeof(f32[0]))
                   : family == 1 ? static_cast<int>(sizeof(b16) / sizeof(b16[0]))
                   : family == 2 ? static_cast<int>(sizeof(cpl) / sizeof(cpl[0]))
+                  : family == 3 ? static_cast<int>(sizeof(crev) / sizeof(crev[0]))
                                 : 0;
     for (int i = 0; i < n && i < max_tiles && out; ++i) {
         out[4 * i] = list[i].vec;

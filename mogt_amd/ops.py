@@ -281,7 +281,7 @@ def _coupled_scan_rev_op(z: torch.Tensor, grad_h: torch.Tensor, rank: int, dampi
     g = grad_h.contiguous().to(torch.float32)
     B, L, D = g.shape
     out = torch.empty_like(g)
-    nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, _lib.MOGT_F32)
+    nbytes = lib.mogt_coupled_rank_scan_rev_workspace_bytes(B, L, rank, D // rank)
     ws = workspace(nbytes, g.device)
     rc = lib.mogt_coupled_rank_scan_rev_fwd(z.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, rank, D // rank,
                                             float(damping), dtype_code(z.dtype, "coupled_scan_rev"), ws.data_ptr(),

@@ -44,6 +44,10 @@ def test_workspace_queries_are_host_only(lib):
     assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 2, 32, 16, 16) == n
     assert lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 2, 24, 16, 16) == 256
     assert lib.mogt_coupled_rank_scan_workspace_bytes(1, 1024, 16, 48, _lib.MOGT_BF16) > 256
+    # the coupled reverse scan's query covers its 4-channel default tile
+    rev = lib.mogt_coupled_rank_scan_rev_workspace_bytes(1, 32768, 16, 48)
+    assert rev >= lib.mogt_diag_scan_workspace_bytes_cfg(1, 32768, 768, 4, 16, 8, 8) > 256
+    assert lib.mogt_coupled_rank_scan_rev_workspace_bytes(0, 32768, 16, 48) == 256
 
 
 def test_argument_errors_without_device(lib):
@@ -94,6 +98,8 @@ def test_empty_problems_are_noops_without_device(lib):
         "diag_rev": lambda B, L: lib.mogt_diag_scan_rev_fwd(N, N, N, B, L, 8, N, 0, N),
         "coupled": lambda B, L: lib.mogt_coupled_rank_scan_fwd(N, N, N, B, L, 4, 6, 1.0, 0, 0, 0, N, 0, N),
         "coupled_rev": lambda B, L: lib.mogt_coupled_rank_scan_rev_fwd(N, N, N, B, L, 4, 6, 1.0, 0, N, 0, N),
+        "coupled_rev_cfg": lambda B, L: lib.mogt_coupled_rank_scan_rev_fwd_cfg(N, N, N, B, L, 4, 8, 1.0, 0, 4, 16,
+                                                                                8, 8, N, 0, N),
         "coupled_grad": lambda B, L: lib.mogt_coupled_rank_scan_grad(N, N, N, N, N, N, B, L, 4, 8, 1.0, 0, N),
         "dense": lambda B, L: lib.mogt_affine_scan_fwd(N, N, N, N, B, L, 16, 8, 0, 0, N, 0, N),
         "dense_vk": lambda B, L: lib.mogt_affine_scan_vk_fwd(N, N, N, N, N, B, L, 16, 16, 0, 0, N, 0, N),
@@ -119,7 +125,7 @@ def test_empty_problems_are_noops_without_device(lib):
 
 
 def test_tile_lists(lib):
-    for fam in (0, 1, 2):
+    for fam in (0, 1, 2, 3):
         tiles = _lib.diag_tiles(fam)
         assert tiles, fam
         for vec, lanes, steps, waves in tiles:
@@ -129,11 +135,13 @@ def test_tile_lists(lib):
 
 
 def test_gpu_tile_lists_match_library(lib):
+    from test_gpu_backward import TILES_COUPLED_REV
     from test_gpu_diag_scan import TILES_BF16, TILES_COUPLED, TILES_F32
 
     assert _lib.diag_tiles(0) == TILES_F32
     assert _lib.diag_tiles(1) == TILES_BF16
     assert _lib.diag_tiles(2) == TILES_COUPLED
+    assert _lib.diag_tiles(3) == TILES_COUPLED_REV
 
 
 def test_check_maps_codes_to_python_errors(lib):

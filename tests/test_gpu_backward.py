@@ -173,6 +173,39 @@ def test_coupled_reverse_scan(gpu, B, L, r, c, zdt):
     assert rel_err(to_np(G), ref) <= FP32_TOL
 
 
+TILES_COUPLED_REV = [(2, 32, 32, 8), (2, 32, 32, 4), (2, 32, 16, 8), (2, 32, 8, 16), (4, 16, 16, 8), (4, 16, 8, 16),
+                     (4, 16, 8, 8), (1, 64, 32, 16), (1, 64, 16, 16), (1, 64, 8, 16)]
+
+
+@pytest.mark.parametrize("tile", TILES_COUPLED_REV)
+def test_every_coupled_reverse_tile(gpu, tile):
+    """Every compiled tile of the coupled reverse scan through its tile-override
+    entry point: ragged L, two sequences, 48 channels per gate (divisible by
+    every vector width), bf16 logits for the vector-4 tiles."""
+    announce(f"coupled reverse tile {tile}")
+    from mogt_amd import _lib, ops
+
+    B, L, r, c = 2, 2777, 4, 48
+    rng = np.random.default_rng(sum(tile))
+    z = (rng.standard_normal((B, L, r)) * 2).astype(np.float32)
+    dh = rng.standard_normal((B, L, r * c)).astype(np.float32)
+    zt = torch.from_numpy(z).to(gpu)
+    if tile[0] == 4:
+        zt = zt.bfloat16()
+    dht = torch.from_numpy(dh).to(gpu)
+    G = torch.empty_like(dht)
+    lib = _lib.load()
+    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes_cfg(B, L, r * c, *tile), gpu)
+    rc = lib.mogt_coupled_rank_scan_rev_fwd_cfg(zt.data_ptr(), dht.data_ptr(), G.data_ptr(), B, L, r, c, 0.995,
+                                                ops.dtype_code(zt.dtype, "z"), *tile, ws.data_ptr(), ws.numel(),
+                                                ops._stream_handle(gpu))
+    _lib.check(rc, "mogt_coupled_rank_scan_rev_fwd_cfg")
+    torch.cuda.synchronize()
+    ref = _coupled_rev64(to_np(zt).astype(np.float64), dh, r, 0.995)
+    assert rel_err(to_np(G), ref) <= FP32_TOL
+    assert ops.workspace_faults() == 0
+
+
 @pytest.mark.parametrize("B,L,r,c,dt,prev,with_const", [(2, 200, 4, 8, "fp32", True, True),
                                                         (1, 300, 16, 48, "fp32", True, True),
                                                         (2, 150, 4, 12, "fp32", False, False),
