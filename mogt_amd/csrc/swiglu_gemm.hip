@@ -35,6 +35,8 @@
 // over the 8 XCDs, so block b is renumbered to give each XCD a contiguous run
 // of tiles, walked 8 row blocks at a time, so that one XCD's L2 keeps the x
 // rows of those 8 blocks while it sweeps the weight blocks.
+#include <type_traits>
+
 #include "common.h"
 
 namespace mogt {
@@ -73,6 +75,13 @@ __device__ __forceinline__ float sg_silu(float g) { return g * __builtin_amdgcn_
 // two fp32 values as one word of two bf16 (round to nearest even)
 __device__ __forceinline__ uint32_t sg_pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((sg_f32x2{lo, hi}), sg_bf16x2));
+}
+
+// lo and hi rounded to bf16 (nearest even) with one conversion, back as fp32
+__device__ __forceinline__ void sg_round2(float lo, float hi, float& rlo, float& rhi) {
+    const uint32_t w = sg_pack(lo, hi);
+    rlo = __uint_as_float(w << 16);
+    rhi = __uint_as_float(w & 0xffff0000u);
 }
 
 // 64 lanes x 16 bytes from (rsrc, voff + soff) into LDS at lds .. lds + 1023
@@ -161,13 +170,12 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     const int wrow0 = SG_OPB + (wn * 64 + l32) * SG_ROWB;
     const int swz = ((l32 >> 1) ^ (l32 >> 2)) & 3;
 
-    sg_f32x16 acc[4][4];   // [weight tile][x tile]
+    // [weight tile][x tile]; the first K-step's MFMAs take a zero accumulator
+    // operand instead of 256 register clears
+    sg_f32x16 acc[4][4];
+    sg_f32x16 zero;
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+    for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
 
     // Fragments of a whole stage (2 K-steps: 4 x and 4 weight fragments each)
     // are read into registers one stage ahead, so the MFMAs never wait on LDS.
@@ -191,19 +199,22 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
 #pragma unroll
         for (int f = 0; f < 8; ++f) f1[f] = *frag_ptr(st, 1, f);
     };
-    auto mfma_half = [&](const sg_bf16x8 (&f)[8]) {
+    auto mfma_half = [&](const sg_bf16x8 (&f)[8], auto first) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[4 + j], f[i], acc[j][i], 0, 0, 0);
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[4 + j], f[i], first ? zero : acc[j][i], 0, 0,
+                                                                    0);
     };
+    constexpr std::true_type FIRST{};
+    constexpr std::false_type LATER{};
     // One stage with every later stage present: the second K-step's 16 MFMAs
     // (fragments `cur`) are interleaved one to one with the 8 loads of stage
     // s + 3 and the 16 fragment reads of stage s + 1 (first K-step into a,
     // free since the first half, then the second K-step into `next`).
-    auto steady = [&](int s, const sg_bf16x8 (&cur)[8], sg_bf16x8 (&next)[8]) {
-        mfma_half(a);
+    auto steady = [&](int s, const sg_bf16x8 (&cur)[8], sg_bf16x8 (&next)[8], auto first) {
+        mfma_half(a, first);
         __builtin_amdgcn_sched_barrier(0);
         sg_wait_vm<8>();
         __syncthreads();
@@ -239,19 +250,30 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     __syncthreads();
     read_stage(0, a, b);
     int s = 0;
+    if (nk > 4) {   // stage 0's first K-step starts the accumulators
+        steady(0, b, c, FIRST);
+        steady(1, c, b, LATER);
+        s = 2;
+    }
     for (; s + 4 < nk; s += 2) {
-        steady(s, b, c);
-        steady(s + 1, c, b);
+        steady(s, b, c, LATER);
+        steady(s + 1, c, b, LATER);
     }
     if (s + 3 < nk) {
-        steady(s, b, c);
+        if (s == 0)
+            steady(s, b, c, FIRST);
+        else
+            steady(s, b, c, LATER);
 #pragma unroll
         for (int f = 0; f < 8; ++f) b[f] = c[f];
         ++s;
     }
     // the last (up to) three stages
     for (; s < nk; ++s) {
-        mfma_half(a);
+        if (s == 0)
+            mfma_half(a, FIRST);
+        else
+            mfma_half(a, LATER);
         __builtin_amdgcn_sched_barrier(0);
         if (s + 1 < nk) {
             if (s + 2 < nk)
@@ -262,7 +284,7 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
             read_stage(s + 1, a, c);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfma_half(b);
+        mfma_half(b, LATER);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int f = 0; f < 8; ++f) b[f] = c[f];
@@ -279,12 +301,15 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                float o[4];
+                // roundings to bf16 two values per conversion
+                float g[4], u[4], sg[4], o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float g = round_bf16(acc[j][i][4 * q + e]);
-                    const float u = round_bf16(acc[j + 2][i][4 * q + e]);
-                    o[e] = round_bf16(sg_silu(g)) * u;
+                for (int e = 0; e < 4; e += 2) {
+                    sg_round2(acc[j][i][4 * q + e], acc[j][i][4 * q + e + 1], g[e], g[e + 1]);
+                    sg_round2(acc[j + 2][i][4 * q + e], acc[j + 2][i][4 * q + e + 1], u[e], u[e + 1]);
+                    sg_round2(sg_silu(g[e]), sg_silu(g[e + 1]), sg[e], sg[e + 1]);
+                    o[e] = sg[e] * u[e];
+                    o[e + 1] = sg[e + 1] * u[e + 1];
                 }
                 const sg_u32x2 w = {sg_pack(o[0], o[1]), sg_pack(o[2], o[3])};
                 const int col = n0 + wn * 64 + 32 * j + 8 * q + 4 * hb;
