@@ -341,10 +341,14 @@ int mogt_silu_mul_bwd(const void* y, const void* dout, void* dy, int64_t rows, i
  * summed in position order (deterministic).  The caller sorts the
  * n token ids stably (sorted_ids, int64) with the positions in that order
  * (positions, int64), zero-fills dweight (fp32 [vocab, dim]) and passes
- * partials: fp32 [ceil(n / 16) * 2, dim] scratch.  grad: [n, dim] rows with
- * stride ld_grad, fp32 or bf16; dim % 4 == 0, <= 4096.  Ids outside
- * [0, vocab) are skipped.                                                    */
-int mogt_embedding_bwd(const void* grad, int64_t ld_grad, int grad_dtype, const int64_t* sorted_ids,
+ * partials: fp32 [ceil(n / 16) * 2, dim] scratch.  Position p < n_first is
+ * row p of grad (row stride ld_grad), position p >= n_first row p - n_first
+ * of grad2 (stride ld_grad2; nullable when n_first = n): two lookups into one
+ * table (the tokens and the prefix-condition rows) share one dweight.  fp32
+ * or bf16 rows; dim % 4 == 0, <= 4096.  Ids outside [0, vocab) are
+ * skipped.                                                                 */
+int mogt_embedding_bwd(const void* grad, int64_t ld_grad, const void* grad2, int64_t ld_grad2,
+                       int64_t n_first, int grad_dtype, const int64_t* sorted_ids,
                        const int64_t* positions, int64_t n, int64_t dim, int64_t vocab, float* dweight,
                        float* partials, void* stream);
 

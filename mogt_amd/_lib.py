@@ -16,7 +16,7 @@ MOGT_F32 = 0
 MOGT_BF16 = 1
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -128,8 +128,8 @@ SIGNATURES: dict[str, tuple] = {
                  _c_int, _c_int, _c_int, _c_void_p, _c_float, _c_int, _c_void_p]),
     "mogt_silu_mul_bwd": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p]),
     "mogt_embedding_bwd": (
-        _c_int, [_c_void_p, _c_i64, _c_int, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_void_p, _c_void_p,
-                 _c_void_p]),
+        _c_int, [_c_void_p, _c_i64, _c_void_p, _c_i64, _c_i64, _c_int, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64,
+                 _c_void_p, _c_void_p, _c_void_p]),
     "mogt_connection_map_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_i64, _c_i64, _c_float, _c_float, _c_int, _c_int, _c_void_p]),
     "mogt_lm_ce_fwd": (

@@ -4,7 +4,9 @@
 //
 // The caller sorts the token ids stably (positions of equal ids keep their
 // order), passes the sorted ids and the positions in that order, and
-// zero-fills dW.  Pass 1: one wave per block of EB consecutive sorted
+// zero-fills dW.  Positions below n1 are rows of the first gradient, the rest
+// rows of a second one (a second lookup into the same table, whose gradient
+// then needs no table of its own).  Pass 1: one wave per block of EB consecutive sorted
 // positions walks them, summing the gradient rows of each run of equal ids: a
 // run that begins and ends inside the block is written to dW directly; the
 // piece of a run that began in an earlier block goes to the block's slot 0;
@@ -23,7 +25,8 @@ constexpr int EMB_WAVES = 4;  // waves (blocks) per work-group
 
 template <typename TG, int VPL>
 __global__ __launch_bounds__(64 * EMB_WAVES) void emb_bwd_blocks(const TG* __restrict__ g, int64_t ldg,
-                                                                 const int64_t* __restrict__ sid,
+                                                                 const TG* __restrict__ g2, int64_t ldg2,
+                                                                 int64_t n1, const int64_t* __restrict__ sid,
                                                                  const int64_t* __restrict__ perm, int64_t n,
                                                                  int D, int64_t V, float* __restrict__ dw,
                                                                  float* __restrict__ part) {
@@ -41,12 +44,13 @@ __global__ __launch_bounds__(64 * EMB_WAVES) void emb_bwd_blocks(const TG* __res
     for (int64_t i = i0; i < i1; ++i) {
         const int64_t id = sid[i];
         const int64_t row = perm[i];
+        const TG* src = row < n1 ? g + row * ldg : g2 + (row - n1) * ldg2;
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int c = (k * 64 + lane) * 4;
             if (c < D) {
                 float v[4];
-                load_vec<TG, 4>(g + row * ldg + c, v);
+                load_vec<TG, 4>(src + c, v);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[k][e] += v[e];
             }
@@ -120,16 +124,16 @@ __global__ __launch_bounds__(64 * EMB_WAVES) void emb_bwd_runs(const int64_t* __
 }
 
 template <typename TG>
-int emb_bwd_launch(const TG* g, int64_t ldg, const int64_t* sid, const int64_t* perm, int64_t n, int D, int64_t V,
-                   float* dw, float* part, hipStream_t st) {
+int emb_bwd_launch(const TG* g, int64_t ldg, const TG* g2, int64_t ldg2, int64_t n1, const int64_t* sid,
+                   const int64_t* perm, int64_t n, int D, int64_t V, float* dw, float* part, hipStream_t st) {
     const int64_t blocks = (n + EB - 1) / EB;
     const dim3 grid(static_cast<unsigned>((blocks + EMB_WAVES - 1) / EMB_WAVES));
     const dim3 block(64 * EMB_WAVES);
     const int vpl = (D + 255) / 256;
 #define MOGT_EMB_CASE(VP)                                                                              \
     if (vpl <= VP) {                                                                                   \
-        hipLaunchKernelGGL((emb_bwd_blocks<TG, VP>), grid, block, 0, st, g, ldg, sid, perm, n, D, V, dw, \
-                           part);                                                                      \
+        hipLaunchKernelGGL((emb_bwd_blocks<TG, VP>), grid, block, 0, st, g, ldg, g2, ldg2, n1, sid, perm, n, D, \
+                           V, dw, part);                                                               \
         int rc = check_launch("emb_bwd_blocks");                                                       \
         if (rc) return rc;                                                                             \
         hipLaunchKernelGGL((emb_bwd_runs<VP>), grid, block, 0, st, sid, n, D, V, part, dw);             \
@@ -150,29 +154,32 @@ int emb_bwd_launch(const TG* g, int64_t ldg, const int64_t* sid, const int64_t* 
 
 using namespace mogt;
 
-extern "C" int mogt_embedding_bwd(const void* grad, int64_t ld_grad, int grad_dtype, const int64_t* sorted_ids,
+extern "C" int mogt_embedding_bwd(const void* grad, int64_t ld_grad, const void* grad2, int64_t ld_grad2,
+                                  int64_t n_first, int grad_dtype, const int64_t* sorted_ids,
                                   const int64_t* positions, int64_t n, int64_t dim, int64_t vocab, float* dweight,
                                   float* partials, void* stream) {
     clear_error();
     if (n < 0 || dim <= 0 || vocab <= 0) return set_error(MOGT_E_INVALID, "embedding_bwd: bad shape");
     if (dim % 4 != 0 || dim > 4096)
         return set_error(MOGT_E_INVALID, "embedding_bwd: row length must be a multiple of 4 and <= 4096");
-    if (ld_grad < dim || ld_grad % 4 != 0)
+    if (n_first < 0 || n_first > n || (!grad2 && n_first != n))
+        return set_error(MOGT_E_INVALID, "embedding_bwd: n_first must be in [0, n], and n without a second gradient");
+    if (ld_grad < dim || ld_grad % 4 != 0 || (grad2 && (ld_grad2 < dim || ld_grad2 % 4 != 0)))
         return set_error(MOGT_E_INVALID, "embedding_bwd: gradient row stride must cover the row (multiple of 4)");
     if (grad_dtype != MOGT_F32 && grad_dtype != MOGT_BF16)
         return set_error(MOGT_E_INVALID, "embedding_bwd: unsupported gradient dtype");
     if (n == 0) return MOGT_OK;
-    if (!grad || !sorted_ids || !positions || !dweight || !partials)
+    if ((n_first > 0 && !grad) || !sorted_ids || !positions || !dweight || !partials)
         return set_error(MOGT_E_INVALID, "embedding_bwd: null pointer");
     const size_t esz = grad_dtype == MOGT_BF16 ? 2 : 4;
-    if ((reinterpret_cast<uintptr_t>(grad) % (4 * esz)) || (reinterpret_cast<uintptr_t>(dweight) % 16) ||
-        (reinterpret_cast<uintptr_t>(partials) % 16))
+    if ((reinterpret_cast<uintptr_t>(grad) % (4 * esz)) || (reinterpret_cast<uintptr_t>(grad2) % (4 * esz)) ||
+        (reinterpret_cast<uintptr_t>(dweight) % 16) || (reinterpret_cast<uintptr_t>(partials) % 16))
         return set_error(MOGT_E_INVALID, "embedding_bwd: gradient, dweight and partials need vector alignment");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int D = static_cast<int>(dim);
     if (grad_dtype == MOGT_BF16)
-        return emb_bwd_launch<bf16_t>(static_cast<const bf16_t*>(grad), ld_grad, sorted_ids, positions, n, D, vocab,
-                                      dweight, partials, st);
-    return emb_bwd_launch<float>(static_cast<const float*>(grad), ld_grad, sorted_ids, positions, n, D, vocab, dweight,
-                                 partials, st);
+        return emb_bwd_launch<bf16_t>(static_cast<const bf16_t*>(grad), ld_grad, static_cast<const bf16_t*>(grad2),
+                                      ld_grad2, n_first, sorted_ids, positions, n, D, vocab, dweight, partials, st);
+    return emb_bwd_launch<float>(static_cast<const float*>(grad), ld_grad, static_cast<const float*>(grad2), ld_grad2,
+                                 n_first, sorted_ids, positions, n, D, vocab, dweight, partials, st);
 }

@@ -566,14 +566,18 @@ class MOGTModel(_WeightCacheOwner):
         return index % max(1, int(getattr(self, "checkpoint_every_n", 1))) == 0
 
     def forward(self, input_ids):
-        h = ops.embedding(input_ids, self.embedding)
-        chain_fused = (h.dtype == torch.float32 and len(self.blocks) > 0 and not self._checkpointed(0)
-                       and all(blk.fused_path_ok() for blk in self.blocks))
-        cond = self._prefix_condition(h)
-        if chain_fused and cond is not None and torch.is_grad_enabled():
-            # the same row looked up again: its gradient goes to the embedding
-            # table directly instead of through a full-size slice of h
-            cond = ops.embedding(input_ids[:, int(self.prefix_condition_position)], self.embedding)
+        chain_fused = (self.embedding.weight.dtype == torch.float32 and len(self.blocks) > 0
+                       and not self._checkpointed(0) and all(blk.fused_path_ok() for blk in self.blocks))
+        pos = getattr(self, "prefix_condition_position", None)
+        if (chain_fused and torch.is_grad_enabled() and pos is not None
+                and -input_ids.size(1) <= int(pos) < input_ids.size(1)):
+            # the prefix row looked up again alongside the tokens: its gradient
+            # joins the tokens' in one table instead of flowing through a
+            # full-size slice of h (or a second table)
+            h, cond = ops.embedding_pair(input_ids, input_ids[:, int(pos)], self.embedding)
+        else:
+            h = ops.embedding(input_ids, self.embedding)
+            cond = self._prefix_condition(h)
         if chain_fused:
             # each block hands its FFN term to the next block's first RMSNorm;
             # the last one is added inside norm_f

@@ -1010,19 +1010,34 @@ def swiglu_gate(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> to
 EMBEDDING_BLOCK = 16   # sorted positions per block of mogt_embedding_bwd
 
 
-@torch.library.custom_op("mogt::embedding_bwd", mutates_args=())
-def _embedding_bwd_op(grad: torch.Tensor, ids: torch.Tensor, vocab: int) -> torch.Tensor:
-    lib = _lib.load()
-    D = grad.shape[-1]
+def _rows_for_embedding_bwd(grad: torch.Tensor, D: int) -> torch.Tensor:
     g = grad.reshape(-1, D)
     if g.stride(-1) != 1 or g.stride(0) % 4 != 0 or g.data_ptr() % 16 != 0:
         g = g.contiguous()
+    return g
+
+
+@torch.library.custom_op("mogt::embedding_bwd", mutates_args=())
+def _embedding_bwd_op(grad: torch.Tensor, ids: torch.Tensor, vocab: int, grad2: torch.Tensor | None = None,
+                      ids2: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [vocab, D] gradient of the table from the rows of ``grad`` at
+    ``ids`` and, optionally, those of ``grad2`` at ``ids2`` (a second lookup
+    into the same table), summed per id in position order."""
+    lib = _lib.load()
+    D = grad.shape[-1]
+    g = _rows_for_embedding_bwd(grad, D)
     flat = ids.reshape(-1).to(torch.int64)
+    n1 = flat.numel()
+    g2 = None
+    if grad2 is not None:
+        g2 = _rows_for_embedding_bwd(grad2.to(g.dtype), D)
+        flat = torch.cat([flat, ids2.reshape(-1).to(torch.int64)])
     sorted_ids, positions = torch.sort(flat, stable=True)
     n = flat.numel()
     dw = torch.zeros((int(vocab), D), dtype=torch.float32, device=grad.device)
     parts = torch.empty((max(1, -(-n // EMBEDDING_BLOCK)) * 2, D), dtype=torch.float32, device=grad.device)
-    rc = lib.mogt_embedding_bwd(g.data_ptr(), g.stride(0), dtype_code(g.dtype, "embedding_bwd"),
+    rc = lib.mogt_embedding_bwd(g.data_ptr(), g.stride(0), g2.data_ptr() if g2 is not None else None,
+                                g2.stride(0) if g2 is not None else 0, n1, dtype_code(g.dtype, "embedding_bwd"),
                                 sorted_ids.data_ptr(), positions.data_ptr(), n, D, int(vocab), dw.data_ptr(),
                                 parts.data_ptr(), _stream_handle(grad.device))
     _lib.check(rc, "mogt_embedding_bwd")
@@ -1030,25 +1045,52 @@ def _embedding_bwd_op(grad: torch.Tensor, ids: torch.Tensor, vocab: int) -> torc
 
 
 @_embedding_bwd_op.register_fake
-def _(grad, ids, vocab):
+def _(grad, ids, vocab, grad2=None, ids2=None):
     return grad.new_empty((int(vocab), grad.shape[-1]), dtype=torch.float32)
 
 
 class _Embedding(torch.autograd.Function):
-    """F.embedding forward; the weight's gradient from mogt_embedding_bwd."""
+    """F.embedding forward (one or two lookups into the same table); the
+    weight's gradient from mogt_embedding_bwd, one table for both lookups."""
 
     @staticmethod
-    def forward(ctx, weight, ids):
-        ctx.save_for_backward(ids)
+    def forward(ctx, weight, ids, ids2=None):
+        ctx.save_for_backward(ids, ids2)
         ctx.vocab = weight.shape[0]
         ctx.wdtype = weight.dtype
-        return F.embedding(ids, weight)
+        if ids2 is None:
+            return F.embedding(ids, weight)
+        return F.embedding(ids, weight), F.embedding(ids2, weight)
 
     @staticmethod
-    def backward(ctx, grad_out):
-        (ids,) = ctx.saved_tensors
-        dw = torch.ops.mogt.embedding_bwd(grad_out, ids, ctx.vocab)
-        return dw.to(ctx.wdtype), None
+    def backward(ctx, grad_out, grad_out2=None):
+        ids, ids2 = ctx.saved_tensors
+        if grad_out is None:
+            grad_out, ids = grad_out2, ids2
+            grad_out2 = None
+        if grad_out is None:
+            return None, None, None
+        dw = torch.ops.mogt.embedding_bwd(grad_out, ids, ctx.vocab, grad_out2, ids2 if grad_out2 is not None else None)
+        return dw.to(ctx.wdtype), None, None
+
+
+def _plain_embedding(module: torch.nn.Embedding) -> bool:
+    w = module.weight
+    plain = (module.padding_idx is None and module.max_norm is None and not module.scale_grad_by_freq
+             and not module.sparse)
+    return (plain and w.is_cuda and w.dim() == 2 and w.shape[1] % 4 == 0 and w.shape[1] <= 4096
+            and w.dtype in (torch.float32, torch.bfloat16))
+
+
+def embedding_pair(ids: torch.Tensor, ids2: torch.Tensor,
+                   module: torch.nn.Embedding) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(module(ids), module(ids2))`` whose backward writes one gradient table
+    for both lookups (the second lookup's rows join the first's in the same
+    position-ordered sums) instead of a full-size table per lookup and their
+    sum."""
+    if not _plain_embedding(module):
+        return module(ids), module(ids2)
+    return _Embedding.apply(module.weight, ids, ids2)
 
 
 def embedding(ids: torch.Tensor, module: torch.nn.Embedding) -> torch.Tensor:
@@ -1056,13 +1098,9 @@ def embedding(ids: torch.Tensor, module: torch.nn.Embedding) -> torch.Tensor:
     position order (deterministic, one pass over the gradient rows).  Plain
     embeddings only (no padding index, norm clipping, frequency scaling or
     sparse gradients); others go through ``module`` itself."""
-    w = module.weight
-    plain = (module.padding_idx is None and module.max_norm is None and not module.scale_grad_by_freq
-             and not module.sparse)
-    if not (plain and w.is_cuda and w.dim() == 2 and w.shape[1] % 4 == 0 and w.shape[1] <= 4096
-            and w.dtype in (torch.float32, torch.bfloat16)):
+    if not _plain_embedding(module):
         return module(ids)
-    return _Embedding.apply(w, ids)
+    return _Embedding.apply(module.weight, ids)
 
 
 # backward of the row kernels -------------------------------------------------

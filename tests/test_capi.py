@@ -82,10 +82,14 @@ def test_argument_errors_without_device(lib):
     assert rc == -1 and b"align" in lib.mogt_last_error()
     assert lib.mogt_swiglu_gate_fwd(None, None, None, None, 0, 64, 128, 64, 128, 1, None) == 0
     # embedding backward: row length, stride and dtype checks before any launch
-    assert lib.mogt_embedding_bwd(16, 64, 0, 16, 16, 4, 6, 10, 16, 16, None) == -1
-    assert lib.mogt_embedding_bwd(16, 32, 0, 16, 16, 4, 64, 10, 16, 16, None) == -1
-    assert lib.mogt_embedding_bwd(16, 64, 5, 16, 16, 4, 64, 10, 16, 16, None) == -1
-    rc = lib.mogt_embedding_bwd(8, 64, 0, 16, 16, 4, 64, 10, 16, 16, None)
+    assert lib.mogt_embedding_bwd(16, 64, None, 0, 4, 0, 16, 16, 4, 6, 10, 16, 16, None) == -1
+    assert lib.mogt_embedding_bwd(16, 32, None, 0, 4, 0, 16, 16, 4, 64, 10, 16, 16, None) == -1
+    assert lib.mogt_embedding_bwd(16, 64, None, 0, 4, 5, 16, 16, 4, 64, 10, 16, 16, None) == -1
+    # a second gradient source: n_first within [0, n] (n without one), its stride
+    rc = lib.mogt_embedding_bwd(16, 64, None, 0, 3, 0, 16, 16, 4, 64, 10, 16, 16, None)
+    assert rc == -1 and b"n_first" in lib.mogt_last_error()
+    assert lib.mogt_embedding_bwd(16, 64, 16, 32, 2, 0, 16, 16, 4, 64, 10, 16, 16, None) == -1
+    rc = lib.mogt_embedding_bwd(8, 64, None, 0, 4, 0, 16, 16, 4, 64, 10, 16, 16, None)
     assert rc == -1 and b"align" in lib.mogt_last_error()
 
 
@@ -118,7 +122,7 @@ def test_empty_problems_are_noops_without_device(lib):
         "silu_mul_bwd": lambda: lib.mogt_silu_mul_bwd(N, N, N, 0, 64, 0, N),
         "connection_map": lambda: lib.mogt_connection_map_fwd(N, N, 0, 16, 1.0, 1.0, 0, 0, N),
         "lm_ce_bwd": lambda: lib.mogt_lm_ce_bwd(N, 32, 0, N, N, 0, 32, -100, N, N, 32, 0, N),
-        "embedding_bwd": lambda: lib.mogt_embedding_bwd(N, 64, 0, N, N, 0, 64, 10, N, N, N),
+        "embedding_bwd": lambda: lib.mogt_embedding_bwd(N, 64, N, 0, 0, 0, N, N, 0, 64, 10, N, N, N),
     }
     for name, call in rows.items():
         assert call() == 0, (name, lib.mogt_last_error())

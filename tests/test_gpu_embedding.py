@@ -61,6 +61,49 @@ def test_embedding_backward_matches_float64(gpu, kind, n, vocab, D, dt):
     assert torch.equal(dw, dw2), "two runs differ"
 
 
+@pytest.mark.parametrize("n,n2,vocab,D,dt", [(32768, 1, 32000, 768, torch.float32), (1000, 7, 50, 768, torch.float32),
+                                             (300, 300, 20, 64, torch.bfloat16), (5, 0, 9, 4, torch.float32)])
+def test_embedding_backward_two_sources(gpu, n, n2, vocab, D, dt):
+    """A second lookup into the same table (the prefix-condition rows): one
+    table holds both lookups' gradients, against float64."""
+    announce(f"embedding backward two sources n={n}+{n2} V={vocab} D={D} {dt}")
+    from mogt_amd import ops  # noqa: F401  (registers the ops)
+
+    gen = torch.Generator().manual_seed(n + n2 + vocab)
+    ids = torch.randint(0, vocab, (n,), generator=gen)
+    ids2 = torch.randint(0, vocab, (n2,), generator=gen)
+    grad = torch.randn(n, D, generator=gen).to(dt)
+    grad2 = torch.randn(n2, D, generator=gen).to(dt)
+    dw = torch.ops.mogt.embedding_bwd(grad.to(gpu), ids.to(gpu), vocab, grad2.to(gpu), ids2.to(gpu))
+    dw_again = torch.ops.mogt.embedding_bwd(grad.to(gpu), ids.to(gpu), vocab, grad2.to(gpu), ids2.to(gpu))
+    torch.cuda.synchronize()
+    ref = _ref(grad, ids, vocab) + _ref(grad2, ids2, vocab)
+    assert rel_err(to_np(dw), ref) <= FP32_TOL
+    assert torch.equal(dw, dw_again), "two runs differ"
+
+
+def test_embedding_pair_gradient_matches_torch(gpu):
+    """ops.embedding_pair: the same outputs as two lookups through the module,
+    and the weight's gradient of both equal to torch's own backward."""
+    announce("embedding pair module gradient")
+    from mogt_amd import ops
+
+    torch.manual_seed(5)
+    emb = torch.nn.Embedding(700, 256).to(gpu)
+    ids = torch.randint(0, 700, (2, 3000), device=gpu)
+    w1 = torch.randn(2, 3000, 256, device=gpu)
+    w2 = torch.randn(2, 256, device=gpu)
+    out, out2 = ops.embedding_pair(ids, ids[:, 1], emb)
+    ((out * w1).sum() + (out2 * w2).sum()).backward()
+    ours = emb.weight.grad.clone()
+    emb.weight.grad = None
+    r1, r2 = F.embedding(ids, emb.weight), F.embedding(ids[:, 1], emb.weight)
+    ((r1 * w1).sum() + (r2 * w2).sum()).backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out, r1) and torch.equal(out2, r2)
+    assert rel_err(to_np(ours), to_np(emb.weight.grad)) <= FP32_TOL
+
+
 def test_embedding_module_gradient_matches_torch(gpu):
     """ops.embedding on an nn.Embedding: same output as the module, the
     weight's gradient equal to torch's own backward to fp32 rounding."""
