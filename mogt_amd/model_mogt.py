@@ -127,6 +127,11 @@ class SwiGLU(nn.Module):
                            lambda: torch.cat([self.w1.weight, self.w2.weight], dim=0))
         return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
 
+    def forward_with(self, x, w12, w3):
+        """The differentiable path on operands the caller built: ``w12`` =
+        [w1; w2] and ``w3`` in the GEMM dtype."""
+        return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
+
 
 def reference_ffn_hidden(d_model: int) -> int:
     """256 * ceil((8 d / 3) / 256) -- model_mogt.py:66-68 (2048 at d = 768)."""
@@ -417,24 +422,31 @@ class MOGTBlock(_WeightCacheOwner):
         return w_pref, gate.bias
 
     def _value_and_gate_projection(self, xn: torch.Tensor, prefix_condition: torch.Tensor | None,
-                                   const: torch.Tensor | None = None, const_given: bool = False):
+                                   const: torch.Tensor | None = None, const_given: bool = False,
+                                   packed: dict | None = None):
         """One GEMM of x against [phi_val; W_cur; W_prev]: v and the value gate's
         pre-logits for the current and the previous token side by side, plus
         the per-sequence logit term (bias + prefix term, fp32 [B, r] or [r]),
-        unless the caller passes it (``const_given``).  Returns (proj,
+        unless the caller passes it (``const_given``).  ``packed``: phi_val's
+        and the gate's weights already in the GEMM dtype.  Returns (proj,
         has_prev, const)."""
         gate: nn.Linear = self.phi_value_gate
         parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
         D = self.d_model
-        W = gate.weight
+        W = packed["gate"] if packed is not None else gate.weight
         if W.shape[1] != len(parts) * D:
             raise RuntimeError(f"phi_value_gate takes {W.shape[1]} inputs, the gate input mode builds "
                                f"{len(parts) * D}")
         # column blocks as views whose backward is one stack (not one zero
         # fill and copy per sliced block)
         cols = dict(zip(parts, W.view(W.shape[0], len(parts), D).unbind(1)))
-        stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
-        W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W), lambda: torch.cat(stacked, dim=0))
+        if packed is not None:
+            stacked = [packed["phi_val"], cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
+            W_all = torch.cat(stacked, dim=0)
+        else:
+            stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
+            W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W),
+                                 lambda: torch.cat(stacked, dim=0))
         proj = F.linear(xn, W_all)
         if const_given:
             return proj, "prev" in cols, const
@@ -463,7 +475,7 @@ class MOGTBlock(_WeightCacheOwner):
         return ops.add_rmsnorm_rowscale(x, Zr, stats, self._residual_scale(Zr), self.norm_ffn.weight,
                                         stat_eps=self.norm_out.eps, eps=self.norm_ffn.eps, out_dtype=gemm_dtype)
 
-    def _mixer_training(self, x, xn, prefix_condition, damping: float, gemm_dtype):
+    def _mixer_training(self, x, xn, prefix_condition, damping: float, gemm_dtype, packed: dict | None = None):
         """Mixer of the fused path under autograd: every kernel has its backward.
         Where the row layout allows, the scan is fed by the one projection GEMM
         of the inference path, so the backward's epilogue writes the
@@ -472,7 +484,7 @@ class MOGTBlock(_WeightCacheOwner):
         parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
         if ops.coupled_proj_scan_supported(self.d_model, self.r, "prev" in parts):
             with torch.autograd.profiler.record_function("mogt.affine_scan"):
-                proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition)
+                proj, gate_prev, gconst = self._value_and_gate_projection(xn, prefix_condition, packed=packed)
                 if gconst is not None:
                     gconst = gconst.expand(xn.size(0), self.r).contiguous()
                 h = ops.coupled_proj_scan(proj, self.d_model, rank=self.r, gate_prev=gate_prev, gate_const=gconst,
@@ -486,17 +498,39 @@ class MOGTBlock(_WeightCacheOwner):
                 h = ops.coupled_rank_scan(z, v_raw, damping=damping, out_dtype=torch.float32)
         with torch.autograd.profiler.record_function("mogt.readout"):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
-            Z = F.linear(hn, _gemm_weight(self, "theta_read", (self.theta_read.weight,),
-                                          lambda: self.theta_read.weight))
+            Wr = packed["theta"] if packed is not None else _gemm_weight(self, "theta_read", (self.theta_read.weight,),
+                                                                           lambda: self.theta_read.weight)
+            Z = F.linear(hn, Wr)
         return ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight, self.norm_ffn.eps,
                                out_dtype=gemm_dtype)
 
-    def forward_fused(self, x: torch.Tensor, prefix_condition, pending, gate_const=None):
+    def training_weight_groups(self) -> list | None:
+        """The parameters behind this block's GEMM operands in the training
+        path, as groups to concatenate and cast (``ops.cast_groups``): phi_val,
+        the value gate, theta_read, [w1; w2], w3.  None where the block's
+        training mixer does not take them so."""
+        parts = _gate_input_parts(getattr(self, "value_gate_input_mode", "current"))
+        ffn = self.ffn
+        if not (isinstance(ffn, SwiGLU) and ops.coupled_proj_scan_supported(self.d_model, self.r, "prev" in parts)
+                and self.phi_value_gate.weight.shape[1] == len(parts) * self.d_model):
+            return None
+        return [[self.phi_val.weight], [self.phi_value_gate.weight], [self.theta_read.weight],
+                [ffn.w1.weight, ffn.w2.weight], [ffn.w3.weight]]
+
+    @staticmethod
+    def packed_weights(outs: list) -> dict:
+        """The operands of ``training_weight_groups`` by name."""
+        return dict(zip(("phi_val", "gate", "theta", "w12", "w3"), outs))
+
+    def forward_fused(self, x: torch.Tensor, prefix_condition, pending, gate_const=None,
+                      packed: dict | None = None):
         """Fused forward.  ``pending = (z, scale)`` is the previous block's last
         residual term (added here inside the first RMSNorm).  ``gate_const``
         (inference only): this block's per-sequence gate-logit term when the
-        caller computed it.  Returns ``(x_after_mixer, (ffn_out, ffn_scale))``:
-        the caller adds the FFN term (or hands it to the next block)."""
+        caller computed it.  ``packed`` (training only): the GEMM operands of
+        ``training_weight_groups`` in the GEMM dtype.  Returns
+        ``(x_after_mixer, (ffn_out, ffn_scale))``: the caller adds the FFN term
+        (or hands it to the next block)."""
         gemm_dtype = _autocast_dtype() or x.dtype
         eps = self.norm_mogt.eps
         if pending is None:
@@ -505,11 +539,11 @@ class MOGTBlock(_WeightCacheOwner):
             x, xn = ops.add_rmsnorm(x, pending[0], pending[1], self.norm_mogt.weight, eps, out_dtype=gemm_dtype)
         damping = float(getattr(self, "connection_damping", 0.999))
         if torch.is_grad_enabled():
-            x, xn2 = self._mixer_training(x, xn, prefix_condition, damping, gemm_dtype)
+            x, xn2 = self._mixer_training(x, xn, prefix_condition, damping, gemm_dtype, packed)
         else:
             x, xn2 = self._mixer_inference(x, xn, prefix_condition, damping, gemm_dtype, gate_const)
         with torch.autograd.profiler.record_function("mogt.ffn"):
-            f = self.ffn(xn2)
+            f = self.ffn(xn2) if packed is None else self.ffn.forward_with(xn2, packed["w12"], packed["w3"])
         return x, (f, float(getattr(self, "mogt_ffn_residual_scale", 1.0)))
 
 
@@ -525,6 +559,22 @@ class MOGTModel(_WeightCacheOwner):
         self.norm_f = RMSNorm(d_model)
         self.gradient_checkpointing = False
         self.checkpoint_every_n = 1
+
+    def _packed_training_weights(self) -> list:
+        """Under autograd and autocast: every block's GEMM operands cast to the
+        autocast dtype in one multi-tensor copy (and their gradients cast back
+        in one), instead of a cast kernel per weight and the fp32
+        concatenations; a list of None otherwise."""
+        ad = _autocast_dtype()
+        groups = [blk.training_weight_groups() for blk in self.blocks]
+        if not torch.is_grad_enabled() or ad is None or any(g is None for g in groups):
+            return [None] * len(self.blocks)
+        outs = ops.cast_groups([grp for g in groups for grp in g], ad)
+        packed, i = [], 0
+        for g in groups:
+            packed.append(MOGTBlock.packed_weights(outs[i:i + len(g)]))
+            i += len(g)
+        return packed
 
     def _prefix_condition(self, h: torch.Tensor) -> torch.Tensor | None:
         """The embedding row at ``prefix_condition_position`` (negative counts
@@ -582,9 +632,10 @@ class MOGTModel(_WeightCacheOwner):
             # each block hands its FFN term to the next block's first RMSNorm;
             # the last one is added inside norm_f
             consts = self._gate_consts(cond) if not torch.is_grad_enabled() else [None] * len(self.blocks)
+            packed = self._packed_training_weights()
             pending = None
-            for blk, gc in zip(self.blocks, consts):
-                h, pending = blk.forward_fused(h, cond, pending, gc)
+            for blk, gc, pk in zip(self.blocks, consts, packed):
+                h, pending = blk.forward_fused(h, cond, pending, gc, pk)
             if not torch.is_grad_enabled():
                 return ops.add_rmsnorm_final(h, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps)
             return ops.add_rmsnorm(h, pending[0], pending[1], self.norm_f.weight, self.norm_f.eps,

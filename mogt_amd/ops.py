@@ -1103,6 +1103,58 @@ def embedding(ids: torch.Tensor, module: torch.nn.Embedding) -> torch.Tensor:
     return _Embedding.apply(module.weight, ids)
 
 
+# GEMM operands of a training step, cast in one pass -------------------------
+class _CastGroups(torch.autograd.Function):
+    """Each group of parameters concatenated along dim 0 and cast to ``dtype``
+    (the casts autocast, or an explicit ``.to``, would make one tensor at a
+    time, after a concatenation) with one multi-tensor copy; backward: every
+    parameter's gradient, its rows of the group's gradient cast back to the
+    parameter's dtype, with one multi-tensor copy."""
+
+    @staticmethod
+    def forward(ctx, dtype, sizes, *params):
+        ctx.sizes = sizes
+        ctx.meta = [(p.shape, p.dtype) for p in params]
+        ctx.set_materialize_grads(False)   # an unused operand gives its parameters no gradient
+        outs, dst = [], []
+        i = 0
+        for n in sizes:
+            grp = params[i:i + n]
+            out = torch.empty((sum(p.shape[0] for p in grp), *grp[0].shape[1:]), dtype=dtype,
+                              device=grp[0].device)
+            outs.append(out)
+            dst.extend(out.split([p.shape[0] for p in grp], dim=0))
+            i += n
+        torch._foreach_copy_(dst, [p.contiguous() for p in params])
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        res = [None] * len(ctx.meta)
+        src, dst = [], []
+        i = 0
+        for n, g in zip(ctx.sizes, grads):
+            if g is not None:
+                parts = g.split([ctx.meta[k][0][0] for k in range(i, i + n)], dim=0)
+                for k, part in zip(range(i, i + n), parts):
+                    res[k] = torch.empty(ctx.meta[k][0], dtype=ctx.meta[k][1], device=part.device)
+                    src.append(part)
+                    dst.append(res[k])
+            i += n
+        if dst:
+            torch._foreach_copy_(dst, src)
+        return (None, None, *res)
+
+
+def cast_groups(groups: list, dtype: torch.dtype) -> list:
+    """For each group (parameters with equal trailing shape), the parameters
+    concatenated along dim 0 in ``dtype``, differentiable.  All the casts, and
+    their gradients' casts back, run as one multi-tensor copy each way instead
+    of a kernel per tensor plus the concatenations."""
+    params = [p for grp in groups for p in grp]
+    return list(_CastGroups.apply(dtype, [len(grp) for grp in groups], *params))
+
+
 # backward of the row kernels -------------------------------------------------
 RMSNORM_BWD_WAVES_PER_GROUP = 4   # mogt_rmsnorm_bwd writes one dw partial row per 4-wave work-group
 

@@ -67,3 +67,27 @@ def test_gemm_table_is_well_formed():
     assert len(rows) >= 40 and all(len(r) == 4 and float(r[3]) > 0 for r in rows)
     shapes = {r[1] for r in rows}
     assert any(s.startswith("tn_6144_32768_768") for s in shapes)   # the fused [w1; w2] projection
+
+
+def test_cast_groups_values_and_gradients():
+    """ops.cast_groups: each group concatenated along rows in the target dtype
+    (the values of cast-then-cat), and every parameter's gradient its rows of
+    the group's gradient cast back to the parameter's dtype -- what separate
+    casts and a torch.cat would give."""
+    from mogt_amd import ops
+
+    torch.manual_seed(0)
+    a = torch.randn(3, 4, requires_grad=True)
+    b = torch.randn(2, 4, requires_grad=True)
+    c = torch.randn(5, 2, requires_grad=True)
+    d = torch.randn(1, 2, requires_grad=True)   # no gradient reaches it
+    ab, cc, dd = ops.cast_groups([[a, b], [c], [d]], torch.bfloat16)
+    assert ab.dtype == torch.bfloat16 and ab.shape == (5, 4) and cc.shape == (5, 2)
+    assert torch.equal(ab, torch.cat([a, b]).bfloat16()) and torch.equal(cc, c.bfloat16())
+    w0, w1 = torch.randn(5, 4), torch.randn(5, 2)
+    ((ab.float() * w0).sum() + (cc.float() * w1).sum()).backward()
+    ref = [t.detach().clone().requires_grad_() for t in (a, b, c)]
+    ((torch.cat(ref[:2]).bfloat16().float() * w0).sum() + (ref[2].bfloat16().float() * w1).sum()).backward()
+    for got, want in zip((a, b, c), ref):
+        assert got.grad.dtype == torch.float32 and torch.equal(got.grad, want.grad)
+    assert d.grad is None
