@@ -321,9 +321,10 @@ int mogt_add_rmsnorm_rowscale_fwd(const float* x, const void* z, const float* ro
  *   r = rsqrt(mean(x^2) + eps); dx has x's dtype, dy fp32 or bf16; dres
  *   (fp32 [rows, dim], may be null) is the residual stream's own gradient of
  *   add_rmsnorm (x fp32).  Each wave covers rows_per_wave rows and each
- *   work-group 4 waves; dw_partial: fp32 [ceil(ceil(rows / rows_per_wave) /
- *   4), dim], one row per work-group of partial sums of dy * n.type_as(x)
- *   (its waves' sums added in a fixed order); the caller sums them over rows.
+ *   work-group 4 waves; dw_partial: fp32 [dim, G], G = ceil(ceil(rows /
+ *   rows_per_wave) / 4) work-groups: per feature, each work-group's partial
+ *   sum of dy * n.type_as(x) (its waves' sums added in a fixed order); the
+ *   caller sums each feature's G partials (a contiguous row).
  *   dz (may be null): also writes dz = dx * dz_scale in dz_dtype, the
  *   gradient of add_rmsnorm's scaled residual term x + scale * z.
  * mogt_silu_mul_bwd: y = [rows, 2*hidden] (forward input), dout = [rows,

@@ -16,7 +16,7 @@ MOGT_F32 = 0
 MOGT_BF16 = 1
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64

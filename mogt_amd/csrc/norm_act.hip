@@ -226,7 +226,8 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
         }
     }
     // the group's waves' dw partials summed in wave order (deterministic):
-    // one partial row per work-group
+    // one partial per work-group and feature, stored feature-major
+    // ([D][groups]) so the caller's sum runs along contiguous memory
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int c = (k * 64 + lane) * 4;
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(64 * NA_WAVES) void rmsnorm_bwd_kernel(
         float t = dw_lds[c];
 #pragma unroll
         for (int q = 1; q < NA_WAVES; ++q) t += dw_lds[q * D + c];
-        dw_part[static_cast<int64_t>(blockIdx.x) * D + c] = t;
+        dw_part[static_cast<int64_t>(c) * gridDim.x + blockIdx.x] = t;
     }
 }
 

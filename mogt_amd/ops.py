@@ -1156,7 +1156,7 @@ def cast_groups(groups: list, dtype: torch.dtype) -> list:
 
 
 # backward of the row kernels -------------------------------------------------
-RMSNORM_BWD_WAVES_PER_GROUP = 4   # mogt_rmsnorm_bwd writes one dw partial row per 4-wave work-group
+RMSNORM_BWD_WAVES_PER_GROUP = 4   # mogt_rmsnorm_bwd writes one dw partial per feature and 4-wave work-group
 
 
 def _rows_per_wave(rows: int) -> int:
@@ -1175,7 +1175,7 @@ def _rmsnorm_bwd_launch(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
     rpw = _rows_per_wave(rows)
     dx = torch.empty_like(x)
     groups = -(-(-(-rows // rpw)) // RMSNORM_BWD_WAVES_PER_GROUP)
-    parts = torch.empty((max(1, groups), D), dtype=torch.float32, device=x.device)
+    parts = torch.empty((D, max(1, groups)), dtype=torch.float32, device=x.device)
     if dres is not None:
         dres = dres.contiguous().to(torch.float32)
     rc = lib.mogt_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
@@ -1185,7 +1185,7 @@ def _rmsnorm_bwd_launch(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor,
                               float(dz_scale), dtype_code(dz.dtype, "rmsnorm_bwd") if dz is not None else 0,
                               _stream_handle(x.device))
     _lib.check(rc, "mogt_rmsnorm_bwd")
-    dw = parts.sum(0) if rows > 0 else torch.zeros(D, dtype=torch.float32, device=x.device)
+    dw = parts.sum(1) if rows > 0 else torch.zeros(D, dtype=torch.float32, device=x.device)
     return dx, dw
 
 
