@@ -445,8 +445,10 @@ def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets
             "tflops": flops / (ms * 1e-3) / 1e12}
 
 
-def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=3):
-    """rank-1 coupled write-forget scan with readout, bf16 I/O."""
+def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=3, path=0):
+    """rank-1 coupled write-forget scan with readout, bf16 I/O.
+    path: 0 = the library's choice (one launch at this length), 2 = the
+    three-launch form."""
     from mogt_amd import synthetic
 
     dev = torch.device("cuda:0")
@@ -455,12 +457,12 @@ def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=
     ws = ops.workspace(lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d), dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
-    fn = lib.mogt_rank1_coupled_scan_fwd
+    fn = lib.mogt_rank1_coupled_scan_fwd_cfg
 
     def launch(i):
         ff, kk, vv, qq, yy = bufs[i % sets]
         rc = fn(ff.data_ptr(), kk.data_ptr(), vv.data_ptr(), qq.data_ptr(), yy.data_ptr(), B, L, H, d,
-                1, 1, 1, ws.data_ptr(), ws.numel(), sh)
+                1, 1, 1, ws.data_ptr(), ws.numel(), path, sh)
         if rc:
             raise RuntimeError(lib.mogt_last_error().decode())
 
@@ -719,10 +721,13 @@ def main():
                 "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
         if full or args.only == "rank1":
             r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
+            r3 = measure_rank1(torch, lib, ops, args.steps, args.warmup, path=2)
             extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out)"}
+                "three_launch_us": round(r3["ms"] * 1e3, 2),
+                "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out); us: one launch "
+                        "(carries exchanged between work-groups), three_launch_us: summaries, carries, outputs"}
         if full or args.only == "dense":
             r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
             extras["dense_affine_r16_c48_L32768"] = {

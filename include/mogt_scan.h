@@ -265,13 +265,24 @@ int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H
  * V_t = (1 - f_t) v_t k_t^T, read out through q_t, without materialising S_t.
  * f: [B, L, H]; k, v, q, y: [B, L, H, head_dim]; head_dim = 64.  Products run
  * on bf16 MFMA with fp32 accumulation and fp32 carried state (inputs are
- * rounded to bf16); three launches (chunk states, carries, outputs).        */
+ * rounded to bf16).  With bf16 k, v, q and sequences of at most 64
+ * super-chunks of 256 steps (L <= 16384) it runs as one launch whose
+ * work-groups exchange the carried states through the workspace; otherwise
+ * as three launches (chunk states, carries, outputs).  The workspace query
+ * covers both.
+ * mogt_rank1_coupled_scan_fwd_cfg: the same with the path forced (0 = by
+ *   length as above, 1 = one launch, 2 = three launches); no counterpart in
+ *   the reference -- for tests and benchmarks of both paths.                */
 size_t mogt_rank1_coupled_scan_workspace_bytes(int64_t batch, int64_t length, int64_t heads,
                                                int64_t head_dim);
 int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, const void* q,
                                 void* y, int64_t batch, int64_t length, int64_t heads,
                                 int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
                                 void* workspace, size_t workspace_bytes, void* stream);
+int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, const void* v, const void* q,
+                                    void* y, int64_t batch, int64_t length, int64_t heads,
+                                    int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
+                                    void* workspace, size_t workspace_bytes, int path, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Row-wise kernels of the MOGT block (one wave per row, rows of `dim`

@@ -16,7 +16,7 @@ MOGT_F32 = 0
 MOGT_BF16 = 1
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -143,6 +143,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_void_p]),
+    "mogt_rank1_coupled_scan_fwd_cfg": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_int, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -126,13 +126,17 @@ __device__ __forceinline__ int tile_m() { return static_cast<int>(threadIdx.x) >
 __device__ __forceinline__ int tile_sg() { return static_cast<int>(threadIdx.x) & 7; }
 
 // Descriptor over the rows t0 .. L - 1 of one (batch, head) sequence of a
-// [B, L, H, n] tensor with n elements of T per row (t0 < L).
+// [B, L, H, n] tensor with n elements of T per row.  For t0 >= L (a padding
+// sub-chunk past the end, which the summary kernel still prefetches) the range
+// is empty and the base stays at the sequence's first row: loads read 0.
 template <typename T>
 __device__ __forceinline__ auto seq_rsrc(const T* base, int64_t rowbase, int64_t t0, int64_t L, int H, int n) {
     const int64_t strideB = static_cast<int64_t>(H) * n * sizeof(T);
-    const int64_t span = (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + t0 * H) * n, 0,
-                                             static_cast<int>(span < 0x7fffffff ? span : 0x7fffffff), 0x00020000);
+    const bool live = t0 < L;
+    int64_t span = live ? (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T) : 0;
+    if (span > 0x7fffffff) span = 0x7fffffff;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + (live ? t0 : 0) * H) * n, 0,
+                                             static_cast<int>(span), 0x00020000);
 }
 
 template <typename TI>
@@ -494,11 +498,548 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Single-pass form, for sequences of at most R1S_MAX_SC super-chunks.
+//
+// One work-group per super-chunk (256 steps); wave j owns sub-chunk j (64
+// steps) from start to end, so the waves never take turns:
+//   1. each wave loads its q, k (MFMA operand registers), v and f, scans its
+//      log-decays, and stages V and K diag(w) (w relative to the sub-chunk's
+//      end) into LDS as natural [step][dim] rows            | barrier
+//   2. wave j: S_j^loc = the state at its sub-chunk's start from a zero state
+//      at the super-chunk's start (Horner over the staged sub-chunks m < j:
+//      S <- 2^LcT_m S + K_m^T diag(w) V_m); wave 0 runs all four and publishes
+//      the super-chunk's aggregate; P^T = K Q^T decayed and masked;
+//      y_pre = 2^Lc_t Q S_j^loc^T + P V
+//   3. carries, cooperatively per sequence: once every aggregate of the
+//      sequence is published, work-group c scans the element slice
+//      [c E, (c + 1) E) of the states through all super-chunks and writes the
+//      carried-in states' slices; once every slice is written, each
+//      work-group reads its own carried-in state S_in
+//   4. y = y_pre + 2^(Lc_t + Lc_start_j) Q S_in^T              -> y
+// The contractions over steps (K^T V, P V) read their operands from the
+// natural LDS rows with ds_read_b64_tr_b16 (gfx950's transposing LDS read):
+// in each 16-lane group, lane 4r + c addresses row r, columns 4c .. 4c + 3 of
+// a 4 x 16 block, and lane i receives column i of the block's 4 rows.  LDS
+// rows hold their 16-byte chunks XOR-permuted by row so these reads are free
+// of bank conflicts.  Operands of the contractions over the head dimension
+// (K Q^T, Q S^T) come straight from registers in a contraction order that
+// matches the MFMA accumulator layout (k = 16 kk + 4 (lane / 32) + 0..3, then
+// + 8), so P^T and S^T accumulators feed the next products without a
+// transpose.  The cross-work-group steps use the workspace epoch tags of the
+// look-back protocol: payloads are written with agent-coherent (sc1) stores,
+// each writer waits for its stores before its flag, readers poll the flags
+// with agent-scope loads and read payloads with sc1 loads.  Every wait is
+// bounded; a wait that gives up poisons the affected outputs with NaN and
+// counts in the workspace header.  Forward progress needs all super-chunks of
+// one sequence resident at once, which in-order dispatch guarantees for at
+// most R1S_MAX_SC of them.
+// ---------------------------------------------------------------------------
+constexpr int R1S_MAX_SC = 64;
+constexpr int R1S_SSR = R1_DH + 4;    // row stride (bf16) of the S_in hi / lo tiles: 136-byte rows
+constexpr int R1S_NB = 16;            // aggregates loaded per batch of the slice scan
+constexpr int R1_SC1 = 16;            // buffer cache policy: agent-coherent (sc1)
+
+struct Rank1SParams {
+    const void* f;
+    const void* k;
+    const void* v;
+    const void* q;
+    void* y;
+    uint32_t* hdr;
+    uint64_t* flag1;   // [n_seq][nsc] {tag | total log2-decay of the super-chunk}
+    uint32_t* flag2;   // [n_seq][nsc] tag: slices of the carried-in states written
+    float* agg;        // [n_seq][nsc][DH*DH] aggregates (accumulator order)
+    float* sin;        // [n_seq][nsc][DH*DH] carried-in states (same order)
+    int64_t L;
+    int H, nsc;
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Natural LDS tile [64 rows][64] bf16: 16-byte chunk c of row r sits at chunk
+// c ^ nsw(r).  A transposing read touches rows R0 .. R0 + 3 (R0 % 4 == 0) and
+// two adjacent chunks per row, which then cover all 32 banks once.
+__device__ __forceinline__ int nsw(int row) { return ((row & 3) << 1) | ((row >> 2) & 1); }
+__device__ __forceinline__ int noff(int row, int col) {   // element offset, col % 4 == 0
+    return row * R1_DH + 8 * ((col >> 3) ^ nsw(row)) + (col & 7);
+}
+
+__device__ __forceinline__ u32x2 ds_tr(bf16_t* p) {
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// 8-bf16 MFMA operand whose contraction runs over the rows of a natural tile:
+// lane l gets column cb + l % 32 and rows 16 kk + 4 (l / 32) + 0..3 (slots
+// 0-3) and the same + 8 (slots 4-7).
+__device__ __forceinline__ bf16x8 tr_op(bf16_t* tile, int kk, int cb) {
+    const int l = threadIdx.x & 63, i = l & 15;
+    const int col = cb + 16 * ((l >> 4) & 1) + 4 * (i & 3);
+    const int r0 = 16 * kk + 4 * (l >> 5) + (i >> 2);
+    const u32x2 a = ds_tr(tile + noff(r0, col));
+    const u32x2 b = ds_tr(tile + noff(r0 + 8, col));
+    return __builtin_bit_cast(bf16x8, (u32x4{a[0], a[1], b[0], b[1]}));
+}
+
+// Descriptor over rows t0 .. L - 1 of one (batch, head) sequence of a
+// [B, L, H, n] tensor; an empty range when t0 >= L (loads read 0, stores drop).
+template <typename T>
+__device__ __forceinline__ auto rows_rsrc(const T* base, int64_t rowbase, int64_t t0, int64_t L, int H, int n) {
+    const int64_t strideB = static_cast<int64_t>(H) * n * sizeof(T);
+    int64_t span = t0 < L ? (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T) : 0;
+    if (span > 0x7fffffff) span = 0x7fffffff;
+    const int64_t tb = t0 < L ? t0 : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + tb * H) * n, 0,
+                                             static_cast<int>(span), 0x00020000);
+}
+
+// Register operand of row `row` of a [64][64] tile in global memory, head-dim
+// slots 16 kk + 4 (lane / 32) + 0..3 and + 8 (the accumulator-matching order).
+// Each lane loads the natural 16-byte piece d = 16 kk + 8 (lane / 32) + 0..7
+// (two lanes cover 32 contiguous bytes of a row), then lanes l and l + 32
+// swap half of it: the lower half-wave keeps d + 0..3 and takes the partner's
+// d + 8..11, the upper one takes the partner's d + 4..7 and keeps d + 12..15.
+template <typename TI, typename R>
+__device__ __forceinline__ bf16x8 ld_op(R rs, int row, int kk, int strideB) {
+    const int hf = (threadIdx.x & 63) >> 5;
+    const int off = row * strideB + (16 * kk + 8 * hf) * static_cast<int>(sizeof(TI));
+    u32x4 x;
+    if constexpr (sizeof(TI) == 2) {
+        x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    } else {
+        const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0));
+        x = u32x4{pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
+    }
+    return __builtin_bit_cast(bf16x8, x);
+}
+__device__ __forceinline__ bf16x8 permute_op(bf16x8 v) {
+    const u32x4 x = __builtin_bit_cast(u32x4, v);
+    const bool hf = ((threadIdx.x & 63) >> 5) != 0;
+    const uint32_t s0 = __shfl_xor(hf ? x[0] : x[2], 32, 64);
+    const uint32_t s1 = __shfl_xor(hf ? x[1] : x[3], 32, 64);
+    return __builtin_bit_cast(bf16x8, hf ? (u32x4{s0, s1, x[2], x[3]}) : (u32x4{x[0], x[1], s0, s1}));
+}
+
+// 16-byte chunk (8 consecutive elements as bf16) of row `row`, chunk `ch`.
+template <typename TI, typename R>
+__device__ __forceinline__ u32x4 ld_chunk(R rs, int row, int ch, int strideB) {
+    const int off = row * strideB + ch * 8 * static_cast<int>(sizeof(TI));
+    if constexpr (sizeof(TI) == 2) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    } else {
+        const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        const f32x4 b = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0));
+        return u32x4{pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3])};
+    }
+}
+
+__device__ __forceinline__ uint32_t scale_bf16x2(uint32_t wd, float s) {
+    return pack_bf16(__uint_as_float(wd << 16) * s, __uint_as_float(wd & 0xffff0000u) * s);
+}
+
+// Slots 8 kh .. 8 kh + 7 of a 32x32 accumulator as bf16 hi and lo operands.
+__device__ __forceinline__ void split_op(const f32x16& acc, int kh, bf16x8& hi, bf16x8& lo) {
+    u32x4 hw, lw;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float x0 = acc[8 * kh + 2 * q], x1 = acc[8 * kh + 2 * q + 1];
+        hw[q] = pack_bf16(x0, x1);
+        const float h0 = __uint_as_float(hw[q] << 16), h1 = __uint_as_float(hw[q] & 0xffff0000u);
+        lw[q] = pack_bf16(x0 - h0, x1 - h1);
+    }
+    hi = __builtin_bit_cast(bf16x8, hw);
+    lo = __builtin_bit_cast(bf16x8, lw);
+}
+
+__device__ __forceinline__ void wait_all_memory() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// bf16 one-hot B operand that makes a 32x32x16 MFMA copy its A operand:
+// slot p of k-step half kh holds 1 where the A slot's head-dim index (the
+// ld_op order, 16 kh + 8 (p / 4) + 4 (lane / 32) + p % 4) equals this lane's
+// output column lane % 32.  The copy C[s][n] = A[s][n] comes out in the
+// accumulator layout (lane = column), i.e. transposed.
+__device__ __forceinline__ bf16x8 ident_op(int kh) {
+    const int l = threadIdx.x & 63, n = l & 31, hf = l >> 5;
+    u32x4 w{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int jp = 16 * kh + 8 * (p >> 2) + 4 * hf + (p & 3);
+        if (jp == n) w[p >> 1] |= 0x3F80u << (16 * (p & 1));
+    }
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+__device__ __forceinline__ bf16x8 scale_op(bf16x8 v, float s) {
+    const u32x4 x = __builtin_bit_cast(u32x4, v);
+    return __builtin_bit_cast(bf16x8, (u32x4{scale_bf16x2(x[0], s), scale_bf16x2(x[1], s), scale_bf16x2(x[2], s),
+                                             scale_bf16x2(x[3], s)}));
+}
+
+// Keeps a computed operand in registers where it is made: without it the
+// compiler sinks the producing arithmetic (and its wider fp32 inputs) down to
+// the distant use, past the carry exchange.
+__device__ __forceinline__ void pin(bf16x8& v) {
+    u32x4 x = __builtin_bit_cast(u32x4, v);
+    asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+    v = __builtin_bit_cast(bf16x8, x);
+}
+
+__device__ __forceinline__ bf16x8 pack_op(const f32x16& acc, int kh) {
+    u32x4 wd;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wd[q] = pack_bf16(acc[8 * kh + 2 * q], acc[8 * kh + 2 * q + 1]);
+    return __builtin_bit_cast(bf16x8, wd);
+}
+
+// Offset (floats) of accumulator register group g4 of state tile T in the
+// accumulator order shared by the aggregates, the carried-in states and the
+// LDS chain buffer: lane-contiguous 16-byte groups.
+__device__ __forceinline__ int acc_off(int T, int g4) { return ((T * 4 + g4) * 64 + (threadIdx.x & 63)) * 4; }
+
+template <typename TF, typename TI, typename TO>
+__global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParams p) {
+    __shared__ __attribute__((aligned(16))) bf16_t sV[R1_SUB][R1_T * R1_DH];   // natural V rows
+    __shared__ __attribute__((aligned(16))) float sX[R1_DH * R1_DH];          // state chain / S_in / y staging
+    __shared__ __attribute__((aligned(16))) float sLc[R1_SUB][R1_T];
+    __shared__ __attribute__((aligned(16))) float sOmf[R1_SUB][R1_T];
+    __shared__ __attribute__((aligned(16))) float sE[R1_SUB][R1_T];
+    __shared__ float sLcT[R1_SUB];
+    __shared__ float sLcS[R1S_MAX_SC];
+    __shared__ uint32_t sEpoch;
+    __shared__ int sFail;
+
+    const int nsc = p.nsc;
+    const int seq = blockIdx.x / nsc, c = blockIdx.x - seq * nsc;
+    const int b = seq / p.H, hh = seq - (seq / p.H) * p.H;
+    // wave j owns sub-chunk j (readfirstlane: uniform, so the buffer descriptors stay scalar)
+    const int tid = threadIdx.x, lane = tid & 63, j = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t rowbase = static_cast<int64_t>(b) * p.L * p.H + hh;
+    const int64_t t0 = static_cast<int64_t>(c) * R1_RS + j * R1_T;
+    const int strideI = p.H * R1_DH * static_cast<int>(sizeof(TI));
+    const TF* fp = static_cast<const TF*>(p.f);
+
+    // ---- 1. k, v, f; decays; V rows to LDS; K diag(w) transposed ----------
+    const TF fraw = fp[rowbase + (t0 + lane < p.L ? t0 + lane : p.L - 1) * p.H];
+    const auto rq = rows_rsrc(static_cast<const TI*>(p.q), rowbase, t0, p.L, p.H, R1_DH);
+    const auto rk = rows_rsrc(static_cast<const TI*>(p.k), rowbase, t0, p.L, p.H, R1_DH);
+    const auto rv = rows_rsrc(static_cast<const TI*>(p.v), rowbase, t0, p.L, p.H, R1_DH);
+    bf16x8 kop[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) kop[rt][kk] = ld_op<TI>(rk, 32 * rt + (lane & 31), kk, strideI);
+    u32x4 vch[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) vch[n] = ld_chunk<TI>(rv, (lane >> 3) + 8 * n, lane & 7, strideI);
+    bf16x8 qop[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) qop[rt][kk] = ld_op<TI>(rq, 32 * rt + (lane & 31), kk, strideI);
+    if (tid == 0) {
+        sEpoch = ld_relaxed(&p.hdr[2]);
+        sFail = 0;
+    }
+    const float fv = fval<TF>(fraw, t0 + lane, p.L);
+    const float lc = wave_incl_scan(fmaxf(__log2f(fv), R1_LOG2_MIN));
+    const float lcT = __shfl(lc, 63, 64);
+    const float wgt = exp2_hw(lcT - lc) * (1.0f - fv);
+    sLc[j][lane] = lc;
+    sOmf[j][lane] = 1.0f - fv;
+    sE[j][lane] = exp2_hw(lc);
+    if (lane == 63) sLcT[j] = lcT;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int s = (lane >> 3) + 8 * n;
+        *reinterpret_cast<u32x4*>(&sV[j][noff(s, 8 * (lane & 7))]) = vch[n];
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) kop[rt][kk] = permute_op(kop[rt][kk]);
+    // (K diag(w))^T as dS A operands kwt[sb][jb][kh]: rows j, steps s of block sb
+    bf16x8 kwt[2][2][2];
+    {
+        const float w0 = __shfl(wgt, lane & 31, 64), w1 = __shfl(wgt, (lane & 31) + 32, 64);
+        const bf16x8 id0 = ident_op(0), id1 = ident_op(1);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) {
+                const float ws = sb ? w1 : w0;
+                f32x16 cc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(scale_op(kop[sb][2 * jb], ws), id0, zero16(), 0, 0, 0);
+                cc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(scale_op(kop[sb][2 * jb + 1], ws), id1, cc, 0, 0, 0);
+                kwt[sb][jb][0] = pack_op(cc, 0);
+                kwt[sb][jb][1] = pack_op(cc, 1);
+            }
+    }
+    __syncthreads();
+    const uint32_t epoch = sEpoch;
+    float lcStart = 0.0f, lcS = 0.0f;
+#pragma unroll
+    for (int m = 0; m < R1_SUB; ++m) {
+        if (m < j) lcStart += sLcT[m];
+        lcS += sLcT[m];
+    }
+
+    // ---- P^T = K Q^T decayed and masked, tiles (sb, tb) = (0,0), (0,1), (1,1),
+    // before the state exists (K, Q, P and the state together exceed the
+    // register budget of three work-groups per CU)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) qop[rt][kk] = permute_op(qop[rt][kk]);
+    bf16x8 pb[3][2];
+    {
+        // (1,1) first: the K operand rows 32..63 die after it
+        constexpr int SB[3] = {0, 0, 1}, TB[3] = {0, 1, 1};
+#pragma unroll
+        for (int n = 2; n >= 0; --n) {
+            f32x16 acc = zero16();
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[SB[n]][kk], qop[TB[n]][kk], acc, 0, 0, 0);
+            const int t = 32 * TB[n] + (lane & 31);
+            const float lct = sLc[j][t];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int s0 = 32 * SB[n] + 8 * g4 + 4 * (lane >> 5);
+                const f32x4 ls = *reinterpret_cast<const f32x4*>(&sLc[j][s0]);
+                const f32x4 om = *reinterpret_cast<const f32x4*>(&sOmf[j][s0]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 4 * g4 + q;
+                    acc[r] = (s0 + q <= t) ? acc[r] * exp2_hw(lct - ls[q]) * om[q] : 0.0f;
+                }
+            }
+            pb[n][0] = pack_op(acc, 0);
+            pb[n][1] = pack_op(acc, 1);
+            pin(pb[n][0]);
+            pin(pb[n][1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- 2. dS_j^T = (K diag(w))^T V_j; state chain through LDS ------------
+    f32x16 S[2][2];   // [jb][ib]: dS_j^T, then S_j^loc^T (state at this sub-chunk's start)
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) S[a][e] = zero16();
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const bf16x8 v0 = tr_op(sV[j], 2 * sb + kh, 0), v1 = tr_op(sV[j], 2 * sb + kh, 32);
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) {
+                S[jb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kwt[sb][jb][kh], v0, S[jb][0], 0, 0, 0);
+                S[jb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kwt[sb][jb][kh], v1, S[jb][1], 0, 0, 0);
+            }
+        }
+    float* const aggSeq = p.agg + static_cast<int64_t>(seq) * nsc * (R1_DH * R1_DH);
+    float* const sinSeq = p.sin + static_cast<int64_t>(seq) * nsc * (R1_DH * R1_DH);
+    const auto rAgg = __builtin_amdgcn_make_buffer_rsrc(aggSeq, 0, nsc * R1_DH * R1_DH * 4, 0x00020000);
+    const auto rSin = __builtin_amdgcn_make_buffer_rsrc(sinSeq, 0, nsc * R1_DH * R1_DH * 4, 0x00020000);
+    // wave m reads X_m = S_m^loc and writes X_{m+1} = 2^LcT_m X_m + dS_m in place;
+    // wave 3 turns X_4 into the super-chunk's aggregate and publishes it
+    const bool publish = c + 1 < nsc;
+#pragma unroll
+    for (int m = 0; m < R1_SUB; ++m) {
+        if (j == m) {
+            const float dec = exp2_hw(sLcT[m]);
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const int off = acc_off(2 * a + e, g4);
+                        const f32x4 x = m > 0 ? *reinterpret_cast<const f32x4*>(&sX[off]) : f32x4{0.f, 0.f, 0.f, 0.f};
+                        f32x4 nx;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            nx[q] = fmaf(dec, x[q], S[a][e][4 * g4 + q]);
+                            S[a][e][4 * g4 + q] = x[q];
+                        }
+                        if (m + 1 < R1_SUB)
+                            *reinterpret_cast<f32x4*>(&sX[off]) = nx;
+                        else if (publish)
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, nx), rAgg,
+                                                                   (c * R1_DH * R1_DH + off) * 4, 0, R1_SC1);
+                    }
+            if (m + 1 == R1_SUB && publish) {
+                wait_all_memory();
+                if (lane == 0)
+                    st_relaxed(&p.flag1[static_cast<int64_t>(seq) * nsc + c], pack_word(lcS, make_tag(epoch, ST_AGG)));
+            }
+        }
+        if (m + 1 < R1_SUB) __syncthreads();
+    }
+
+    // ---- 3. carries -------------------------------------------------------
+    const int64_t fbase = static_cast<int64_t>(seq) * nsc;
+    if (nsc > 1) {
+        if (j == 0 && lane < nsc - 1) {   // every aggregate of the sequence but the last
+            const uint32_t tag = make_tag(epoch, ST_AGG);
+            uint64_t wd = ld_relaxed(&p.flag1[fbase + lane]);
+            uint32_t n = 0;
+            bool ok = true;
+            while (word_tag(wd) != tag) {
+                if (++n > MAX_SPIN) {
+                    note_timeout(p.hdr);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                wd = ld_relaxed(&p.flag1[fbase + lane]);
+            }
+            sLcS[lane] = ok ? word_val(wd) : __builtin_nanf("");
+        }
+        __syncthreads();
+        // slice [e0, e1) of every carried-in state: S_in(m + 1) = 2^LcS_m S_in(m) + agg_m
+        const int E = (R1_DH * R1_DH + nsc - 1) / nsc;
+        const int e0 = c * E, e1 = min(R1_DH * R1_DH, e0 + E);
+        for (int e = e0 + tid; e < e1; e += R1_THREADS) {
+            float Sv = 0.0f;
+            for (int m0 = 0; m0 < nsc - 1; m0 += R1S_NB) {
+                float av[R1S_NB];
+#pragma unroll
+                for (int i = 0; i < R1S_NB; ++i)   // past the published aggregates: out of range, reads 0
+                    av[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        rAgg, ((m0 + i < nsc - 1 ? m0 + i : nsc) * R1_DH * R1_DH + e) * 4, 0, R1_SC1));
+#pragma unroll
+                for (int i = 0; i < R1S_NB; ++i) {
+                    const int m = m0 + i;
+                    if (m < nsc - 1) {
+                        Sv = fmaf(exp2_hw(sLcS[m]), Sv, av[i]);
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sv), rSin,
+                                                              ((m + 1) * R1_DH * R1_DH + e) * 4, 0, R1_SC1);
+                    }
+                }
+            }
+        }
+        wait_all_memory();
+        __syncthreads();
+        if (tid == 0) st_relaxed(&p.flag2[fbase + c], make_tag(epoch, ST_INC));
+    } else if (tid == 0) {
+        st_relaxed(&p.flag2[fbase + c], make_tag(epoch, ST_INC));
+    }
+
+    // ---- carried-in state: S_j = 2^Lc_start_j S_in + S_j^loc -----------------
+    if (nsc > 1 && c > 0) {
+        if (j == 0 && lane < nsc) {   // every slice written
+            const uint32_t tag = make_tag(epoch, ST_INC);
+            uint32_t n = 0;
+            while (ld_relaxed(&p.flag2[fbase + lane]) != tag) {
+                if (++n > MAX_SPIN) {
+                    note_timeout(p.hdr);
+                    sFail = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {   // S_in (accumulator order) into the chain buffer
+            const int o = 4 * (tid + R1_THREADS * n);
+            *reinterpret_cast<u32x4*>(&sX[o]) = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rSin, (c * R1_DH * R1_DH + o) * 4, 0, R1_SC1));
+        }
+        __syncthreads();
+        const float es = sFail ? __builtin_nanf("") : exp2_hw(lcStart);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(&sX[acc_off(2 * a + e, g4)]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) S[a][e][4 * g4 + q] = fmaf(es, x[q], S[a][e][4 * g4 + q]);
+                }
+    }
+    __syncthreads();   // the chain buffer is free: y staging from here
+
+    // ---- 4. y = 2^Lc_t Q S_j^T + P V, one column block ib at a time ---------
+    constexpr int SO = static_cast<int>(sizeof(TO));
+    const int strideO = p.H * R1_DH * SO;
+    const auto ry = rows_rsrc(static_cast<const TO*>(p.y), rowbase, t0, p.L, p.H, R1_DH);
+    bf16_t* const sy = reinterpret_cast<bf16_t*>(sX) + j * (R1_T * 32);   // [64 t][32 i] per wave
+    // S_j^T as bf16 hi + lo operands, made once (the fp32 state dies here)
+    bf16x8 sh[4][2], sl[4][2];   // [kk][ib]
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) {
+            split_op(S[kk >> 1][ib], kk & 1, sh[kk][ib], sl[kk][ib]);
+            pin(sh[kk][ib]);
+            pin(sl[kk][ib]);
+        }
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            f32x16 acc = zero16();
+            if (j > 0 || c > 0) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qop[tb][kk], sh[kk][ib], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qop[tb][kk], sl[kk][ib], acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const f32x4 e4 = *reinterpret_cast<const f32x4*>(&sE[j][32 * tb + 8 * g4 + 4 * (lane >> 5)]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[4 * g4 + q] *= e4[q];
+                }
+            }
+#pragma unroll
+            for (int sb = 0; sb <= tb; ++sb)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[tb == 0 ? 0 : 1 + sb][kh],
+                                                                  tr_op(sV[j], 2 * sb + kh, 32 * ib), acc, 0, 0, 0);
+            if constexpr (SO == 2) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int t = 32 * tb + mrow(r), i = lane & 31;
+                    sy[t * 32 + 8 * ((i >> 3) ^ (t & 3)) + (i & 7)] = f32_to_bf16(acc[r]);
+                }
+            } else {
+                const int colB = (32 * ib + (lane & 31)) * SO;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[r]), ry,
+                                                          (32 * tb + mrow(r)) * strideO + colB, 0, 2);
+            }
+        }
+        if constexpr (SO == 2) {   // this wave's [64 t][32 i] block as 16-byte row pieces
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const int t = (lane >> 2) + 16 * n, ch = lane & 3;
+                const u32x4 x = *reinterpret_cast<const u32x4*>(&sy[t * 32 + 8 * (ch ^ (t & 3))]);
+                __builtin_amdgcn_raw_buffer_store_b128(x, ry, t * strideO + (32 * ib + 8 * ch) * SO, 0, 2);
+            }
+        }
+    }
+    ws_finish(p.hdr, p.flag2, static_cast<int64_t>(gridDim.x), epoch);
+}
+
 namespace {
 
 struct R1Geo {
     int nsc;
     size_t off_ds, off_lct, off_sin, bytes;
+    size_t s_flag1, s_flag2, s_agg, s_sin, s_bytes;   // single-pass layout
 };
 
 R1Geo r1_geometry(int64_t B, int64_t L, int64_t H) {
@@ -511,6 +1052,12 @@ R1Geo r1_geometry(int64_t B, int64_t L, int64_t H) {
     g.off_lct = take(nseq * g.nsc * sizeof(float));
     g.off_sin = take(nseq * g.nsc * R1_DH * R1_DH * sizeof(float));
     g.bytes = off;
+    off = WS_HDR_BYTES;
+    g.s_flag1 = take(nseq * g.nsc * sizeof(uint64_t));
+    g.s_flag2 = take(nseq * g.nsc * sizeof(uint32_t));
+    g.s_agg = take(nseq * g.nsc * R1_DH * R1_DH * sizeof(float));
+    g.s_sin = take(nseq * g.nsc * R1_DH * R1_DH * sizeof(float));
+    g.s_bytes = off;
     return g;
 }
 
@@ -527,6 +1074,23 @@ int run_rank1(const Rank1Params& prm, int n_seq, hipStream_t st) {
     return check_launch("rank1_output_kernel");
 }
 
+template <typename TF, typename TI, typename TO>
+int run_rank1_single(const Rank1SParams& prm, int n_seq, hipStream_t st) {
+    hipLaunchKernelGGL((rank1_single_kernel<TF, TI, TO>), dim3(n_seq * prm.nsc), dim3(R1_THREADS), 0, st, prm);
+    return check_launch("rank1_single_kernel");
+}
+
+// The one-launch kernel takes bf16 k, v, q only: fp32 operands would double
+// its load registers past the budget of three work-groups per CU, so fp32
+// k, v, q always take the three-launch path.
+template <typename TF, typename TI, typename TO>
+int run_path(bool single, const Rank1Params& p3, const Rank1SParams& p1, int n_seq, hipStream_t st) {
+    if constexpr (sizeof(TI) == 2) {
+        if (single) return run_rank1_single<TF, TI, TO>(p1, n_seq, st);
+    }
+    return run_rank1<TF, TI, TO>(p3, n_seq, st);
+}
+
 }  // namespace
 }  // namespace mogt
 
@@ -535,42 +1099,68 @@ using namespace mogt;
 extern "C" size_t mogt_rank1_coupled_scan_workspace_bytes(int64_t batch, int64_t length, int64_t heads,
                                                           int64_t head_dim) {
     if (batch <= 0 || length <= 0 || heads <= 0 || head_dim != R1_DH) return WS_HDR_BYTES;
-    return r1_geometry(batch, length, heads).bytes;
+    const R1Geo g = r1_geometry(batch, length, heads);
+    return g.bytes > g.s_bytes ? g.bytes : g.s_bytes;
 }
 
-extern "C" int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, const void* q,
-                                           void* y, int64_t batch, int64_t length, int64_t heads,
-                                           int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
-                                           void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, const void* v, const void* q,
+                                               void* y, int64_t batch, int64_t length, int64_t heads,
+                                               int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
+                                               void* workspace, size_t workspace_bytes, int path,
+                                               void* stream) {
     clear_error();
     if (batch < 0 || length < 0 || heads <= 0)
         return set_error(MOGT_E_INVALID, "f must be [B, L, H] and k, v, q [B, L, H, d]");
     if (head_dim != R1_DH) return set_error(MOGT_E_INVALID, "head_dim %lld not supported (64)", (long long)head_dim);
     for (int d : {f_dtype, kvq_dtype, out_dtype})
         if (d != MOGT_F32 && d != MOGT_BF16) return set_error(MOGT_E_INVALID, "unsupported dtype code");
+    if (path < 0 || path > 2) return set_error(MOGT_E_INVALID, "path %d not in {0, 1, 2}", path);
     if (batch == 0 || length == 0) return MOGT_OK;
     if (!f || !k || !v || !q || !y) return set_error(MOGT_E_INVALID, "null tensor pointer");
-    const R1Geo g = r1_geometry(batch, length, heads);
-    if (!workspace || workspace_bytes < g.bytes)
-        return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", g.bytes, workspace_bytes);
     if (batch * heads > 65535) return set_error(MOGT_E_INVALID, "batch * heads > 65535");
     if (length > (int64_t(1) << 40)) return set_error(MOGT_E_INVALID, "length too large");
+    const R1Geo g = r1_geometry(batch, length, heads);
+    const bool bf16_io = kvq_dtype == MOGT_BF16;
+    const bool single = path == 1 || (path == 0 && g.nsc <= R1S_MAX_SC && bf16_io);
+    if (single && g.nsc > R1S_MAX_SC)
+        return set_error(MOGT_E_INVALID, "single-pass rank-1 scan takes at most %d super-chunks (L <= %d)",
+                         R1S_MAX_SC, R1S_MAX_SC * R1_RS);
+    if (single && !bf16_io) return set_error(MOGT_E_INVALID, "single-pass rank-1 scan takes bf16 k, v, q");
+    const size_t need = single ? g.s_bytes : g.bytes;
+    if (!workspace || workspace_bytes < need)
+        return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", need, workspace_bytes);
     char* base = static_cast<char*>(workspace);
-    Rank1Params prm{};
-    prm.f = f; prm.k = k; prm.v = v; prm.q = q; prm.y = y;
-    prm.dS = reinterpret_cast<float*>(base + g.off_ds);
-    prm.lcT = reinterpret_cast<float*>(base + g.off_lct);
-    prm.Sin = reinterpret_cast<float*>(base + g.off_sin);
-    prm.L = length; prm.H = static_cast<int>(heads); prm.nsc = g.nsc;
+    Rank1Params p3{};
+    p3.f = f; p3.k = k; p3.v = v; p3.q = q; p3.y = y;
+    p3.dS = reinterpret_cast<float*>(base + g.off_ds);
+    p3.lcT = reinterpret_cast<float*>(base + g.off_lct);
+    p3.Sin = reinterpret_cast<float*>(base + g.off_sin);
+    p3.L = length; p3.H = static_cast<int>(heads); p3.nsc = g.nsc;
+    Rank1SParams p1{};
+    p1.f = f; p1.k = k; p1.v = v; p1.q = q; p1.y = y;
+    p1.hdr = reinterpret_cast<uint32_t*>(base);
+    p1.flag1 = reinterpret_cast<uint64_t*>(base + g.s_flag1);
+    p1.flag2 = reinterpret_cast<uint32_t*>(base + g.s_flag2);
+    p1.agg = reinterpret_cast<float*>(base + g.s_agg);
+    p1.sin = reinterpret_cast<float*>(base + g.s_sin);
+    p1.L = length; p1.H = static_cast<int>(heads); p1.nsc = g.nsc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n_seq = static_cast<int>(batch * heads);
     const bool fb = f_dtype == MOGT_BF16, ib = kvq_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
-    if (fb && ib && ob) return run_rank1<bf16_t, bf16_t, bf16_t>(prm, n_seq, st);
-    if (fb && ib && !ob) return run_rank1<bf16_t, bf16_t, float>(prm, n_seq, st);
-    if (!fb && ib && ob) return run_rank1<float, bf16_t, bf16_t>(prm, n_seq, st);
-    if (!fb && ib && !ob) return run_rank1<float, bf16_t, float>(prm, n_seq, st);
-    if (fb && !ib && ob) return run_rank1<bf16_t, float, bf16_t>(prm, n_seq, st);
-    if (fb && !ib && !ob) return run_rank1<bf16_t, float, float>(prm, n_seq, st);
-    if (!fb && !ib && ob) return run_rank1<float, float, bf16_t>(prm, n_seq, st);
-    return run_rank1<float, float, float>(prm, n_seq, st);
+    if (fb && ib && ob) return run_path<bf16_t, bf16_t, bf16_t>(single, p3, p1, n_seq, st);
+    if (fb && ib && !ob) return run_path<bf16_t, bf16_t, float>(single, p3, p1, n_seq, st);
+    if (!fb && ib && ob) return run_path<float, bf16_t, bf16_t>(single, p3, p1, n_seq, st);
+    if (!fb && ib && !ob) return run_path<float, bf16_t, float>(single, p3, p1, n_seq, st);
+    if (fb && !ib && ob) return run_path<bf16_t, float, bf16_t>(single, p3, p1, n_seq, st);
+    if (fb && !ib && !ob) return run_path<bf16_t, float, float>(single, p3, p1, n_seq, st);
+    if (!fb && !ib && ob) return run_path<float, float, bf16_t>(single, p3, p1, n_seq, st);
+    return run_path<float, float, float>(single, p3, p1, n_seq, st);
+}
+
+extern "C" int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, const void* q,
+                                           void* y, int64_t batch, int64_t length, int64_t heads,
+                                           int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+    return mogt_rank1_coupled_scan_fwd_cfg(f, k, v, q, y, batch, length, heads, head_dim, f_dtype, kvq_dtype,
+                                           out_dtype, workspace, workspace_bytes, 0, stream);
 }

@@ -1374,35 +1374,42 @@ def connection_map(A: torch.Tensor, impl: str, *, scale: float = 1.0, damping: f
 # ---------------------------------------------------------------------------
 # rank-1 coupled write-forget scan with readout
 # ---------------------------------------------------------------------------
+RANK1_PATHS = {"auto": 0, "single": 1, "three": 2}
+
+
 @torch.library.custom_op("mogt::rank1_coupled_scan", mutates_args=())
 def _rank1_op(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
-              out_dtype: torch.dtype) -> torch.Tensor:
+              out_dtype: torch.dtype, path: int) -> torch.Tensor:
     lib = _lib.load()
     f, k, v, q = (t.contiguous() for t in (f, k, v, q))
     B, L, H, d = k.shape
     y = torch.empty(k.shape, dtype=out_dtype, device=k.device)
     ws = workspace(lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d), k.device)
-    rc = lib.mogt_rank1_coupled_scan_fwd(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
-                                         y.data_ptr(), B, L, H, d,
-                                         dtype_code(f.dtype, "rank1_coupled_scan"),
-                                         dtype_code(k.dtype, "rank1_coupled_scan"),
-                                         dtype_code(out_dtype, "rank1_coupled_scan"),
-                                         ws.data_ptr(), ws.numel(), _stream_handle(k.device))
-    _lib.check(rc, "mogt_rank1_coupled_scan_fwd")
+    rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
+                                             y.data_ptr(), B, L, H, d,
+                                             dtype_code(f.dtype, "rank1_coupled_scan"),
+                                             dtype_code(k.dtype, "rank1_coupled_scan"),
+                                             dtype_code(out_dtype, "rank1_coupled_scan"),
+                                             ws.data_ptr(), ws.numel(), int(path), _stream_handle(k.device))
+    _lib.check(rc, "mogt_rank1_coupled_scan_fwd_cfg")
+    _checked(ws, "mogt_rank1_coupled_scan_fwd")
     return y
 
 
 @_rank1_op.register_fake
-def _(f, k, v, q, out_dtype):
+def _(f, k, v, q, out_dtype, path):
     return k.new_empty(k.shape, dtype=out_dtype)
 
 
 def rank1_coupled_scan(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor, *,
-                       out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                       out_dtype: torch.dtype | None = None, path: str = "auto") -> torch.Tensor:
     """``y_t = S_t q_t`` with ``S_t = f_t S_{t-1} + (1 - f_t) v_t k_t^T`` per
     (batch, head); f ``[B, L, H]``, k/v/q ``[B, L, H, 64]``.  Products on bf16
     MFMA (inputs rounded to bf16), fp32 state; ``out_dtype`` defaults to
-    ``q.dtype``."""
+    ``q.dtype``.  ``path``: "auto" (one launch up to L = 16384, three beyond),
+    "single" or "three" to force one."""
+    if path not in RANK1_PATHS:
+        raise ValueError(f"path must be one of {sorted(RANK1_PATHS)}")
     require_cuda("rank1_coupled_scan", f, k, v, q)
     if k.ndim != 4 or k.shape != v.shape or k.shape != q.shape:
         raise ValueError("k, v and q must be [B, L, H, d] of the same shape")
@@ -1412,7 +1419,7 @@ def rank1_coupled_scan(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: tor
         raise ValueError("k, v and q must share a dtype")
     if k.shape[-1] != 64:
         raise ValueError(f"head dim {k.shape[-1]} not supported (64)")
-    return torch.ops.mogt.rank1_coupled_scan(f, k, v, q, out_dtype or q.dtype)
+    return torch.ops.mogt.rank1_coupled_scan(f, k, v, q, out_dtype or q.dtype, RANK1_PATHS[path])
 
 
 # ---------------------------------------------------------------------------

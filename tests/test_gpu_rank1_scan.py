@@ -14,33 +14,80 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 2e-2
 
 
-def _run(gpu, B, L, H, seed, out_dtype=torch.bfloat16):
+PATHS = ["single", "three"]
+
+
+def _run(gpu, B, L, H, seed, out_dtype=torch.bfloat16, path="auto"):
     import mogt_amd
 
     f, k, v, q = synthetic.rank1_inputs(B, L, H, 64, seed=seed)
     ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
     ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
-    y = mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, out_dtype=out_dtype)
+    y = mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, out_dtype=out_dtype, path=path)
     torch.cuda.synchronize()
     return y, ref
 
 
-@pytest.mark.parametrize("B,L,H", [(1, 1, 1), (1, 64, 2), (1, 200, 3), (2, 1000, 2)])
-def test_small_and_ragged(gpu, B, L, H):
-    announce(f"rank1 B={B} L={L} H={H}")
-    y, ref = _run(gpu, B, L, H, seed=L + H)
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("B,L,H", [(1, 1, 1), (1, 64, 2), (1, 200, 3), (1, 256, 1), (1, 257, 2),
+                                   (2, 1000, 2), (1, 3000, 3)])
+def test_small_and_ragged(gpu, B, L, H, path):
+    announce(f"rank1 B={B} L={L} H={H} path={path}")
+    y, ref = _run(gpu, B, L, H, seed=L + H, path=path)
     assert y.shape == (B, L, H, 64) and y.dtype == torch.bfloat16
     assert rel_err(to_np(y), ref) <= BF16_TOL
     # fp32 output: the bulk agrees much tighter than the bf16 bar
-    y32, _ = _run(gpu, B, L, H, seed=L + H, out_dtype=torch.float32)
+    y32, _ = _run(gpu, B, L, H, seed=L + H, out_dtype=torch.float32, path=path)
     assert rel_err(to_np(y32), ref) <= 5e-3
+    from mogt_amd import ops
+    assert ops.workspace_faults() == 0
 
 
-def test_cfg3_full_size(gpu):
+@pytest.mark.parametrize("path", PATHS)
+def test_cfg3_full_size(gpu, path):
     """B=2, L=8192, H=12, d=64, bf16 I/O."""
-    announce("rank1 cfg3 full size")
-    y, ref = _run(gpu, 2, 8192, 12, seed=0)
+    announce(f"rank1 cfg3 full size path={path}")
+    y, ref = _run(gpu, 2, 8192, 12, seed=0, path=path)
     assert rel_err(to_np(y), ref) <= BF16_TOL
+
+
+def test_paths_agree_and_repeat(gpu):
+    """The one-launch and three-launch forms agree (they round different
+    bf16 operands: per-sub-chunk vs per-super-chunk decay weights, so the bar
+    is the fp32-output bar against the oracle), and repeated one-launch calls
+    (workspace reused without clearing, a new epoch each time) agree to fp32
+    rounding."""
+    announce("rank1 paths agree, repeated calls")
+    import mogt_amd
+
+    f, k, v, q = synthetic.rank1_inputs(2, 4096, 5, 64, seed=21)
+    ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
+    run = lambda path: mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, out_dtype=torch.float32, path=path)
+    y1 = run("single")
+    y3 = run("three")
+    y1b = run("single")
+    y1c = run("single")
+    torch.cuda.synchronize()
+    assert rel_err(to_np(y1), to_np(y3)) <= 5e-3
+    assert rel_err(to_np(y1b), to_np(y1)) <= 1e-5
+    assert rel_err(to_np(y1c), to_np(y1)) <= 1e-5
+    assert mogt_amd.ops.workspace_faults() == 0
+
+
+def test_length_switch(gpu):
+    """L = 16384 (64 super-chunks) runs in one launch, L = 16640 in three; both
+    against the oracle on one head."""
+    announce("rank1 length switch")
+    import mogt_amd
+
+    for L in (16384, 16640):
+        y, ref = _run(gpu, 1, L, 1, seed=L)
+        assert rel_err(to_np(y), ref) <= BF16_TOL
+    with pytest.raises(ValueError):
+        f, k, v, q = synthetic.rank1_inputs(1, 16640, 1, 64, seed=1)
+        ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
+        mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, path="single")
+    assert mogt_amd.ops.workspace_faults() == 0
 
 
 def test_equals_dense_scan_with_scalar_transport(gpu):
@@ -63,8 +110,10 @@ def test_equals_dense_scan_with_scalar_transport(gpu):
 
 @pytest.mark.parametrize("L,H", [(77, 1), (700, 2)])
 def test_fp32_inputs(gpu, L, H):
-    """fp32 f, k, v, q (rounded to bf16 inside the products): against the oracle
-    on the unrounded inputs, fp32 output."""
+    """fp32 k, v, q take the three-launch path (the one-launch kernel refuses
+    them); checked through the default path and the refusal of the forced one."""
+    # fp32 f, k, v, q (rounded to bf16 inside the products): against the oracle
+    # on the unrounded inputs, fp32 output
     announce(f"rank1 fp32 inputs L={L} H={H}")
     import mogt_amd
 
@@ -75,3 +124,5 @@ def test_fp32_inputs(gpu, L, H):
     torch.cuda.synchronize()
     assert y.dtype == torch.float32
     assert rel_err(to_np(y), ref) <= 1e-2
+    with pytest.raises(ValueError):
+        mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, path="single")
