@@ -7,7 +7,9 @@
  * Conventions shared by every entry point
  *   - Tensors are contiguous row-major device buffers in the layouts named
  *     below (the reference's layouts: U [B,L,R,R], V/H [B,L,R,C]).
- *   - Arithmetic and carried state are fp32; I/O may be fp32 or bf16.
+ *   - Arithmetic and carried state are fp32; I/O may be fp32 or bf16 (the
+ *     generic affine scan also carries an fp64 state and reads / writes fp16
+ *     and fp64).
  *   - Work is enqueued on `stream`; calls are asynchronous.
  *   - Return 0 on success, a negative MOGT_E* code on failure; the message is
  *     kept per thread and read with mogt_last_error().
@@ -30,6 +32,8 @@ extern "C" {
 /* dtype codes */
 #define MOGT_F32 0
 #define MOGT_BF16 1
+#define MOGT_F64 2  /* mogt_affine_scan_generic_fwd only */
+#define MOGT_F16 3  /* mogt_affine_scan_generic_fwd only */
 
 /* error codes */
 #define MOGT_OK 0
@@ -240,6 +244,32 @@ int mogt_affine_scan_vk_fwd(const void* U, const void* v, const void* k, void* H
                             int64_t batch, int64_t length, int64_t rank, int64_t channels,
                             int vk_dtype, int out_dtype,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Generic affine scan  H_t = U_t H_{t-1} + V_t,  H_0 = 0,  for any rank
+ * R <= 1024 and any C, with the state carried in fp32 or fp64.
+ *
+ * Replaces affine_scan_sequential / _doubling / _block_reference
+ * (affine_scan.py:14-62, :127-172, :175-278) for what the MFMA pipeline above
+ * does not take: their state_dtype argument (affine_scan.py:18; float64 in the
+ * reference's own sanity check, sanity_affine_scan.py:19-61), ranks above 32,
+ * and fp16 / fp64 inputs and outputs.  U: [B, L, R, R] in state_dtype
+ * (MOGT_F32 or MOGT_F64; the reference casts U to state_dtype,
+ * affine_scan.py:35); V: [B, L, R, C] in v_dtype; H: [B, L, R, C] and U_prefix
+ * (nullable, U_t ... U_1, return_prefix=True, affine_scan.py:43-55): out_dtype.
+ * v_dtype / out_dtype: MOGT_F32, MOGT_BF16, MOGT_F64 or MOGT_F16; narrow
+ * outputs round the state through fp32, as torch's float64 -> bf16 cast does.
+ * reverse = 1 runs the total-gradient recursion of the backward instead
+ * (affine_scan_sequential_backward, affine_scan.py:110-118):
+ * H_t = V_t + U_{t+1}^T H_{t+1}, H_{L-1} = V_{L-1}, with U_prefix NULL.
+ * Up to three launches on `stream` (chunk summaries, carries, output); the
+ * workspace (query with the same prefix flag and state dtype) needs no
+ * clearing.                                                                 */
+size_t mogt_affine_scan_generic_workspace_bytes(int64_t batch, int64_t length, int64_t rank,
+                                                int64_t channels, int with_prefix, int state_dtype);
+int mogt_affine_scan_generic_fwd(const void* U, const void* V, void* H, void* U_prefix,
+                                 int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                 int v_dtype, int state_dtype, int out_dtype, int reverse,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* Transport-only prefix product Y_t = U_t Y_{t-1}, Y_0 = I.
  * Replaces triton_fused_scan / _fused_scan_kernel (triton_scan.py:13-51,

@@ -14,9 +14,11 @@ from . import _build
 
 MOGT_F32 = 0
 MOGT_BF16 = 1
+MOGT_F64 = 2
+MOGT_F16 = 3
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -99,6 +101,11 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
          _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_affine_scan_generic_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "mogt_affine_scan_generic_fwd": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+         _c_int, _c_void_p, _c_size, _c_void_p]),
     "mogt_fused_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "mogt_fused_scan_fwd": (
         _c_int,

@@ -31,7 +31,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* mogt_last_error(void) { return mogt::g_last_error; }
 
-extern "C" int mogt_abi_version(void) { return 8; }
+extern "C" int mogt_abi_version(void) { return 9; }
 
 extern "C" int mogt_workspace_faults(const void* workspace, size_t workspace_bytes, uint32_t* count,
                                      void* stream) {

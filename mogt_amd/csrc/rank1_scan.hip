@@ -536,7 +536,6 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
 // most R1S_MAX_SC of them.
 // ---------------------------------------------------------------------------
 constexpr int R1S_MAX_SC = 64;
-constexpr int R1S_SSR = R1_DH + 4;    // row stride (bf16) of the S_in hi / lo tiles: 136-byte rows
 constexpr int R1S_NB = 16;            // aggregates loaded per batch of the slice scan
 constexpr int R1_SC1 = 16;            // buffer cache policy: agent-coherent (sc1)
 

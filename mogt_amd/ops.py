@@ -588,6 +588,13 @@ def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping
 # ---------------------------------------------------------------------------
 # dense affine scan: H_t = U_t H_{t-1} + V_t (U [B,L,R,R], V/H [B,L,R,C])
 # ---------------------------------------------------------------------------
+MFMA_MAX_RANK = 32        # the matrix-core pipeline (dense_scan.hip)
+GENERIC_MAX_RANK = 1024   # the generic scan (generic_scan.hip)
+STATE_DTYPES = (torch.float32, torch.float64)
+_GENERIC_CODE = {torch.float32: _lib.MOGT_F32, torch.bfloat16: _lib.MOGT_BF16,
+                 torch.float64: _lib.MOGT_F64, torch.float16: _lib.MOGT_F16}
+
+
 def check_affine_shapes(U: torch.Tensor, V: torch.Tensor) -> tuple[int, int, int, int]:
     """The reference's shape checks (affine_scan.py:26-32, triton_scan.py:193-199)."""
     if U.ndim != 4 or V.ndim != 4:
@@ -596,9 +603,14 @@ def check_affine_shapes(U: torch.Tensor, V: torch.Tensor) -> tuple[int, int, int
     Bv, Lv, Rv, C = V.shape
     if (B, L, R) != (Bv, Lv, Rv) or R != R2:
         raise ValueError("U must be [B, L, R, R] and V must be [B, L, R, C]")
-    if R > 32:
-        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= 32)")
+    if R > GENERIC_MAX_RANK:
+        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= {GENERIC_MAX_RANK})")
     return B, L, R, C
+
+
+def check_mfma_rank(R: int, what: str) -> None:
+    if R > MFMA_MAX_RANK:
+        raise ValueError(f"{what}: R = {R} not supported by the MI355X scan (R <= {MFMA_MAX_RANK})")
 
 
 def _affine_launch(U: torch.Tensor, V: torch.Tensor | None, H: torch.Tensor | None,
@@ -663,19 +675,164 @@ def _(U, V, out_dtype):
     return U.new_empty(U.shape, dtype=out_dtype), V.new_empty(V.shape, dtype=out_dtype)
 
 
+@torch.library.custom_op("mogt::affine_scan_generic", mutates_args=())
+def _affine_scan_generic_op(U: torch.Tensor, V: torch.Tensor, state_dtype: torch.dtype,
+                            out_dtype: torch.dtype, with_prefix: bool,
+                            reverse: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """The generic scan (any R <= 1024, fp32 or fp64 state): returns
+    ``(U_prefix, H)``, ``U_prefix`` empty unless ``with_prefix``; ``reverse``
+    runs the backward's recursion H_t = V_t + U_{t+1}^T H_{t+1}."""
+    lib = _lib.load()
+    Us = U.to(state_dtype).contiguous()        # U_work = U.to(state_dtype), affine_scan.py:35
+    Vc = (V if V.dtype in _GENERIC_CODE else V.to(state_dtype)).contiguous()
+    B, L, R, _ = U.shape
+    C = V.shape[-1]
+    H = torch.empty(V.shape, dtype=out_dtype, device=V.device)
+    P = torch.empty(U.shape if with_prefix else (0,), dtype=out_dtype, device=U.device)
+    sc = _GENERIC_CODE[state_dtype]
+    ws = workspace(lib.mogt_affine_scan_generic_workspace_bytes(B, L, R, C, int(with_prefix), sc), U.device)
+    rc = lib.mogt_affine_scan_generic_fwd(
+        Us.data_ptr(), Vc.data_ptr() if Vc.numel() else None, H.data_ptr() if H.numel() else None,
+        P.data_ptr() if with_prefix and P.numel() else None, B, L, R, C, _GENERIC_CODE[Vc.dtype], sc,
+        _GENERIC_CODE[out_dtype], int(reverse), ws.data_ptr(), ws.numel(), _stream_handle(U.device))
+    _lib.check(rc, "mogt_affine_scan_generic_fwd")
+    return P, H
+
+
+@_affine_scan_generic_op.register_fake
+def _(U, V, state_dtype, out_dtype, with_prefix, reverse):
+    return (U.new_empty(U.shape if with_prefix else (0,), dtype=out_dtype),
+            V.new_empty(V.shape, dtype=out_dtype))
+
+
+def _use_mfma(R: int, state_dtype: torch.dtype, output_dtype: torch.dtype) -> bool:
+    return state_dtype == torch.float32 and R <= MFMA_MAX_RANK and output_dtype in _DTYPE_CODE
+
+
+def _forward_state(U: torch.Tensor, V: torch.Tensor, state_dtype: torch.dtype, prefix: bool):
+    """H (and U_prefix) kept in the state dtype, as the backward needs them."""
+    if _use_mfma(U.shape[-1], state_dtype, state_dtype):
+        if prefix:
+            return torch.ops.mogt.affine_scan_prefix(U, V, state_dtype)
+        return torch.ops.mogt.affine_scan(U, V, state_dtype)
+    P, H = torch.ops.mogt.affine_scan_generic(U, V, state_dtype, state_dtype, prefix, False)
+    return (P, H) if prefix else H
+
+
+def _reverse_scan(U: torch.Tensor, X: torch.Tensor, state_dtype: torch.dtype) -> torch.Tensor:
+    """G_t = X_t + U_{t+1}^T G_{t+1}, G_{L-1} = X_{L-1}, in the state dtype
+    (the carry recursion of affine_scan.py:110-118)."""
+    B, L, R, _ = U.shape
+    if _use_mfma(R, state_dtype, state_dtype):
+        # the matrix-core pipeline scans forward: reversed sequence with
+        # U_back = [I, flip(U^T[1:])] (the construction of triton_scan.py:398-416)
+        Uf = U.to(torch.float32)
+        eye = torch.eye(R, device=U.device, dtype=torch.float32).view(1, 1, R, R).expand(B, 1, R, R)
+        if L > 1:
+            U_back = torch.cat([eye, Uf.transpose(-2, -1)[:, 1:].flip(1)], dim=1)
+        else:
+            U_back = eye.contiguous()
+        G_rev = torch.ops.mogt.affine_scan(U_back, X.to(torch.float32).flip(1).contiguous(), torch.float32)
+        return G_rev.flip(1)
+    _, G = torch.ops.mogt.affine_scan_generic(U, X, state_dtype, state_dtype, False, True)
+    return G
+
+
+def affine_scan_grad(U: torch.Tensor, V: torch.Tensor, grad_H: torch.Tensor | None,
+                     grad_P: torch.Tensor | None = None, *, state_dtype: torch.dtype = torch.float32,
+                     need_grad_u: bool = True, need_grad_v: bool = True):
+    """Gradients of H_t = U_t H_{t-1} + V_t (affine_scan_sequential_backward,
+    affine_scan.py:65-124) and, with ``grad_P``, of U_prefix_t = U_t U_prefix_{t-1}:
+    the augmented state M = [H | U_prefix] gets G = [dH | dP] + U_{t+1}^T G_{t+1}
+    (one reverse scan), dV = G[..., :C] and dU_t = G_t M_{t-1}^T with
+    M_{-1} = [0 | I].  Computed in ``state_dtype``, returned in U's / V's dtypes."""
+    B, L, R, C = V.shape
+    X = (grad_H.to(state_dtype) if grad_H is not None
+         else torch.zeros(V.shape, dtype=state_dtype, device=V.device))
+    if grad_P is not None:
+        X = torch.cat([X, grad_P.to(state_dtype)], dim=-1)
+    G = _reverse_scan(U, X.contiguous(), state_dtype)
+    grad_v = G[..., :C].to(V.dtype) if need_grad_v else None
+    grad_u = None
+    if need_grad_u:
+        zeros = torch.zeros(B, 1, R, C, dtype=state_dtype, device=V.device)
+        if grad_P is not None:
+            P, H = _forward_state(U, V, state_dtype, True)
+            M = torch.cat([H, P], dim=-1)
+            eye = torch.eye(R, dtype=state_dtype, device=V.device).expand(B, 1, R, R)
+            M0 = torch.cat([zeros, eye], dim=-1)
+        else:
+            M = _forward_state(U, V, state_dtype, False)
+            M0 = zeros
+        M_prev = torch.cat([M0, M[:, :-1]], dim=1)
+        grad_u = torch.matmul(G, M_prev.transpose(-2, -1).contiguous()).to(U.dtype)
+    return grad_u, grad_v
+
+
+def _affine_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0], inputs[1])
+
+
+def _affine_backward(ctx, grad_H):
+    U, V = ctx.saved_tensors
+    gu, gv = affine_scan_grad(U, V, grad_H, None, state_dtype=torch.float32,
+                              need_grad_u=ctx.needs_input_grad[0], need_grad_v=ctx.needs_input_grad[1])
+    return gu, gv, None
+
+
+def _affine_prefix_backward(ctx, grad_P, grad_H):
+    U, V = ctx.saved_tensors
+    gu, gv = affine_scan_grad(U, V, grad_H, grad_P, state_dtype=torch.float32,
+                              need_grad_u=ctx.needs_input_grad[0], need_grad_v=ctx.needs_input_grad[1])
+    return gu, gv, None
+
+
+def _generic_setup(ctx, inputs, output):
+    U, V, state_dtype, _out_dtype, with_prefix, reverse = inputs
+    ctx.state_dtype = state_dtype
+    ctx.with_prefix = with_prefix
+    ctx.reverse = reverse
+    ctx.save_for_backward(U, V)
+
+
+def _generic_backward(ctx, grad_P, grad_H):
+    if ctx.reverse:
+        raise RuntimeError("the reverse affine scan (a backward pass) is not differentiable")
+    U, V = ctx.saved_tensors
+    gu, gv = affine_scan_grad(U, V, grad_H, grad_P if ctx.with_prefix else None,
+                              state_dtype=ctx.state_dtype, need_grad_u=ctx.needs_input_grad[0],
+                              need_grad_v=ctx.needs_input_grad[1])
+    return gu, gv, None, None, None, None
+
+
+torch.library.register_autograd("mogt::affine_scan", _affine_backward, setup_context=_affine_setup)
+torch.library.register_autograd("mogt::affine_scan_prefix", _affine_prefix_backward,
+                                setup_context=_affine_setup)
+torch.library.register_autograd("mogt::affine_scan_generic", _generic_backward,
+                                setup_context=_generic_setup)
+
+
 def affine_scan(U: torch.Tensor, V: torch.Tensor, *, output_dtype: torch.dtype | None = None,
-                return_prefix: bool = False):
-    """H_t = U_t H_{t-1} + V_t on the GPU (fp32 state), ``output_dtype``
-    defaulting to ``V.dtype``; with ``return_prefix`` returns ``(U_prefix, H)``
-    (affine_scan.py:14-62 semantics)."""
+                return_prefix: bool = False, state_dtype: torch.dtype = torch.float32):
+    """H_t = U_t H_{t-1} + V_t on the GPU, the state kept in ``state_dtype``
+    (float32 or float64), ``output_dtype`` defaulting to ``V.dtype``; with
+    ``return_prefix`` returns ``(U_prefix, H)`` (affine_scan.py:14-62
+    semantics).  Differentiable in U and V.  fp32 state with R <= 32 and
+    fp32 / bf16 output runs on the matrix-core pipeline, everything else on the
+    generic scan."""
     require_cuda("affine_scan", U, V)
-    check_affine_shapes(U, V)
+    _, _, R, _ = check_affine_shapes(U, V)
     output_dtype = output_dtype or V.dtype
-    if output_dtype not in _DTYPE_CODE:
-        raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
-    if return_prefix:
-        return torch.ops.mogt.affine_scan_prefix(U, V, output_dtype)
-    return torch.ops.mogt.affine_scan(U, V, output_dtype)
+    if state_dtype not in STATE_DTYPES:
+        raise ValueError(f"state dtype {state_dtype} not supported (float32 or float64)")
+    if output_dtype not in _GENERIC_CODE:
+        raise ValueError(f"output dtype {output_dtype} not supported (float32, bfloat16, float16, float64)")
+    if _use_mfma(R, state_dtype, output_dtype):
+        if return_prefix:
+            return torch.ops.mogt.affine_scan_prefix(U, V, output_dtype)
+        return torch.ops.mogt.affine_scan(U, V, output_dtype)
+    P, H = torch.ops.mogt.affine_scan_generic(U, V, state_dtype, output_dtype, return_prefix, False)
+    return (P, H) if return_prefix else H
 
 
 # ---------------------------------------------------------------------------
@@ -687,8 +844,7 @@ def check_vk_shapes(U: torch.Tensor, v: torch.Tensor, k: torch.Tensor) -> tuple[
     B, L, R, R2 = U.shape
     if R != R2 or tuple(v.shape) != (B, L, R) or tuple(k.shape[:2]) != (B, L):
         raise ValueError("U must be [B, L, R, R], v [B, L, R] and k [B, L, C]")
-    if R > 32:
-        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= 32)")
+    check_mfma_rank(R, "dense_scan")
     return B, L, R, k.shape[-1]
 
 
@@ -756,12 +912,18 @@ def fused_scan(U: torch.Tensor, *, output_dtype: torch.dtype | None = None) -> t
     require_cuda("fused_scan", U)
     if U.ndim != 4 or U.shape[2] != U.shape[3]:
         raise ValueError("U must be [B, L, R, R]")
-    if U.shape[2] > 32:
-        raise ValueError(f"R = {U.shape[2]} not supported by the MI355X scan (R <= 32)")
+    B, L, R, _ = U.shape
+    if R > GENERIC_MAX_RANK:
+        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= {GENERIC_MAX_RANK})")
     output_dtype = output_dtype or U.dtype
-    if output_dtype not in _DTYPE_CODE:
-        raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
-    return torch.ops.mogt.fused_scan(U, output_dtype)
+    if output_dtype not in _GENERIC_CODE:
+        raise ValueError(f"output dtype {output_dtype} not supported (float32, bfloat16, float16, float64)")
+    if R <= MFMA_MAX_RANK and output_dtype in _DTYPE_CODE:
+        return torch.ops.mogt.fused_scan(U, output_dtype)
+    # the generic scan's prefix columns with no channels: Y_t = U_t Y_{t-1}, Y_0 = I
+    Y, _ = torch.ops.mogt.affine_scan_generic(U, U.new_empty((B, L, R, 0), dtype=torch.float32),
+                                              torch.float32, output_dtype, True, False)
+    return Y
 
 
 @torch.library.custom_op("mogt::affine_local_scan", mutates_args=())
@@ -797,7 +959,8 @@ def _(U, V, block_size):
 
 def affine_local_scan(U: torch.Tensor, V: torch.Tensor, *, block_size: int = 256):
     require_cuda("affine_local_scan", U, V)
-    check_affine_shapes(U, V)
+    _, _, R, _ = check_affine_shapes(U, V)
+    check_mfma_rank(R, "affine_local_scan")
     if block_size <= 0:
         raise ValueError("block_size must be positive")
     return torch.ops.mogt.affine_local_scan(U, V, int(block_size))

@@ -6,7 +6,9 @@ conditions as lkcfqy/MOGT ``triton_scan.py``, backed by the HIP kernels of
 ``block_size`` / ``block_c`` / ``carry_scan`` are validated exactly like the
 reference but only hint at the internal chunking (results do not depend on
 them beyond fp32 rounding), and the reference's ``R == 16`` restriction
-(triton_scan.py:200-201) is lifted to ``R <= 32``.
+(triton_scan.py:200-201) is lifted: ``R <= 32`` on the matrix-core pipeline,
+up to 1024 on the generic scan for the hybrid scan and the fused prefix
+product (the block-local scan stays at ``R <= 32``).
 """
 from __future__ import annotations
 
@@ -74,38 +76,14 @@ def _triton_affine_scan_hybrid_forward(U: torch.Tensor, V: torch.Tensor, *, bloc
     return ops.affine_scan(U, V, output_dtype=output_dtype, return_prefix=return_prefix)
 
 
-def _reverse_total_grad(U: torch.Tensor, grad_H: torch.Tensor) -> torch.Tensor:
-    """G_t = dH_t + U_{t+1}^T G_{t+1} as a forward scan of the reversed sequence
-    with U_back = [I, flip(U^T[1:])] (the reference's construction,
-    triton_scan.py:398-416)."""
-    B, L, R, _ = U.shape
-    Uf = U.to(torch.float32)
-    eye = torch.eye(R, device=U.device, dtype=torch.float32).view(1, 1, R, R).expand(B, 1, R, R)
-    if L > 1:
-        U_back = torch.cat([eye, Uf.transpose(-2, -1)[:, 1:].flip(1)], dim=1)
-    else:
-        U_back = eye.contiguous()
-    G_rev = ops.affine_scan(U_back, grad_H.to(torch.float32).flip(1).contiguous(),
-                            output_dtype=torch.float32)
-    return G_rev.flip(1)
-
-
 def _triton_affine_scan_hybrid_backward(U: torch.Tensor, V: torch.Tensor, grad_H: torch.Tensor, *,
                                         block_size: int, block_c: int, carry_scan: str,
                                         need_grad_u: bool, need_grad_v: bool):
-    """dV = G (reverse scan), dU_t = G_t H_{t-1}^T (triton_scan.py:359-426);
-    H is recomputed with the forward scan, the outer products use a batched
-    GEMM."""
-    G = _reverse_total_grad(U, grad_H)
-    grad_v = G.to(V.dtype) if need_grad_v else None
-    grad_u = None
-    if need_grad_u:
-        H = ops.affine_scan(U, V, output_dtype=torch.float32)
-        B, L, R, C = V.shape
-        H_prev = torch.cat([torch.zeros(B, 1, R, C, device=V.device, dtype=torch.float32),
-                            H[:, :-1]], dim=1)
-        grad_u = torch.matmul(G, H_prev.transpose(-2, -1).contiguous()).to(U.dtype)
-    return grad_u, grad_v
+    """dV = G (reverse scan G_t = dH_t + U_{t+1}^T G_{t+1}), dU_t = G_t H_{t-1}^T
+    (triton_scan.py:359-426) in fp32; H is recomputed with the forward scan,
+    the outer products use a batched GEMM."""
+    return ops.affine_scan_grad(U, V, grad_H, None, state_dtype=torch.float32,
+                                need_grad_u=need_grad_u, need_grad_v=need_grad_v)
 
 
 class _TritonAffineScanHybridAutograd(torch.autograd.Function):

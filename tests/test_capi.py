@@ -185,3 +185,27 @@ def test_workspace_fault_query_validates_arguments(lib):
     assert b"null" in lib.mogt_last_error()
     assert lib.mogt_workspace_faults(1, 16, ctypes.byref(count), None) == -2
     assert b"workspace" in lib.mogt_last_error()
+
+
+def test_generic_scan_host_checks(lib):
+    """The generic affine scan validates on the host: state dtype, rank limit,
+    I/O dtypes, no prefix with the reverse scan, and a workspace for more
+    than one chunk (the sequence is one chunk up to 16 steps)."""
+    F32, BF16, F64 = _lib.MOGT_F32, _lib.MOGT_BF16, _lib.MOGT_F64
+    ws = lib.mogt_affine_scan_generic_workspace_bytes
+    assert ws(1, 16, 4, 3, 1, F64) == 256
+    assert ws(1, 17, 4, 3, 1, F64) > ws(1, 17, 4, 3, 0, F64) > ws(1, 17, 4, 3, 0, F32) > 256
+    assert ws(1, 17, 1025, 3, 0, F32) == 256
+    fwd = lib.mogt_affine_scan_generic_fwd
+    rc = fwd(1, 1, 1, None, 1, 8, 4, 3, F32, BF16, F32, 0, None, 0, None)
+    assert rc == -1 and b"state dtype" in lib.mogt_last_error()
+    rc = fwd(1, 1, 1, None, 1, 8, 1025, 3, F32, F32, F32, 0, None, 0, None)
+    assert rc == -1 and b"limit" in lib.mogt_last_error()
+    assert fwd(1, 1, 1, None, 1, 8, 4, 3, 7, F32, F32, 0, None, 0, None) == -1
+    rc = fwd(1, 1, 1, 1, 1, 8, 4, 3, F32, F32, F32, 1, None, 0, None)
+    assert rc == -1 and b"reverse" in lib.mogt_last_error()
+    rc = fwd(1, 1, 1, None, 1, 17, 4, 3, F32, F64, F64, 0, None, 0, None)
+    assert rc == -2 and b"workspace" in lib.mogt_last_error()
+    assert fwd(None, None, None, None, 0, 17, 4, 3, F32, F64, F64, 0, None, 0, None) == 0
+    rc = fwd(None, 1, 1, None, 1, 8, 4, 3, F32, F64, F64, 0, None, 0, None)
+    assert rc == -1 and b"null" in lib.mogt_last_error()

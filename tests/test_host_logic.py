@@ -91,3 +91,26 @@ def test_cast_groups_values_and_gradients():
     for got, want in zip((a, b, c), ref):
         assert got.grad.dtype == torch.float32 and torch.equal(got.grad, want.grad)
     assert d.grad is None
+
+
+def test_affine_scan_dropins_need_a_gpu():
+    """Host tensors are scanned on the GPU; without one the drop-ins raise
+    instead of computing on the CPU."""
+    import pytest
+    import torch
+
+    from mogt_amd import affine_scan as das
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    U = torch.eye(3, dtype=torch.float64).expand(1, 5, 3, 3)
+    V = torch.ones(1, 5, 3, 2, dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        das.affine_scan_sequential(U, V, state_dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        das.affine_scan_sequential_backward(U, V, V, state_dtype=torch.float64)
+    # argument errors come first, as in the reference
+    with pytest.raises(ValueError):
+        das.affine_scan_sequential(U, V, state_dtype=torch.int64)
+    with pytest.raises(ValueError):
+        das.affine_scan_block_reference(U, V, block_size=0)
