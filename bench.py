@@ -445,6 +445,35 @@ def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets
             "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def measure_generic(torch, lib, ops, B, L, R, C, steps, warmup, f64=True, sets=2):
+    """The generic affine scan (mogt_affine_scan_generic_fwd): U, V, H in the
+    state dtype (float64 or fp32), U = I + small noise scaled to norm <= 1."""
+    dev = torch.device("cuda:0")
+    dt = torch.float64 if f64 else torch.float32
+    code = 2 if f64 else 0   # MOGT_F64 / MOGT_F32
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    U0 = torch.eye(R, device=dev, dtype=dt) + (0.3 / R ** 0.5) * torch.randn(B, L, R, R, generator=gen,
+                                                                             device=dev, dtype=dt)
+    U0 = U0 / torch.linalg.matrix_norm(U0, ord=2).clamp(min=1.0)[..., None, None]
+    V0 = torch.randn(B, L, R, C, generator=gen, device=dev, dtype=dt)
+    bufs = [(U0.clone(), V0.clone(), torch.empty(B, L, R, C, device=dev, dtype=dt)) for _ in range(sets)]
+    del U0, V0
+    ws = ops.workspace(lib.mogt_affine_scan_generic_workspace_bytes(B, L, R, C, 0, code), dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def launch(i):
+        u, v, h = bufs[i % sets]
+        rc = lib.mogt_affine_scan_generic_fwd(u.data_ptr(), v.data_ptr(), h.data_ptr(), None, B, L, R, C,
+                                              code, code, code, 0, ws.data_ptr(), ws.numel(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    ms = EventTimer(torch, stream).time(launch, steps, warmup)
+    total = B * L * (R * R + 2 * R * C) * (8 if f64 else 4)
+    return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
+
+
 def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=3, path=0):
     """rank-1 coupled write-forget scan with readout, bf16 I/O.
     path: 0 = the library's choice (one launch at this length), 2 = the
@@ -750,6 +779,16 @@ def main():
                 "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
                 "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
                         "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
+        if full or args.only == "dense":
+            r = measure_generic(torch, lib, ops, 1, 32768, 16, 48, max(3, args.steps // 10), 1)
+            extras["generic_affine_f64_r16_c48_L32768"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "note": "float64 state and I/O (affine_scan_sequential(..., state_dtype=torch.float64)) on the "
+                        "generic scan; latency-bound (256 + 127 + 256 dependent steps), not an HBM roofline case"}
+            r = measure_generic(torch, lib, ops, 24, 2048, 64, 64, max(3, args.steps // 10), 1, f64=False)
+            extras["generic_affine_f32_r64_c64_b24_L2048"] = {
+                "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
+                "note": "R = 64 (above the matrix-core pipeline's 32): fp32 on the generic scan"}
         if full:
             for impl in ("matrix_exp", "cayley"):
                 r = measure_connection_map(torch, lib, ops, impl, 32768, 16, args.steps, args.warmup)

@@ -94,13 +94,29 @@ __device__ __forceinline__ void put(const GParams& p, int64_t b, int64_t idx, in
     }
 }
 
+// Row length in LDS of the staged transition and of a state column: R rounded
+// up to 16 bytes, plus 16 bytes of skew between rows.
+template <typename TS>
+__host__ __device__ constexpr int gs_ld(int R) {
+    return (R + static_cast<int>(16 / sizeof(TS)) - 1) / static_cast<int>(16 / sizeof(TS)) *
+               static_cast<int>(16 / sizeof(TS)) + static_cast<int>(16 / sizeof(TS));
+}
+
 template <typename TS, bool ULDS>
-__global__ __launch_bounds__(GS_THREADS) void generic_scan_kernel(GParams p) {
+__global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_scan_kernel(GParams p) {
     extern __shared__ __align__(16) unsigned char gs_smem[];
+    // LDS: the step's transition U [R][ld] (staged variant) then two state
+    // buffers stored column-major, [Cb][ld]; ld = R rounded up to 16 bytes plus
+    // 16 bytes of skew, so a thread reads 16 bytes of a U row or of its state
+    // column per instruction.  Padding columns / rows stay zero.
+    constexpr int VE = 16 / sizeof(TS);
     const int R = p.R, Cb = p.Cb, RCb = R * Cb;
-    const int uld = R + 1;  // padded rows: lanes of one wave read different rows at one k
+    const int ld = gs_ld<TS>(R);
     TS* sU = reinterpret_cast<TS*>(gs_smem);
-    TS* sS = sU + (ULDS ? R * uld : 0);  // two state buffers of R x Cb
+    TS* sS = sU + (ULDS ? R * ld : 0);
+    const int lds_elems = (ULDS ? R * ld : 0) + 2 * Cb * ld;
+    for (int e = threadIdx.x; e < lds_elems; e += GS_THREADS) sU[e] = TS(0);
+    __syncthreads();
 
     const int tid = threadIdx.x;
     int64_t blk = blockIdx.x;
@@ -134,7 +150,7 @@ __global__ __launch_bounds__(GS_THREADS) void generic_scan_kernel(GParams p) {
             if (p.shift) put<TS>(p, b, 0, oi[m], oc[m], v0);
         }
         acc[m] = v0;
-        if (own[m]) sS[tid + m * GS_THREADS] = v0;
+        if (own[m]) sS[ocl[m] * ld + oi[m]] = v0;
     }
 
     TS ureg[ULDS ? GS_UPT : 1];
@@ -172,8 +188,8 @@ __global__ __launch_bounds__(GS_THREADS) void generic_scan_kernel(GParams p) {
                 if (idx < R * R) {
                     const int rr = idx / R, cc = idx - rr * R;
                     // stored as the transition itself: row i, column k
-                    if (p.rev) sU[cc * uld + rr] = ureg[m];
-                    else sU[rr * uld + cc] = ureg[m];
+                    if (p.rev) sU[cc * ld + rr] = ureg[m];
+                    else sU[rr * ld + cc] = ureg[m];
                 }
             }
         }
@@ -183,35 +199,50 @@ __global__ __launch_bounds__(GS_THREADS) void generic_scan_kernel(GParams p) {
         if (s + 1 < n) fetch(q + 1);  // next step's loads overlap this step's arithmetic
         if constexpr (ULDS) __syncthreads();
 
-        const TS* Sc = sS + cur * RCb;
-        TS* Sn = sS + (cur ^ 1) * RCb;
+        const TS* Sc = sS + cur * Cb * ld;
+        TS* Sn = sS + (cur ^ 1) * Cb * ld;
         const bool ident = p.rev && q == 0;
         const int64_t tt = p.rev ? p.L - q : q;
         const int64_t tout = (p.rev ? p.L - 1 - q : q) + p.shift;
+        // every element a thread owns sits in one column (the tile width divides
+        // the thread count), so each state value read serves all of them
+        const TS* scol = Sc + ocl[0] * ld;
+        TS a[GS_EPT];
+#pragma unroll
+        for (int m = 0; m < GS_EPT; ++m) a[m] = vin[m];
+        if (ident) {
+#pragma unroll
+            for (int m = 0; m < GS_EPT; ++m) a[m] += scol[oi[m]];
+        } else if constexpr (ULDS) {
+            typedef TS vec_t __attribute__((ext_vector_type(VE)));
+#pragma unroll 2
+            for (int k = 0; k < R; k += VE) {
+                const vec_t sv = *reinterpret_cast<const vec_t*>(scol + k);
+#pragma unroll
+                for (int m = 0; m < GS_EPT; ++m) {
+                    const vec_t uv = *reinterpret_cast<const vec_t*>(sU + oi[m] * ld + k);
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) a[m] += uv[e] * sv[e];
+                }
+            }
+        } else {
+            const TS* ut = static_cast<const TS*>(p.tr.p);
+            for (int k = 0; k < R; ++k) {
+                const TS sv = scol[k];
+#pragma unroll
+                for (int m = 0; m < GS_EPT; ++m) {
+                    const int64_t ui = p.rev ? at(p.tr, b, tt, k, p.tr_c0 + oi[m]) : at(p.tr, b, tt, oi[m], p.tr_c0 + k);
+                    a[m] += ut[ui] * sv;
+                }
+            }
+        }
 #pragma unroll
         for (int m = 0; m < GS_EPT; ++m) {
             if (!own[m]) continue;
-            TS a = vin[m];
-            if (ok[m]) {
-                const int i = oi[m], cl = ocl[m];
-                if (ident) {
-                    a += Sc[i * Cb + cl];
-                } else if constexpr (ULDS) {
-                    const TS* urow = sU + i * uld;
-                    for (int k = 0; k < R; ++k) a += urow[k] * Sc[k * Cb + cl];
-                } else {
-                    const TS* ut = static_cast<const TS*>(p.tr.p);
-                    if (p.rev) {
-                        for (int k = 0; k < R; ++k) a += ut[at(p.tr, b, tt, k, p.tr_c0 + i)] * Sc[k * Cb + cl];
-                    } else {
-                        const TS* urow = ut + at(p.tr, b, tt, i, p.tr_c0);
-                        for (int k = 0; k < R; ++k) a += urow[k] * Sc[k * Cb + cl];
-                    }
-                }
-                if (p.every) put<TS>(p, b, tout, i, oc[m], a);
-            }
-            acc[m] = a;
-            Sn[tid + m * GS_THREADS] = a;
+            if (!ok[m]) a[m] = TS(0);
+            else if (p.every) put<TS>(p, b, tout, oi[m], oc[m], a[m]);
+            acc[m] = a[m];
+            Sn[ocl[m] * ld + oi[m]] = a[m];
         }
         __syncthreads();
         cur ^= 1;
@@ -251,8 +282,8 @@ GGeo generic_geometry(int64_t B, int64_t L, int64_t R, int64_t C, int with_prefi
 }
 
 int tile_width(int R, int W) {
-    int cap = 1;
-    while (cap * 2 * R <= GS_MAX_ELEMS) cap *= 2;
+    int cap = 1;   // a power of two dividing the thread count (one column per thread)
+    while (cap * 2 * R <= GS_MAX_ELEMS && cap < GS_THREADS) cap *= 2;
     int cb = 1;
     while (cb < W && cb < cap) cb *= 2;
     return cb;
@@ -266,8 +297,8 @@ int launch_generic(GParams p, int64_t batch, hipStream_t st, const char* what) {
     if (blocks <= 0) return MOGT_OK;
     if (blocks > 0x7fffffffLL) return set_error(MOGT_E_INVALID, "%s: problem too large for one launch", what);
     const bool ulds = p.R <= GS_ULDS_MAX_R;
-    const size_t lds = (static_cast<size_t>(ulds ? p.R * (p.R + 1) : 0) + 2 * static_cast<size_t>(p.R) * p.Cb) *
-                       sizeof(TS);
+    const int ld = gs_ld<TS>(p.R);
+    const size_t lds = (static_cast<size_t>(ulds ? p.R * ld : 0) + 2 * static_cast<size_t>(p.Cb) * ld) * sizeof(TS);
     if (ulds)
         hipLaunchKernelGGL((generic_scan_kernel<TS, true>), dim3(static_cast<unsigned>(blocks)), dim3(GS_THREADS),
                            lds, st, p);

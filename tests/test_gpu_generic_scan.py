@@ -96,7 +96,8 @@ def test_reference_backward_sanity_fp64(gpu):
     assert np.max(np.abs(gV.numpy() - gV_ref)) <= 1e-10
 
 
-@pytest.mark.parametrize("B,L,R,C", [(2, 3000, 16, 48), (1, 5000, 4, 3), (3, 700, 24, 5), (1, 17, 1, 1)])
+@pytest.mark.parametrize("B,L,R,C", [(2, 3000, 16, 48), (1, 5000, 4, 3), (3, 700, 24, 5), (1, 17, 1, 1),
+                                     (1, 40, 1, 600), (2, 33, 2, 300)])
 def test_fp64_state_multichunk(gpu, B, L, R, C):
     """float64 state across many chunks (carry pass and chunk summaries), with
     the prefix product, on the device."""
