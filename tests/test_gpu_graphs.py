@@ -136,3 +136,34 @@ def test_rank1_scan_graph_replays(gpu):
         assert rel_err(to_np(replayed), to_np(eager)) <= 1e-6
         ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
         assert rel_err(to_np(replayed), ref) <= 2e-2
+
+
+def test_generic_scan_graph_replays(gpu):
+    """The generic scan (float64 state, R = 40, prefix product, three passes)
+    under capture: its workspace needs no clearing, so replays match eager
+    launches exactly."""
+    import mogt_amd
+
+    B, L, R, C = 2, 600, 40, 5
+    gen = np.random.default_rng(95)
+    mk = lambda: (np.eye(R) * 0.95 + (0.2 / np.sqrt(R)) * gen.standard_normal((B, L, R, R)),
+                  gen.standard_normal((B, L, R, C)))
+    U0, V0 = mk()
+    U = torch.from_numpy(U0).to(gpu)
+    V = torch.from_numpy(V0).to(gpu)
+    announce(f"graph generic fp64 L={L} R={R} C={C}: capture")
+    g, out = _capture(lambda: mogt_amd.ops.affine_scan(U, V, state_dtype=torch.float64, return_prefix=True))
+    for i in range(REPLAYS):
+        Un, Vn = mk()
+        U.copy_(torch.from_numpy(Un))
+        V.copy_(torch.from_numpy(Vn))
+        announce(f"graph generic replay {i}")
+        g.replay()
+        torch.cuda.synchronize()
+        P_rep, H_rep = out[0].clone(), out[1].clone()
+        P_eag, H_eag = mogt_amd.ops.affine_scan(U, V, state_dtype=torch.float64, return_prefix=True)
+        torch.cuda.synchronize()
+        assert torch.equal(P_rep, P_eag) and torch.equal(H_rep, H_eag)
+        P_ref, H_ref = so.affine_scan_sequential(Un, Vn, return_prefix=True)
+        assert rel_err(H_rep.cpu().numpy(), H_ref) <= 1e-12
+        assert rel_err(P_rep.cpu().numpy(), P_ref) <= 1e-12
