@@ -271,6 +271,18 @@ int mogt_affine_scan_generic_fwd(const void* U, const void* V, void* H, void* U_
                                  int v_dtype, int state_dtype, int out_dtype, int reverse,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Block-local scan on the generic kernel, for what mogt_affine_local_scan
+ * does not take (R > 32, float64): per block of `block_size` steps, from the
+ * identity / zero state, every step's U_prefix [B, L, R, R] and H_prefix
+ * [B, L, R, C] in out_dtype (the per-step outputs of triton_affine_local_scan,
+ * triton_scan.py:54-148, :178-229; its per-block summaries are the prefixes at
+ * each block's last step, which the caller gathers).  U in state_dtype, V in
+ * v_dtype, as mogt_affine_scan_generic_fwd.  No workspace; one launch.      */
+int mogt_affine_local_scan_generic(const void* U, const void* V, void* U_prefix, void* H_prefix,
+                                   int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                   int64_t block_size, int v_dtype, int state_dtype, int out_dtype,
+                                   void* stream);
+
 /* Transport-only prefix product Y_t = U_t Y_{t-1}, Y_0 = I.
  * Replaces triton_fused_scan / _fused_scan_kernel (triton_scan.py:13-51,
  * :151-175), which hard-codes R = 16; here any R <= 32.  U fp32, Y out_dtype. */

@@ -106,6 +106,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
          _c_int, _c_void_p, _c_size, _c_void_p]),
+    "mogt_affine_local_scan_generic": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+         _c_int, _c_void_p]),
     "mogt_fused_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64]),
     "mogt_fused_scan_fwd": (
         _c_int,

@@ -395,3 +395,33 @@ extern "C" int mogt_affine_scan_generic_fwd(const void* U, const void* V, void* 
                : run_generic<float>(U, V, H, U_prefix, batch, length, rank, channels, v_dtype, state_dtype,
                                     out_dtype, reverse, workspace, st);
 }
+
+extern "C" int mogt_affine_local_scan_generic(const void* U, const void* V, void* U_prefix, void* H_prefix,
+                                              int64_t batch, int64_t length, int64_t rank, int64_t channels,
+                                              int64_t block_size, int v_dtype, int state_dtype, int out_dtype,
+                                              void* stream) {
+    clear_error();
+    int rc = check_generic(batch, length, rank, channels, v_dtype, state_dtype, out_dtype, 0, nullptr);
+    if (rc) return rc;
+    if (block_size <= 0) return set_error(MOGT_E_INVALID, "block_size must be positive");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!U || !U_prefix || (channels > 0 && (!V || !H_prefix))) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    const int64_t nb = (length + block_size - 1) / block_size;
+    if (nb > 0x7fffffffLL) return set_error(MOGT_E_INVALID, "too many blocks");
+    const int iR = static_cast<int>(rank), iC = static_cast<int>(channels);
+    const GView none{nullptr, 0, 0, 0, state_dtype};
+    GParams loc{};
+    // one pass: every block from [0 | I], every step written (the OUTPUT pass
+    // with no carries)
+    loc.tr = GView{const_cast<void*>(U), length * rank * rank, rank * rank, rank, state_dtype};
+    loc.in = GView{const_cast<void*>(V), length * rank * channels, rank * channels, channels, v_dtype};
+    loc.init = none;
+    loc.out_h = GView{H_prefix, length * rank * channels, rank * channels, channels, out_dtype};
+    loc.out_p = GView{U_prefix, length * rank * rank, rank * rank, rank, out_dtype};
+    loc.L = length; loc.seg = block_size; loc.nseg = static_cast<int>(nb);
+    loc.R = iR; loc.W = iC + iR; loc.tr_c0 = 0; loc.cin = iC; loc.cid = iC; loc.csplit = iC;
+    loc.every = 1; loc.shift = 0; loc.rev = 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return state_dtype == MOGT_F64 ? launch_generic<double>(loc, batch, st, "generic local scan")
+                                   : launch_generic<float>(loc, batch, st, "generic local scan");
+}

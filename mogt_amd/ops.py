@@ -957,12 +957,47 @@ def _(U, V, block_size):
             U.new_empty((B, nb, R, R), **f), V.new_empty((B, nb, R, C), **f))
 
 
+@torch.library.custom_op("mogt::affine_local_scan_generic", mutates_args=())
+def _affine_local_scan_generic_op(U: torch.Tensor, V: torch.Tensor, block_size: int
+                                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The block-local scan on the generic kernel (R > 32), fp32 like the
+    matrix-core pass; summaries are the prefixes at each block's last step
+    (the identity padding of the tail block changes neither)."""
+    lib = _lib.load()
+    Us = U.to(torch.float32).contiguous()
+    Vc = (V if V.dtype in _GENERIC_CODE else V.to(torch.float32)).contiguous()
+    B, L, R, _ = U.shape
+    C = V.shape[-1]
+    Up = torch.empty(U.shape, dtype=torch.float32, device=U.device)
+    Hp = torch.empty(V.shape, dtype=torch.float32, device=V.device)
+    rc = lib.mogt_affine_local_scan_generic(
+        Us.data_ptr(), Vc.data_ptr() if Vc.numel() else None, Up.data_ptr(), Hp.data_ptr() if Hp.numel() else None,
+        B, L, R, C, block_size, _GENERIC_CODE[Vc.dtype], _lib.MOGT_F32, _lib.MOGT_F32, _stream_handle(U.device))
+    _lib.check(rc, "mogt_affine_local_scan_generic")
+    ends = torch.clamp(torch.arange(1, (L + block_size - 1) // block_size + 1, device=U.device) * block_size,
+                       max=L) - 1
+    return Up, Hp, Up[:, ends].contiguous(), Hp[:, ends].contiguous()
+
+
+@_affine_local_scan_generic_op.register_fake
+def _(U, V, block_size):
+    B, L, R, _ = U.shape
+    C = V.shape[-1]
+    nb = (L + block_size - 1) // block_size
+    f = dict(dtype=torch.float32)
+    return (U.new_empty(U.shape, **f), V.new_empty(V.shape, **f),
+            U.new_empty((B, nb, R, R), **f), V.new_empty((B, nb, R, C), **f))
+
+
 def affine_local_scan(U: torch.Tensor, V: torch.Tensor, *, block_size: int = 256):
+    """Block-local prefixes and per-block summaries (triton_scan.py:178-229),
+    fp32; R <= 32 on the matrix-core pass, larger R on the generic kernel."""
     require_cuda("affine_local_scan", U, V)
     _, _, R, _ = check_affine_shapes(U, V)
-    check_mfma_rank(R, "affine_local_scan")
     if block_size <= 0:
         raise ValueError("block_size must be positive")
+    if R > MFMA_MAX_RANK:
+        return torch.ops.mogt.affine_local_scan_generic(U, V, int(block_size))
     return torch.ops.mogt.affine_local_scan(U, V, int(block_size))
 
 

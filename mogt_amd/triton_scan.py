@@ -7,8 +7,7 @@ conditions as lkcfqy/MOGT ``triton_scan.py``, backed by the HIP kernels of
 reference but only hint at the internal chunking (results do not depend on
 them beyond fp32 rounding), and the reference's ``R == 16`` restriction
 (triton_scan.py:200-201) is lifted: ``R <= 32`` on the matrix-core pipeline,
-up to 1024 on the generic scan for the hybrid scan and the fused prefix
-product (the block-local scan stays at ``R <= 32``).
+up to 1024 on the generic scan.
 """
 from __future__ import annotations
 

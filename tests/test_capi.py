@@ -209,3 +209,14 @@ def test_generic_scan_host_checks(lib):
     assert fwd(None, None, None, None, 0, 17, 4, 3, F32, F64, F64, 0, None, 0, None) == 0
     rc = fwd(None, 1, 1, None, 1, 8, 4, 3, F32, F64, F64, 0, None, 0, None)
     assert rc == -1 and b"null" in lib.mogt_last_error()
+
+
+def test_generic_local_scan_host_checks(lib):
+    F32, F64 = _lib.MOGT_F32, _lib.MOGT_F64
+    fn = lib.mogt_affine_local_scan_generic
+    rc = fn(1, 1, 1, 1, 1, 8, 40, 3, 0, F32, F32, F32, None)
+    assert rc == -1 and b"block_size" in lib.mogt_last_error()
+    rc = fn(1, 1, None, 1, 1, 8, 40, 3, 4, F32, F32, F32, None)
+    assert rc == -1 and b"null" in lib.mogt_last_error()
+    assert fn(1, 1, 1, 1, 1, 8, 40, 3, 4, F32, 1, F32, None) == -1   # bf16 state
+    assert fn(None, None, None, None, 0, 8, 40, 3, 4, F32, F64, F64, None) == 0

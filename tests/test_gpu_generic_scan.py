@@ -275,3 +275,21 @@ def test_zz_generic_no_lookback_wait_gave_up(gpu):
     import mogt_amd.ops as ops
 
     assert ops.workspace_faults() == 0
+
+
+@pytest.mark.parametrize("R,block", [(40, 1), (40, 7), (64, 64), (100, 33)])
+def test_local_scan_ranks_above_32(gpu, R, block):
+    """triton_affine_local_scan beyond R = 32 (the generic kernel's block-local
+    pass): per-step prefixes and per-block summaries against the oracle's
+    local_scan, ragged tail block included."""
+    announce(f"generic local scan R={R} block={block}")
+    from mogt_amd import triton_scan
+
+    U, V = _stable(2, 155, R, 3, seed=R + block)
+    ref = so.local_scan(U, V, block_size=block)
+    out = triton_scan.triton_affine_local_scan(torch.from_numpy(U.astype(np.float32)).to(gpu),
+                                               torch.from_numpy(V.astype(np.float32)).to(gpu), block_size=block)
+    torch.cuda.synchronize()
+    for got, want in zip(out, ref):
+        assert got.dtype == torch.float32 and tuple(got.shape) == want.shape
+        assert rel_err(np64(got), want) <= FP32_TOL
