@@ -844,7 +844,8 @@ def check_vk_shapes(U: torch.Tensor, v: torch.Tensor, k: torch.Tensor) -> tuple[
     B, L, R, R2 = U.shape
     if R != R2 or tuple(v.shape) != (B, L, R) or tuple(k.shape[:2]) != (B, L):
         raise ValueError("U must be [B, L, R, R], v [B, L, R] and k [B, L, C]")
-    check_mfma_rank(R, "dense_scan")
+    if R > GENERIC_MAX_RANK:
+        raise ValueError(f"R = {R} not supported by the MI355X scan (R <= {GENERIC_MAX_RANK})")
     return B, L, R, k.shape[-1]
 
 
@@ -887,10 +888,15 @@ def dense_scan(A: torch.Tensor, Bm: torch.Tensor | None = None, *, v: torch.Tens
     if Bm is not None:
         return affine_scan(A, Bm, output_dtype=output_dtype)
     require_cuda("dense_scan", A, v, k)
-    check_vk_shapes(A, v, k)
+    _, _, R, _ = check_vk_shapes(A, v, k)
     output_dtype = output_dtype or v.dtype
     if output_dtype not in _DTYPE_CODE:
         raise ValueError(f"output dtype {output_dtype} not supported (float32 or bfloat16)")
+    if R > MFMA_MAX_RANK:
+        # above the matrix-core pipeline's rank: B_t = v_t k_t^T formed as fp32
+        # products (as the in-register form does) and scanned by the generic kernel
+        Bm = v.to(torch.float32).unsqueeze(-1) * k.to(torch.float32).unsqueeze(-2)
+        return affine_scan(A, Bm, output_dtype=output_dtype)
     return torch.ops.mogt.affine_scan_vk(A, v, k, output_dtype)
 
 

@@ -293,3 +293,22 @@ def test_local_scan_ranks_above_32(gpu, R, block):
     for got, want in zip(out, ref):
         assert got.dtype == torch.float32 and tuple(got.shape) == want.shape
         assert rel_err(np64(got), want) <= FP32_TOL
+
+
+def test_dense_scan_vk_rank_above_32(gpu):
+    """dense_scan(A, v=v, k=k) at R = 48: B_t = v_t k_t^T formed as fp32
+    products and scanned by the generic kernel, against the oracle."""
+    announce("generic dense_scan vk R=48")
+    import mogt_amd
+
+    U, _ = _stable(2, 200, 48, 1, seed=48)
+    g = synthetic.rng(5)
+    v = g.standard_normal((2, 200, 48)).astype(np.float32)
+    k = g.standard_normal((2, 200, 20)).astype(np.float32)
+    V = (v[..., :, None] * k[..., None, :]).astype(np.float64)
+    H_ref = so.affine_scan_sequential(U.astype(np.float32).astype(np.float64), V)
+    S = mogt_amd.dense_scan(torch.from_numpy(U.astype(np.float32)).to(gpu), v=torch.from_numpy(v).to(gpu),
+                            k=torch.from_numpy(k).to(gpu))
+    torch.cuda.synchronize()
+    assert S.dtype == torch.float32 and S.shape == (2, 200, 48, 20)
+    assert rel_err(np64(S), H_ref) <= FP32_TOL
