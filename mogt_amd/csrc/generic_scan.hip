@@ -34,7 +34,6 @@ constexpr int GS_EPT = 4;                          // state elements per thread
 constexpr int GS_MAX_ELEMS = GS_THREADS * GS_EPT;  // R * column-tile width
 constexpr int GS_MAX_R = 1024;
 constexpr int GS_ULDS_MAX_R = 64;                  // transitions staged in LDS up to this rank
-constexpr int GS_UPT = GS_ULDS_MAX_R * GS_ULDS_MAX_R / GS_THREADS;  // staged values per thread
 
 // A [batch][sequence][rows][cols] view of a device buffer (strides in elements).
 struct GView {
@@ -102,7 +101,9 @@ __host__ __device__ constexpr int gs_ld(int R) {
                static_cast<int>(16 / sizeof(TS)) + static_cast<int>(16 / sizeof(TS));
 }
 
-template <typename TS, bool ULDS>
+// ULDS: the step's transition staged through LDS (R <= 64), UPT of its values
+// per thread; PD: steps of operands in flight.
+template <typename TS, bool ULDS, int UPT, int PD>
 __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_scan_kernel(GParams p) {
     extern __shared__ __align__(16) unsigned char gs_smem[];
     // LDS: the step's transition U [R][ld] (staged variant) then two state
@@ -153,50 +154,56 @@ __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_s
         if (own[m]) sS[ocl[m] * ld + oi[m]] = v0;
     }
 
-    TS ureg[ULDS ? GS_UPT : 1];
-    TS vreg[GS_EPT];
-    auto fetch = [&](int64_t q) {
+    // Operands of the next PD steps are in flight: slot pp of the ring holds
+    // step s0 + pp of the current round and is refilled with step s0 + pp + PD
+    // once its values have been consumed.
+    TS ureg[PD][ULDS ? UPT : 1];
+    TS vreg[PD][GS_EPT];
+    auto fetch = [&](int64_t q, TS (&u)[ULDS ? UPT : 1], TS (&v)[GS_EPT]) {
         if constexpr (ULDS) {
             const bool ident = p.rev && q == 0;
             const int64_t tt = p.rev ? p.L - q : q;
 #pragma unroll
-            for (int m = 0; m < GS_UPT; ++m) {
+            for (int m = 0; m < UPT; ++m) {
                 const int idx = tid + m * GS_THREADS;
                 if (idx < R * R) {
                     const int rr = idx / R, cc = idx - rr * R;
-                    ureg[m] = ident ? TS(rr == cc ? 1 : 0)
-                                    : static_cast<const TS*>(p.tr.p)[at(p.tr, b, tt, rr, p.tr_c0 + cc)];
+                    u[m] = ident ? TS(rr == cc ? 1 : 0)
+                                 : static_cast<const TS*>(p.tr.p)[at(p.tr, b, tt, rr, p.tr_c0 + cc)];
                 }
             }
         }
         const int64_t ti = p.rev ? p.L - 1 - q : q;
 #pragma unroll
         for (int m = 0; m < GS_EPT; ++m)
-            vreg[m] = (ok[m] && oc[m] < p.cin) ? ld_code<TS>(p.in.p, at(p.in, b, ti, oi[m], oc[m]), p.in.code)
-                                               : TS(0);
+            v[m] = (ok[m] && oc[m] < p.cin) ? ld_code<TS>(p.in.p, at(p.in, b, ti, oi[m], oc[m]), p.in.code)
+                                            : TS(0);
     };
 
-    if (n > 0) fetch(q0);
+#pragma unroll
+    for (int pp = 0; pp < PD; ++pp)
+        if (pp < n) fetch(q0 + pp, ureg[pp], vreg[pp]);
     __syncthreads();
     int cur = 0;
-    for (int64_t s = 0; s < n; ++s) {
+    // one step: slot (u, v) holds step s; refilled with step s + PD
+    auto step = [&](int64_t s, TS (&u)[ULDS ? UPT : 1], TS (&v)[GS_EPT]) {
         const int64_t q = q0 + s;
         if constexpr (ULDS) {
 #pragma unroll
-            for (int m = 0; m < GS_UPT; ++m) {
+            for (int m = 0; m < UPT; ++m) {
                 const int idx = tid + m * GS_THREADS;
                 if (idx < R * R) {
                     const int rr = idx / R, cc = idx - rr * R;
                     // stored as the transition itself: row i, column k
-                    if (p.rev) sU[cc * ld + rr] = ureg[m];
-                    else sU[rr * ld + cc] = ureg[m];
+                    if (p.rev) sU[cc * ld + rr] = u[m];
+                    else sU[rr * ld + cc] = u[m];
                 }
             }
         }
         TS vin[GS_EPT];
 #pragma unroll
-        for (int m = 0; m < GS_EPT; ++m) vin[m] = vreg[m];
-        if (s + 1 < n) fetch(q + 1);  // next step's loads overlap this step's arithmetic
+        for (int m = 0; m < GS_EPT; ++m) vin[m] = v[m];
+        if (s + PD < n) fetch(q + PD, u, v);   // later steps' loads overlap this step's arithmetic
         if constexpr (ULDS) __syncthreads();
 
         const TS* Sc = sS + cur * Cb * ld;
@@ -204,8 +211,8 @@ __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_s
         const bool ident = p.rev && q == 0;
         const int64_t tt = p.rev ? p.L - q : q;
         const int64_t tout = (p.rev ? p.L - 1 - q : q) + p.shift;
-        // every element a thread owns sits in one column (the tile width divides
-        // the thread count), so each state value read serves all of them
+        // every element a thread owns sits in one column (the tile width
+        // divides the thread count), so each state value read serves all
         const TS* scol = Sc + ocl[0] * ld;
         TS a[GS_EPT];
 #pragma unroll
@@ -246,6 +253,17 @@ __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_s
         }
         __syncthreads();
         cur ^= 1;
+    };
+    if constexpr (PD == 1) {
+        for (int64_t s = 0; s < n; ++s) step(s, ureg[0], vreg[0]);
+    } else {
+        for (int64_t s0 = 0; s0 < n; s0 += PD) {
+#pragma unroll
+            for (int pp = 0; pp < PD; ++pp) {
+                if (s0 + pp >= n) break;   // uniform over the work-group
+                step(s0 + pp, ureg[pp], vreg[pp]);
+            }
+        }
     }
     if (!p.every) {
 #pragma unroll
@@ -299,12 +317,18 @@ int launch_generic(GParams p, int64_t batch, hipStream_t st, const char* what) {
     const bool ulds = p.R <= GS_ULDS_MAX_R;
     const int ld = gs_ld<TS>(p.R);
     const size_t lds = (static_cast<size_t>(ulds ? p.R * ld : 0) + 2 * static_cast<size_t>(p.Cb) * ld) * sizeof(TS);
-    if (ulds)
-        hipLaunchKernelGGL((generic_scan_kernel<TS, true>), dim3(static_cast<unsigned>(blocks)), dim3(GS_THREADS),
-                           lds, st, p);
+    const dim3 grid(static_cast<unsigned>(blocks)), block(GS_THREADS);
+    // transitions staged per thread: R^2 / 256 values (1, 4 or 16); the
+    // shallower the stash, the more steps in flight
+    if (p.R <= 16)
+        hipLaunchKernelGGL((generic_scan_kernel<TS, true, 1, 4>), grid, block, lds, st, p);
+    else if (p.R <= 32)
+        hipLaunchKernelGGL((generic_scan_kernel<TS, true, 4, 4>), grid, block, lds, st, p);
+    else if (ulds)
+        hipLaunchKernelGGL((generic_scan_kernel<TS, true, GS_ULDS_MAX_R * GS_ULDS_MAX_R / GS_THREADS, 1>), grid,
+                           block, lds, st, p);
     else
-        hipLaunchKernelGGL((generic_scan_kernel<TS, false>), dim3(static_cast<unsigned>(blocks)), dim3(GS_THREADS),
-                           lds, st, p);
+        hipLaunchKernelGGL((generic_scan_kernel<TS, false, 1, 2>), grid, block, lds, st, p);
     return check_launch(what);
 }
 
