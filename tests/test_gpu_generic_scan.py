@@ -312,3 +312,25 @@ def test_dense_scan_vk_rank_above_32(gpu):
     torch.cuda.synchronize()
     assert S.dtype == torch.float32 and S.shape == (2, 200, 48, 20)
     assert rel_err(np64(S), H_ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("sdt,tol", [(torch.float64, F64_TOL), (torch.float32, FP32_TOL)])
+def test_hand_backward_rank_above_64(gpu, sdt, tol):
+    """The reverse scan with U read transposed from memory (R > 64, not staged
+    in LDS), several chunks: affine_scan_sequential_backward against the
+    oracle."""
+    announce(f"generic reverse scan R=70 L=300 state {sdt}")
+    from mogt_amd import affine_scan as das
+
+    U, V = _stable(1, 300, 70, 3, seed=70)
+    G = synthetic.rng(8).standard_normal(V.shape)
+    tdt = torch.float64 if sdt == torch.float64 else torch.float32
+    if sdt == torch.float32:
+        U, V, G = (x.astype(np.float32).astype(np.float64) for x in (U, V, G))
+    gU_ref, gV_ref = so.affine_scan_sequential_backward(U, V, G)
+    gU, gV = das.affine_scan_sequential_backward(torch.from_numpy(U).to(gpu, tdt), torch.from_numpy(V).to(gpu, tdt),
+                                                 torch.from_numpy(G).to(gpu, tdt), state_dtype=sdt)
+    torch.cuda.synchronize()
+    assert gU.dtype == tdt and gV.dtype == tdt
+    assert rel_err(np64(gV), gV_ref) <= tol
+    assert rel_err(np64(gU), gU_ref) <= tol
