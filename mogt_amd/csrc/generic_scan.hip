@@ -103,7 +103,7 @@ __host__ __device__ constexpr int gs_ld(int R) {
 
 // ULDS: the step's transition staged through LDS (R <= 64), UPT of its values
 // per thread; PD: steps of operands in flight.
-template <typename TS, bool ULDS, int UPT, int PD>
+template <typename TS, bool ULDS, int UPT, int PD, int RM = 0>
 __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_scan_kernel(GParams p) {
     extern __shared__ __align__(16) unsigned char gs_smem[];
     // LDS: the step's transition U [R][ld] (staged variant) then two state
@@ -222,8 +222,7 @@ __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_s
             for (int m = 0; m < GS_EPT; ++m) a[m] += scol[oi[m]];
         } else if constexpr (ULDS) {
             typedef TS vec_t __attribute__((ext_vector_type(VE)));
-#pragma unroll 2
-            for (int k = 0; k < R; k += VE) {
+            auto kstep = [&](int k) {
                 const vec_t sv = *reinterpret_cast<const vec_t*>(scol + k);
 #pragma unroll
                 for (int m = 0; m < GS_EPT; ++m) {
@@ -231,6 +230,16 @@ __global__ __launch_bounds__(GS_THREADS, sizeof(TS) == 4 ? 3 : 2) void generic_s
 #pragma unroll
                     for (int e = 0; e < VE; ++e) a[m] += uv[e] * sv[e];
                 }
+            };
+            if constexpr (RM > 0) {
+                // rank bounded at compile time: the whole contraction unrolled,
+                // its LDS reads issued together
+#pragma unroll
+                for (int k = 0; k < RM; k += VE)
+                    if (k < R) kstep(k);
+            } else {
+#pragma unroll 2
+                for (int k = 0; k < R; k += VE) kstep(k);
             }
         } else {
             const TS* ut = static_cast<const TS*>(p.tr.p);
@@ -321,7 +330,7 @@ int launch_generic(GParams p, int64_t batch, hipStream_t st, const char* what) {
     // transitions staged per thread: R^2 / 256 values (1, 4 or 16); the
     // shallower the stash, the more steps in flight
     if (p.R <= 16)
-        hipLaunchKernelGGL((generic_scan_kernel<TS, true, 1, 4>), grid, block, lds, st, p);
+        hipLaunchKernelGGL((generic_scan_kernel<TS, true, 1, 4, 16>), grid, block, lds, st, p);
     else if (p.R <= 32)
         hipLaunchKernelGGL((generic_scan_kernel<TS, true, 4, 4>), grid, block, lds, st, p);
     else if (ulds)
