@@ -34,6 +34,8 @@ METRIC = "scan core ms + HBM GB/s at D768 L=32768; MOGT 4-layer fwd ms"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 REF_TRITON_CORE_MS_L4 = 5.48   # reference hybrid core @ L=32768 (R=16, C=48, NVIDIA L4)
+# rocprofv3 profile of the headline kernel (trace + FETCH_SIZE / WRITE_SIZE)
+HEADLINE_PROFILE = "diag_scan_d768_l32768_fp32.md"
 
 
 def parse_args():
@@ -43,17 +45,21 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true")
-    p.add_argument("--only", choices=["diag", "coupled", "rank1", "dense", "swiglu", "backbone", "all"],
-                   default="all",
-                   help="after the headline: every extra (all), none (diag), or only the coupled "
-                        "mixer scan, rank-1 (configs[2]), dense (core shape and configs[3]) or "
-                        "backbone (configs[4] forward and training step) lines")
+    p.add_argument("--only", default="all",
+                   help="after the headline: every extra (all), none (diag), or a comma list of "
+                        "coupled (the mixer scan), rank1 (configs[2]), dense (core shape and configs[3]), "
+                        "swiglu, backbone (configs[4] forward and training step)")
     p.add_argument("--tile", default=None,
                    help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC calibration)")
-    return p.parse_args()
+    args = p.parse_args()
+    groups = {"diag", "coupled", "rank1", "dense", "swiglu", "backbone", "all"}
+    args.only = set(args.only.split(","))
+    if not args.only <= groups:
+        p.error(f"--only takes a comma list of {sorted(groups)}")
+    return args
 
 
 def log(msg: str) -> None:
@@ -376,20 +382,36 @@ def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48, tile=None):
 
 def _cayley_transport_gpu(torch, n_seq, L, d, seed):
     """U_t = sigmoid(N(2,1)) * (I - W)^{-1} (I + W), W = T - T^T, T strictly upper
-    N(0, 0.05): the configs[3] distribution, generated on the GPU."""
+    N(0, 0.05): the configs[3] distribution, generated on the GPU (the Cayley
+    solve on this library's connection-map kernel, which the GPU tests check
+    against torch.linalg.solve; a few launches instead of torch's batched solve,
+    so the inputs are made quickly also under a counter-collecting profiler)."""
+    from mogt_amd import ops
+
     gen = torch.Generator(device="cuda").manual_seed(seed)
     dev = torch.device("cuda:0")
-    U = torch.empty(n_seq, L, d, d, device=dev)
-    eye = torch.eye(d, device=dev)
-    for s0 in range(0, L, 4096):
-        s1 = min(L, s0 + 4096)
-        T = torch.triu(torch.randn(n_seq, s1 - s0, d, d, generator=gen, device=dev) * 0.05, 1)
-        W = T - T.transpose(-1, -2)
-        gate = torch.sigmoid(torch.randn(n_seq, s1 - s0, 1, 1, generator=gen, device=dev) + 2.0)
-        U[:, s0:s1] = torch.linalg.solve(eye - W, eye + W) * gate
+    T = torch.triu(torch.randn(n_seq, L, d, d, generator=gen, device=dev) * 0.05, 1)
+    W = T - T.transpose(-1, -2)
+    del T
+    gate = torch.sigmoid(torch.randn(n_seq, L, 1, 1, generator=gen, device=dev) + 2.0)
+    U = ops.connection_map(W, "cayley", scale=2.0) * gate
+    del W
     v = torch.randn(n_seq, L, d, 1, generator=gen, device=dev)
     k = torch.nn.functional.normalize(torch.randn(n_seq, L, 1, d, generator=gen, device=dev), dim=-1)
     return U, (v * k).contiguous(), v[..., 0].contiguous(), k[..., 0, :].contiguous()
+
+
+def _unit_spectral(torch, U):
+    """U / max(1, 1.1 * ||U||_2), the norm from power iteration on U^T U (a
+    few dozen batched products rather than a batched SVD)."""
+    G = torch.matmul(U.transpose(-1, -2).contiguous(), U)
+    x = torch.ones(*U.shape[:-1], 1, device=U.device, dtype=U.dtype)
+    x[..., 1::2, :] = -1.0
+    for _ in range(30):
+        x = torch.matmul(G, x)
+        x = x / x.norm(dim=-2, keepdim=True)
+    s = torch.matmul(G, x).norm(dim=-2, keepdim=True).sqrt()
+    return U / (1.1 * s).clamp(min=1.0)
 
 
 def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets=2, vk=False):
@@ -422,7 +444,7 @@ def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets
     else:
         gen = torch.Generator(device="cuda").manual_seed(5)
         U0 = torch.eye(R, device=dev) + 0.05 * torch.randn(B, L, R, R, generator=gen, device=dev)
-        U0 = U0 / torch.linalg.matrix_norm(U0, ord=2).clamp(min=1.0)[..., None, None]
+        U0 = _unit_spectral(torch, U0)
         V0 = torch.randn(B, L, R, C, generator=gen, device=dev)
     bufs = [(U0.clone(), V0.clone(), torch.empty(B, L, R, C, device=dev)) for _ in range(sets)]
     del U0, V0
@@ -454,7 +476,7 @@ def measure_generic(torch, lib, ops, B, L, R, C, steps, warmup, f64=True, sets=2
     gen = torch.Generator(device="cuda").manual_seed(9)
     U0 = torch.eye(R, device=dev, dtype=dt) + (0.3 / R ** 0.5) * torch.randn(B, L, R, R, generator=gen,
                                                                              device=dev, dtype=dt)
-    U0 = U0 / torch.linalg.matrix_norm(U0, ord=2).clamp(min=1.0)[..., None, None]
+    U0 = _unit_spectral(torch, U0)
     V0 = torch.randn(B, L, R, C, generator=gen, device=dev, dtype=dt)
     bufs = [(U0.clone(), V0.clone(), torch.empty(B, L, R, C, device=dev, dtype=dt)) for _ in range(sets)]
     del U0, V0
@@ -655,21 +677,36 @@ def cpu_baseline(L=32768, D=768):
     }
 
 
-def read_traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    scaled by a plain copy's counter reading); kept as key=value text."""
+def read_traffic(name: str, manifest: dict):
+    """HBM bytes per launch of the headline kernel, measured with rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counter reading) and kept
+    as key=value lines in a profile.  The profile names the source hashes of the
+    kernel it measured (``kernel_sources=``); the figure is used only when they
+    equal the loaded library's, i.e. the profile came from this kernel's build.
+    Returns (bytes or None, provenance dict)."""
     path = ROOT / "profiles" / name
+    info = {"file": f"profiles/{name}"}
     if not path.exists():
-        return None
+        info["status"] = "missing"
+        return None, info
     kv = {}
     for line in path.read_text().splitlines():
-        if "=" in line and not line.lstrip().startswith("#"):
+        if "=" in line and not line.lstrip().startswith(("#", "|", "`")):
             k, v = line.split("=", 1)
             kv[k.strip()] = v.strip()
+    srcs = dict(item.split(":", 1) for item in kv.get("kernel_sources", "").split(",") if ":" in item)
+    stale = sorted(k for k, h in srcs.items() if manifest.get(k) != h)
+    if not srcs or stale:
+        info["status"] = f"refused: profile taken from other sources ({', '.join(stale) or 'none named'})"
+        return None, info
     try:
-        return float(kv["hbm_bytes_per_launch"])
+        traffic = float(kv["hbm_bytes_per_launch"])
     except (KeyError, ValueError):
-        return None
+        info["status"] = "no hbm_bytes_per_launch"
+        return None, info
+    info.update(status="matches this build", kernel_sources=kv["kernel_sources"],
+                profile_avg_us=float(kv.get("avg_us", "nan")))
+    return traffic, info
 
 
 def main():
@@ -717,8 +754,9 @@ def main():
     log(f"headline: {head['ms'] * 1e3:.1f} us/launch, {head['gbs']:.0f} GB/s")
 
     extras = {}
-    if not args.no_extras and args.only != "diag":
-        full = args.only == "all"
+    only = args.only
+    if not args.no_extras and only != {"diag"}:
+        full = "all" in only
         if full:
             for L in (8192, 16384):
                 r = measure_diag(torch, lib, ops, L, torch.float32, torch.float32, args.steps,
@@ -742,13 +780,13 @@ def main():
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                 "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
-        if full or args.only == "coupled":
+        if full or "coupled" in only:
             r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
             extras["coupled_rank_scan_r16c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                 "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
-        if full or args.only == "rank1":
+        if full or "rank1" in only:
             r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
             r3 = measure_rank1(torch, lib, ops, args.steps, args.warmup, path=2)
             extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
@@ -757,7 +795,7 @@ def main():
                 "three_launch_us": round(r3["ms"] * 1e3, 2),
                 "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out); us: one launch "
                         "(carries exchanged between work-groups), three_launch_us: summaries, carries, outputs"}
-        if full or args.only == "dense":
+        if full or "dense" in only:
             r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
             extras["dense_affine_r16_c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
@@ -779,7 +817,7 @@ def main():
                 "TFLOP/s": round(r["tflops"], 2), "frac_fp32_matrix_peak": round(r["tflops"] / 157.3, 4),
                 "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
                         "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
-        if full or args.only == "dense":
+        if full or "dense" in only:
             r = measure_generic(torch, lib, ops, 1, 32768, 16, 48, max(3, args.steps // 10), 1)
             extras["generic_affine_f64_r16_c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
@@ -809,7 +847,7 @@ def main():
                 "note": "chunked_linear_cross_entropy fwd+bwd, chunk 4096, bf16 hidden, fp32 tied weight; "
                         "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
                         "torch ops on the same GPU"}
-        if full or args.only == "swiglu":
+        if full or "swiglu" in only:
             r = measure_swiglu(torch, args.steps, args.warmup)
             extras["swiglu_gate_gemm_32768x768_to_3072_bf16"] = {
                 "us": round(r["ms"] * 1e3, 2), "TFLOP/s": round(r["tflops"], 1),
@@ -817,7 +855,7 @@ def main():
                 "unfused_us": round(r["ms_unfused"] * 1e3, 2), "library_gemm_only_us": round(r["ms_gemm_only"] * 1e3, 2),
                 "note": "FFN gate silu(x w1^T) * (x w2^T) as one GEMM with the gate in its epilogue vs the "
                         "library GEMM against [w1; w2] + the silu_mul row kernel (model_mogt.py:29-30)"}
-        if full or args.only == "backbone":
+        if full or "backbone" in only:
             from mogt_amd import gemm_tuning
 
             # the libraries' default GEMM choice first, then the tuned table
@@ -874,7 +912,7 @@ def main():
               file=sys.stderr)
         sys.exit(3)
 
-    traffic = read_traffic("diag_scan_d768_l32768_fp32_traffic.txt")
+    traffic, traffic_info = read_traffic(HEADLINE_PROFILE, mogt_amd._lib.build_manifest())
     achieved = head["gbs"]
     line = {
         "metric": METRIC,
@@ -908,6 +946,8 @@ def main():
                          if cpu else None),
         "scan_core_us": round(head["ms"] * 1e3, 3),
         "lookback_give_ups": give_ups,
+        "build_id": mogt_amd._lib.build_id(),
+        "traffic_profile": traffic_info,
         "reference_triton_core_ms_L4": REF_TRITON_CORE_MS_L4,
         "extras": extras,
     }

@@ -47,6 +47,14 @@ const char* mogt_last_error(void);
 /* ABI version of the loaded library (bumped on incompatible changes). */
 int mogt_abi_version(void);
 
+/* Build identity: "name:hash;name:hash;..." — a 12-hex-digit SHA-256 prefix
+ * of every source file the library was compiled from (the .hip and .h files
+ * of csrc/ and this header) and of the compiler flags (name "flags").  Profiles of a
+ * kernel record the hashes of the sources behind it, so a measurement can be
+ * matched to the build it came from.  No counterpart in the reference (its
+ * kernels are JIT-compiled by Triton from the Python source).              */
+const char* mogt_build_manifest(void);
+
 /* Health of a single-pass scan workspace (the diag, coupled and reverse
  * scans' look-back buffer): *count receives the number of bounded waits that
  * gave up in launches on it since it was zero-filled.  It must be 0; a

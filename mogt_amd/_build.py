@@ -8,6 +8,7 @@ the ``.so`` travels with the source tree to the GPU host.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -41,6 +42,33 @@ FILE_FLAGS = {
 }
 
 
+def source_manifest() -> dict[str, str]:
+    """Build identity: ``name -> sha256[:12]`` of every source the library is
+    compiled from (``csrc/*.hip``, ``csrc/*.h``, the public header) plus the
+    compiler flags (key ``flags``).  The same string is compiled into the
+    library (``mogt_build_manifest``), so a loaded library can be matched
+    against the tree, and a profile taken from one build can name the exact
+    sources its kernels came from."""
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [INCLUDE / "mogt_scan.h"]
+    out = {f.name: hashlib.sha256(f.read_bytes()).hexdigest()[:12] for f in files}
+    flags = repr((HIPCC_FLAGS, sorted(FILE_FLAGS.items())))
+    out["flags"] = hashlib.sha256(flags.encode()).hexdigest()[:12]
+    return out
+
+
+def manifest_string(manifest: dict[str, str]) -> str:
+    return ";".join(f"{k}:{v}" for k, v in sorted(manifest.items()))
+
+
+def parse_manifest(text: str) -> dict[str, str]:
+    return dict(item.split(":", 1) for item in text.split(";") if ":" in item)
+
+
+def build_id(manifest: dict[str, str]) -> str:
+    """Short hash of a whole manifest (one id per library build)."""
+    return hashlib.sha256(manifest_string(manifest).encode()).hexdigest()[:16]
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -52,8 +80,9 @@ def lib_path() -> Path:
     return LIBDIR / LIBNAME
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, defines: tuple[str, ...] = ()) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), *defines, f"-I{INCLUDE}", "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -78,8 +107,10 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objs = [objdir / (s.stem + ".o") for s in srcs]
     jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 2))
+    manifest = manifest_string(source_manifest())
+    defines = [(f'-DMOGT_BUILD_MANIFEST="{manifest}"',) if s.name == "capi.hip" else () for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(_compile, srcs, objs))
+        list(ex.map(_compile, srcs, objs, defines))
     out = lib_path()
     tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]

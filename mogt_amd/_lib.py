@@ -18,7 +18,7 @@ MOGT_F64 = 2
 MOGT_F16 = 3
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -30,6 +30,7 @@ _c_float = ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
     "mogt_last_error": (ctypes.c_char_p, []),
     "mogt_abi_version": (_c_int, []),
+    "mogt_build_manifest": (ctypes.c_char_p, []),
     "mogt_workspace_faults": (_c_int, [_c_void_p, _c_size, ctypes.POINTER(ctypes.c_uint32), _c_void_p]),
     "mogt_diag_scan_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
     "mogt_diag_scan_fwd": (
@@ -205,6 +206,16 @@ def check(rc: int, what: str) -> None:
         if rc == -1:
             raise ValueError(f"{what}: {msg}")
         raise MogtError(f"{what} failed ({rc}): {msg}")
+
+
+def build_manifest() -> dict[str, str]:
+    """``name -> hash`` of the sources and flags the loaded library was built from."""
+    return _build.parse_manifest(load().mogt_build_manifest().decode())
+
+
+def build_id() -> str:
+    """One short id for the loaded library's build (hash of its manifest)."""
+    return _build.build_id(build_manifest())
 
 
 def exported_symbols() -> list[str]:

@@ -31,7 +31,14 @@ int check_launch(const char* what) {
 
 extern "C" const char* mogt_last_error(void) { return mogt::g_last_error; }
 
-extern "C" int mogt_abi_version(void) { return 9; }
+extern "C" int mogt_abi_version(void) { return 10; }
+
+// "name:sha256[:12];..." of the sources and compiler flags this library was
+// built from, passed in by the build script (mogt_amd/_build.py).
+#ifndef MOGT_BUILD_MANIFEST
+#define MOGT_BUILD_MANIFEST ""
+#endif
+extern "C" const char* mogt_build_manifest(void) { return MOGT_BUILD_MANIFEST; }
 
 extern "C" int mogt_workspace_faults(const void* workspace, size_t workspace_bytes, uint32_t* count,
                                      void* stream) {

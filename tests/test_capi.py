@@ -38,6 +38,19 @@ def test_abi_version(lib):
     assert lib.mogt_abi_version() == _lib.ABI_VERSION
 
 
+def test_library_built_from_these_sources(lib):
+    # the manifest compiled into the library names every source and its hash;
+    # a library older than any source (or built with other flags) fails here
+    from mogt_amd import _build
+
+    built = _lib.build_manifest()
+    tree = _build.source_manifest()
+    assert set(built) == set(tree)
+    stale = sorted(k for k in tree if built[k] != tree[k])
+    assert not stale, f"library built from other sources: {stale} (rebuild)"
+    assert _lib.build_id() == _build.build_id(tree)
+
+
 def test_workspace_queries_are_host_only(lib):
     n = lib.mogt_diag_scan_workspace_bytes(1, 32768, 768, _lib.MOGT_F32)
     assert 256 < n < 64 << 20

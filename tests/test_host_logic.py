@@ -114,3 +114,51 @@ def test_affine_scan_dropins_need_a_gpu():
         das.affine_scan_sequential(U, V, state_dtype=torch.int64)
     with pytest.raises(ValueError):
         das.affine_scan_block_reference(U, V, block_size=0)
+
+
+def test_bench_traffic_needs_a_profile_of_this_build(tmp_path, monkeypatch):
+    """bench.py takes the headline's HBM traffic only from a profile whose
+    kernel-source hashes equal the loaded library's manifest."""
+    import bench
+
+    prof = tmp_path / "profiles"
+    prof.mkdir()
+    (prof / "p.md").write_text(
+        "# profile\n\n| `k` | 1 |\n\nkernel_sources=diag_kernel.h:aaaa,common.h:bbbb,flags:cccc\n"
+        "avg_us=56.8\nhbm_bytes_per_launch=307157755\n")
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    manifest = {"diag_kernel.h": "aaaa", "common.h": "bbbb", "flags": "cccc", "rank1_scan.hip": "dddd"}
+    t, info = bench.read_traffic("p.md", manifest)
+    assert t == 307157755.0 and info["status"] == "matches this build"
+    t, info = bench.read_traffic("p.md", dict(manifest, **{"common.h": "eeee"}))
+    assert t is None and "common.h" in info["status"]
+    t, info = bench.read_traffic("p.md", dict(manifest, flags="ffff"))
+    assert t is None and "flags" in info["status"]
+    t, info = bench.read_traffic("missing.md", manifest)
+    assert t is None and info["status"] == "missing"
+    (prof / "q.md").write_text("avg_us=1\nhbm_bytes_per_launch=5\n")   # names no sources
+    t, info = bench.read_traffic("q.md", manifest)
+    assert t is None and "refused" in info["status"]
+
+
+def test_rocprof_summary_groups_and_calibrates(tmp_path):
+    """The profile summariser groups dispatches by kernel and launch shape and
+    scales the counters by the process's first five copy dispatches."""
+    import csv
+
+    from mogt_amd import rocprof_summary as rs
+
+    assert rs.short_name("void mogt::diag_scan_kernel<0, float, 2>(float const*, int)") == \
+        "diag_scan_kernel<0, float, 2>"
+    rows = []
+    for i in range(5):      # calibration: 256 MiB copied, counter reads half of it
+        rows.append(dict(Counter_Name="FETCH_SIZE", Counter_Value="131072", Dispatch_Id=str(i + 1),
+                         Kernel_Name="__amd_rocclr_copyBuffer", Workgroup_Size="512", Grid_Size="131072"))
+    rows.append(dict(Counter_Name="FETCH_SIZE", Counter_Value="999999", Dispatch_Id="9",
+                     Kernel_Name="__amd_rocclr_copyBuffer", Workgroup_Size="512", Grid_Size="262144"))
+    for i, v in enumerate((100.0, 200.0)):
+        rows.append(dict(Counter_Name="FETCH_SIZE", Counter_Value=str(v), Dispatch_Id=str(10 + i),
+                         Kernel_Name="void mogt::k<1>(int)", Workgroup_Size="256", Grid_Size="2048"))
+    per, copy = rs.counter_table(rows, "FETCH_SIZE")
+    assert copy == 131072.0                      # the later, larger copy is not the calibration
+    assert per[("k<1>", 8, 256)] == 150.0
