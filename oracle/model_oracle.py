@@ -41,6 +41,9 @@ def block_forward(p: dict, x: torch.Tensor, prefix: torch.Tensor | None, cfg: di
     transport_gate_scale, mogt_residual_scale, mogt_ffn_residual_scale, r, and
     residual_gate for mogt_residual_gate_enabled).
 
+    ``scan_impl = "transport_triton"`` (or ``fast_throughput_mode``) selects the
+    reference's transport-only mode; every other scan_impl is the affine scan.
+
     ``ref_casts=False`` keeps every intermediate in x's dtype (the oracle of
     the GPU paths).  ``ref_casts=True`` reproduces the reference's own float32
     steps for any input dtype: RMSNorm statistics (:19), the connection map
@@ -98,7 +101,17 @@ def block_forward(p: dict, x: torch.Tensor, prefix: torch.Tensor | None, cfg: di
         V = V * vg.to(V.dtype)
         if cfg.get("couple_forget_to_value_gate", False):
             U = U * (1.0 - vg).to(U.dtype)
-    if ref_casts or (torch.is_grad_enabled() and (U.requires_grad or V.requires_grad)):
+    if cfg.get("scan_impl") == "transport_triton" or cfg.get("fast_throughput_mode"):
+        # transport-only mode (model_mogt.py:187-192): V_t = Y_t V_raw with the
+        # prefix product Y_t = U_t Y_{t-1}, Y_0 = I (triton_scan.py:37-48), in
+        # U's dtype as the Triton kernel keeps it
+        Y = U.new_empty(U.shape)
+        acc = torch.eye(r, dtype=U.dtype).expand(B, r, r)
+        for t in range(L):
+            acc = torch.matmul(U[:, t], acc)
+            Y[:, t] = acc
+        H = torch.matmul(Y, V.to(Y.dtype))
+    elif ref_casts or (torch.is_grad_enabled() and (U.requires_grad or V.requires_grad)):
         # the reference's bmm loop: float32 state with ref_casts; otherwise a
         # float64 state, differentiable for autograd checks of the GPU backward
         from .torch_ref import affine_scan_sequential_torch

@@ -46,9 +46,14 @@ def state_dict(tag: str, strip: str = "", dtype=torch.float64) -> dict[str, torc
     """The parameters of a fixture group (everything but its inputs/outputs),
     keys with ``strip`` removed from the front."""
     io = {"ids", "out", "x", "prefix", "labels", "logits", "loss", "logits_chunked", "loss_chunked",
-          "hidden", "loss_fused", "grad_hidden", "grad_weight", "block0_out", "block1_out"}
+          "hidden", "loss_fused", "grad_hidden", "grad_weight", "block0_out", "block1_out", "w"}
     return {k[len(strip):]: v for k, v in group(tag, dtype).items()
-            if k not in io and k.startswith(strip)}
+            if k not in io and not k.startswith("grad/") and k.startswith(strip)}
+
+
+def grads(tag: str, dtype=torch.float64) -> dict[str, torch.Tensor]:
+    """Parameter gradients stored with a fixture group (``grad/<name>``)."""
+    return {k[len("grad/"):]: v for k, v in group(tag, dtype).items() if k.startswith("grad/")}
 
 
 def meta(tag: str):

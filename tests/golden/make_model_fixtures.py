@@ -37,6 +37,22 @@ CPU scan, which every other scan_impl evaluates to fp32 rounding):
 * ``ga``   -- under CPU bf16 autocast, the coupled block's gate logits, the
   ``phi_val`` output and the (U, V) pair handed to the scan: the dtype flow of
   model_mogt.py:166-182 (``V_t_raw * value_gate.to(V_t_raw.dtype)`` in bf16).
+* ``tt``   -- a block in ``fast_throughput_mode`` (``scan_impl =
+  "transport_triton"``, model_mogt.py:71-74, 187-192): ``V_t = Y_t V_raw`` with
+  ``Y_t = U_t Y_{t-1}``, ``Y_0 = I``.  The Triton kernel (triton_scan.py:13-51,
+  151-175) needs a GPU and fixes R = 16 at launch, so this block has r = 16
+  (d_model 64), and its recurrence is evaluated by the reference's own prefix
+  product, ``affine_scan_sequential(U, 0, return_prefix=True)``
+  (affine_scan.py:43-55), in place of the Triton launch.
+* ``ck``   -- a 3-layer MOGTModel in training mode with
+  ``gradient_checkpointing = True`` and ``checkpoint_every_n = 2``
+  (model_mogt.py:278-285), the backbone wiring of ``bb``, blocks selecting
+  ``parallel_reference``, ``block_reference`` (block size 7, doubling carry
+  scan) and ``sequential`` (model_mogt.py:204-221); the output, the loss
+  ``sum(out * w)`` for seeded ``w`` and every parameter's gradient.
+* ``pr``, ``br`` -- single blocks on the dense (non-identity) transport with
+  ``scan_impl = "parallel_reference"`` (matrix_exp) and ``"block_reference"``
+  (Cayley, ``scan_block_size = 5``, ``block_carry_scan = "doubling"``).
 """
 from __future__ import annotations
 
@@ -250,6 +266,113 @@ def main(ref: Path) -> None:
     arrays.update(_arrays_of("ga", {k: captured[k] for k in ("z", "v_raw", "U", "V")}))
     meta["ga"] = {"damping": 0.98, "dtypes": {k: str(captured[k].dtype) for k in ("z", "v_raw", "U", "V")},
                   "torch": torch.__version__}
+
+    # ---- tt: transport-only mode (fast_throughput_mode) ----------------------
+    torch.set_default_dtype(torch.float64)
+
+    def fused_prefix(U):
+        """triton_fused_scan's recurrence Y_t = U_t Y_{t-1}, Y_0 = I
+        (triton_scan.py:37-48), as the reference's own prefix product."""
+        Y, _ = mm.affine_scan_sequential(U, torch.zeros_like(U[..., :1]), state_dtype=U.dtype,
+                                         output_dtype=U.dtype, return_prefix=True)
+        return Y
+
+    import types
+    sys.modules["triton_scan"] = types.SimpleNamespace(triton_fused_scan=fused_prefix)
+    torch.manual_seed(5)
+    DT, RT = 64, 16
+    blk = mm.MOGTBlock(d_model=DT, r=RT)
+    blk.ffn = mm.SwiGLU(DT, 2 * DT)
+    blk.fast_throughput_mode = True
+    blk.connection_impl = "matrix_exp"
+    blk.connection_damping = 0.999
+    blk.phi_transport_gate = torch.nn.Linear(DT, RT, bias=True)
+    blk.transport_gate_mode = "multiply"
+    blk.phi_value_gate = torch.nn.Linear(DT, 1, bias=True)
+    blk.value_gate_input_mode = "current"
+    blk.couple_forget_to_value_gate = True
+    _reseed_weights(blk, gen)
+    blk.eval()
+    x = _f32(torch.randn(B, 24, DT, generator=gen))
+    with torch.no_grad():
+        out = blk(x)
+    del sys.modules["triton_scan"]
+    arrays.update(_arrays_of("tt", blk.state_dict()))
+    arrays["tt/x"] = x.float().numpy()
+    arrays["tt/out"] = out.numpy()
+    meta["tt"] = {"d_model": DT, "r": RT, "ffn_hidden": 2 * DT, "fast_throughput_mode": True,
+                  "connection_impl": "matrix_exp", "connection_damping": 0.999, "transport_gate": RT,
+                  "transport_gate_mode": "multiply", "value_gate": 1, "value_gate_input_mode": "current",
+                  "couple_forget_to_value_gate": True}
+
+    # ---- ck: gradient checkpointing, scan_impl per block ---------------------
+    torch.manual_seed(6)
+    model = mm.MOGTModel(vocab_size=VOCAB, d_model=D, num_layers=3, r=R)
+    impls = ["parallel_reference", "block_reference", "sequential"]
+    for i, blk in enumerate(model.blocks):
+        blk.ffn = mm.SwiGLU(D, 4 * D)
+        blk.scan_impl = impls[i]
+        blk.scan_block_size = 7
+        blk.block_carry_scan = "doubling"
+        blk.connection_impl = "identity"
+        blk.connection_damping = 1.0
+        blk.phi_value_gate = torch.nn.Linear(3 * D, R, bias=True)
+        blk.value_gate_input_mode = "current_prev_prefix"
+        blk.couple_forget_to_value_gate = True
+    model.prefix_condition_position = 1
+    model.gradient_checkpointing = True
+    model.checkpoint_every_n = 2
+    _reseed_weights(model, gen)
+    model.train()
+    ids = torch.randint(0, VOCAB, (B, L), generator=gen)
+    wts = _f32(torch.randn(B, L, D, generator=gen))
+    calls = [0, 0, 0]
+    hooks = [blk.register_forward_pre_hook(lambda m, a, i=i: calls.__setitem__(i, calls[i] + 1))
+             for i, blk in enumerate(model.blocks)]
+    y = model(ids)
+    loss = (y * wts).sum()
+    loss.backward()
+    for h in hooks:
+        h.remove()
+    assert calls == [2, 1, 2], calls     # blocks 0 and 2 recomputed in backward
+    arrays.update(_arrays_of("ck", model.state_dict()))
+    arrays.update({"ck/ids": ids.numpy(), "ck/w": wts.float().numpy(), "ck/out": y.detach().numpy(),
+                   "ck/loss": loss.detach().numpy()})
+    no_grad = []
+    for name, p_ in model.named_parameters():
+        if p_.grad is None:          # phi_conn: the identity connection ignores A
+            no_grad.append(name)
+        else:
+            arrays[f"ck/grad/{name}"] = p_.grad.numpy()
+    meta["ck"] = {"params_without_grad": no_grad,"layers": 3, "ffn_hidden": 4 * D, "prefix_condition_position": 1,
+                  "gradient_checkpointing": True, "checkpoint_every_n": 2, "scan_impl": impls,
+                  "scan_block_size": 7, "block_carry_scan": "doubling", "block_calls": calls}
+
+    # ---- pr, br: parallel / block reference scans on a dense transport -------
+    def dense_case(tag: str, cfg: dict) -> None:
+        torch.manual_seed(7)
+        blk = mm.MOGTBlock(d_model=D, r=R)
+        blk.ffn = mm.SwiGLU(D, 4 * D)
+        for k_, v_ in cfg.items():
+            setattr(blk, k_, v_)
+        blk.phi_value_gate = torch.nn.Linear(2 * D, R, bias=True)
+        blk.value_gate_input_mode = "current_prev"
+        blk.couple_forget_to_value_gate = True
+        _reseed_weights(blk, gen)
+        blk.eval()
+        x = _f32(torch.randn(B, 24, D, generator=gen))
+        with torch.no_grad():
+            out = blk(x)
+        arrays.update(_arrays_of(tag, blk.state_dict()))
+        arrays[f"{tag}/x"] = x.float().numpy()
+        arrays[f"{tag}/out"] = out.numpy()
+        meta[tag] = dict(cfg, value_gate=R, value_gate_input_mode="current_prev",
+                         couple_forget_to_value_gate=True)
+
+    dense_case("pr", {"scan_impl": "parallel_reference", "connection_impl": "matrix_exp",
+                      "connection_damping": 0.999})
+    dense_case("br", {"scan_impl": "block_reference", "connection_impl": "cayley", "connection_damping": 0.99,
+                      "scan_block_size": 5, "block_carry_scan": "doubling"})
 
     np.savez_compressed(HERE / "model_fixtures.npz", **arrays)
     manifest = {"meta": meta,

@@ -166,3 +166,62 @@ def test_lm_losses_oracle_matches_reference():
     assert abs(loss - float(g["loss_fused"])) < FP32_GAP * abs(loss)
     assert rel_err(gh, g["grad_hidden"].numpy()) < 1e-5
     assert rel_err(gw, g["grad_weight"].numpy()) < 1e-5
+
+
+def _cfg_of(m: dict, r: int = R) -> dict:
+    cfg = _block_cfg(m)
+    cfg["r"] = r
+    for k in ("scan_impl", "fast_throughput_mode"):
+        if k in m:
+            cfg[k] = m[k]
+    return cfg
+
+
+def test_transport_only_oracle_matches_reference():
+    """fast_throughput_mode / scan_impl="transport_triton" (model_mogt.py:71-74,
+    187-192): V_t = (U_t ... U_1) V_raw, not the affine recurrence.  Exact with
+    the reference's float32 steps; the affine scan in its place fails the pin."""
+    g = fx.group("tt")
+    m = fx.meta("tt")
+    cfg = _cfg_of(m, r=m["r"])
+    for ref_casts, tol in ((True, EXACT), (False, FP32_GAP)):
+        y = mo.block_forward(fx.state_dict("tt"), g["x"], None, cfg, ref_casts=ref_casts)
+        assert rel_err(y.numpy(), g["out"].numpy()) < tol, f"ref_casts={ref_casts}"
+    affine = {k: v for k, v in cfg.items() if k != "fast_throughput_mode"}
+    y = mo.block_forward(fx.state_dict("tt"), g["x"], None, affine, ref_casts=True)
+    assert rel_err(y.numpy(), g["out"].numpy()) > 1e-3
+
+
+@pytest.mark.parametrize("tag", ["pr", "br"])
+def test_parallel_and_block_reference_scans_match_the_recurrence(tag):
+    """scan_impl="parallel_reference" (affine_scan_doubling) and
+    "block_reference" (affine_scan_block_reference, block 5, doubling carries)
+    on a dense transport (model_mogt.py:204-221): the reference evaluates them
+    with a float32 state, so they agree with the sequential recurrence to
+    float32 rounding."""
+    g = fx.group(tag)
+    cfg = _cfg_of(fx.meta(tag))
+    for ref_casts in (True, False):
+        y = mo.block_forward(fx.state_dict(tag), g["x"], None, cfg, ref_casts=ref_casts)
+        assert rel_err(y.numpy(), g["out"].numpy()) < FP32_GAP, f"ref_casts={ref_casts}"
+
+
+def test_checkpointed_backbone_oracle_matches_reference():
+    """A 3-layer MOGTModel trained with gradient checkpointing every 2 blocks
+    (model_mogt.py:278-285; blocks 0 and 2 recomputed in the backward) and one
+    scan_impl per block: output, loss and every parameter's gradient against
+    float64 autograd of the oracle."""
+    g = fx.group("ck")
+    m = fx.meta("ck")
+    assert m["block_calls"] == [2, 1, 2]
+    cfg = _cfg_of(fx.meta("bb")["blocks"][0])
+    st = {k: v.clone().requires_grad_() for k, v in fx.state_dict("ck").items()}
+    y = mo.model_forward(st, g["ids"], m["layers"], cfg, prefix_position=m["prefix_condition_position"])
+    assert rel_err(y.detach().numpy(), g["out"].numpy()) < FP32_GAP
+    loss = (y * g["w"]).sum()
+    assert abs(float(loss.detach()) - float(g["loss"])) < FP32_GAP * abs(float(g["loss"])) * 10
+    loss.backward()
+    want = fx.grads("ck")
+    assert set(want) == {k for k in st if "phi_conn" not in k}
+    for k, gw in want.items():
+        assert rel_err(st[k].grad.numpy(), gw.numpy()) < 1e-5, k

@@ -105,6 +105,108 @@ def test_block_fixture_fp32(gpu, tag):
     assert rel_err(to_np(out), fx.group(tag)["out"].numpy()) <= FP32_TOL
 
 
+def _configured_block(dev, tag: str, d_model: int, r: int, ffn_hidden: int):
+    """This package's MOGTBlock with a fixture group's duck-typed attributes
+    and weights."""
+    from mogt_amd.model_mogt import MOGTBlock
+
+    m = fx.meta(tag)
+    blk = MOGTBlock(d_model=d_model, r=r, ffn_hidden=ffn_hidden).to(dev)
+    for k in ("scan_impl", "fast_throughput_mode", "connection_impl", "connection_damping",
+              "scan_block_size", "block_carry_scan", "transport_gate_mode", "value_gate_input_mode",
+              "couple_forget_to_value_gate"):
+        if k in m:
+            setattr(blk, k, m[k])
+    if m.get("transport_gate"):
+        blk.phi_transport_gate = nn.Linear(d_model, m["transport_gate"], bias=True).to(dev)
+    if m.get("value_gate"):
+        n_in = {"current": 1, "current_prev": 2, "current_prev_prefix": 3}[m["value_gate_input_mode"]]
+        blk.phi_value_gate = nn.Linear(n_in * d_model, m["value_gate"], bias=True).to(dev)
+    blk.load_state_dict(_to(fx.state_dict(tag), dev))
+    return blk.eval()
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+def test_transport_only_fixture(gpu, autocast):
+    """fast_throughput_mode (scan_impl = "transport_triton", model_mogt.py:71-74,
+    187-192): V_t = Y_t V_raw with the HIP prefix product Y (triton_fused_scan)
+    on a matrix_exp transport with rank-wise transport and coupled value gates,
+    r = 16 as the reference's kernel requires."""
+    announce(f"transport-only fixture autocast={autocast}")
+    m = fx.meta("tt")
+    blk = _configured_block(gpu, "tt", m["d_model"], m["r"], m["ffn_hidden"])
+    assert blk._resolve_scan_impl() == "transport_triton"
+    g = fx.group("tt", torch.float32)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        out = blk(g["x"].to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(out), fx.group("tt")["out"].numpy()) <= (BF16_TOL if autocast else FP32_TOL)
+
+
+@pytest.mark.parametrize("tag", ["pr", "br"])
+def test_parallel_and_block_reference_fixtures(gpu, tag):
+    """scan_impl = "parallel_reference" (matrix_exp) and "block_reference"
+    (Cayley, block 5, doubling carries) selected on the block
+    (model_mogt.py:204-221), on the dense HIP scan."""
+    announce(f"block fixture {tag}")
+    blk = _configured_block(gpu, tag, fx.meta("D"), fx.meta("R"), 4 * fx.meta("D"))
+    assert blk._resolve_scan_impl() == fx.meta(tag)["scan_impl"]
+    g = fx.group(tag, torch.float32)
+    with torch.no_grad():
+        out = blk(g["x"].to(gpu))
+    torch.cuda.synchronize()
+    assert rel_err(to_np(out), fx.group(tag)["out"].numpy()) <= FP32_TOL
+
+
+def test_checkpointed_backbone_fixture_training(gpu):
+    """A 3-layer backbone in training mode with gradient_checkpointing and
+    checkpoint_every_n = 2 (model_mogt.py:278-285) and blocks selecting
+    parallel_reference / block_reference / sequential: blocks 0 and 2 run
+    again in the backward, and the output, the loss and every parameter's
+    gradient match the reference's float64 run."""
+    announce("checkpointed backbone fixture (training)")
+    from mogt_amd.model_mogt import MOGTModel
+
+    m = fx.meta("ck")
+    D, R, V = fx.meta("D"), fx.meta("R"), fx.meta("VOCAB")
+    model = MOGTModel(vocab_size=V, d_model=D, num_layers=m["layers"], r=R, ffn_hidden=m["ffn_hidden"]).to(gpu)
+    for blk, impl in zip(model.blocks, m["scan_impl"]):
+        blk.scan_impl = impl
+        blk.scan_block_size = m["scan_block_size"]
+        blk.block_carry_scan = m["block_carry_scan"]
+        blk.connection_impl = "identity"
+        blk.connection_damping = 1.0
+        blk.phi_value_gate = nn.Linear(3 * D, R, bias=True).to(gpu)
+        blk.value_gate_input_mode = "current_prev_prefix"
+        blk.couple_forget_to_value_gate = True
+    model.prefix_condition_position = m["prefix_condition_position"]
+    model.gradient_checkpointing = m["gradient_checkpointing"]
+    model.checkpoint_every_n = m["checkpoint_every_n"]
+    model.load_state_dict(_to(fx.state_dict("ck"), gpu))
+    model.train()
+    calls = [0] * len(model.blocks)
+    hooks = [blk.register_forward_pre_hook(lambda mod, a, i=i: calls.__setitem__(i, calls[i] + 1))
+             for i, blk in enumerate(model.blocks)]
+    g = fx.group("ck", torch.float32)
+    y = model(g["ids"].to(gpu))
+    loss = (y * g["w"].to(gpu)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    for h in hooks:
+        h.remove()
+    assert calls == m["block_calls"]
+    ref = fx.group("ck")
+    assert rel_err(to_np(y.detach()), ref["out"].numpy()) <= FP32_TOL
+    assert abs(float(loss.detach()) - float(ref["loss"])) <= FP32_TOL * abs(float(ref["loss"]))
+    params = dict(model.named_parameters())
+    want = fx.grads("ck")
+    for k, gw in want.items():
+        assert params[k].grad is not None, k
+        assert rel_err(to_np(params[k].grad), gw.numpy()) <= FP32_TOL, k
+    for k in m["params_without_grad"]:
+        assert params[k].grad is None or not params[k].grad.any(), k
+
+
 def _lm(dev):
     from mogt_amd.model_mogt import MOGTForCausalLM
 
