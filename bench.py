@@ -107,7 +107,7 @@ def diag_launcher(torch, lib, ops, B, L, D, dtype, out_dtype, sets, tile=None, s
         nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, ic)
     else:
         nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, D, *tile)
-    ws = ops.workspace(nbytes, dev)
+    ws = ops.workspace(nbytes, dev, "diag", ("bench", B, L, D, ic, tile))
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     args = [(x.data_ptr(), y.data_ptr(), z.data_ptr()) for x, y, z in bufs]
@@ -186,7 +186,7 @@ def measure_diag_rev(torch, lib, ops, L, steps, warmup, D=768, B=1, sets=3):
     bufs = [(torch.sigmoid(torch.randn(B, L, D, generator=gen, device=dev) + 3.0),
              torch.randn(B, L, D, generator=gen, device=dev), torch.empty(B, L, D, device=dev))
             for _ in range(sets)]
-    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, 0), dev)
+    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, 0), dev, "diag_rev", ("bench", B, L, D))
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
@@ -360,7 +360,7 @@ def measure_coupled(torch, lib, ops, L, steps, warmup, r=16, c=48, tile=None):
         nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(1, L, r, c, 1)
     else:
         nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(1, L, r * c, *tile)
-    ws = ops.workspace(nbytes, dev)
+    ws = ops.workspace(nbytes, dev, "coupled", ("bench", L, r, c, tile))
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
@@ -505,7 +505,8 @@ def measure_rank1(torch, lib, ops, steps, warmup, B=2, L=8192, H=12, d=64, sets=
     dev = torch.device("cuda:0")
     f, k, v, q = (torch.from_numpy(x).to(dev).bfloat16() for x in synthetic.rank1_inputs(B, L, H, d, seed=0))
     bufs = [(f.clone(), k.clone(), v.clone(), q.clone(), torch.empty_like(q)) for _ in range(sets)]
-    ws = ops.workspace(lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d), dev)
+    nbytes = lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d)
+    ws = ops.workspace(nbytes, dev, "rank1", ("bench", B, L, H)) if path in (0, 1) else ops.workspace(nbytes, dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     fn = lib.mogt_rank1_coupled_scan_fwd_cfg

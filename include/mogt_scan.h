@@ -320,9 +320,24 @@ int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H
  * work-groups exchange the carried states through the workspace; otherwise
  * as three launches (chunk states, carries, outputs).  The workspace query
  * covers both.
+ * The one-launch form needs every super-chunk of a sequence resident at
+ * once (in-order dispatch guarantees it on an otherwise idle GPU); if a
+ * kernel on another stream holds the compute units its bounded waits give
+ * up, the affected outputs are NaN and mogt_workspace_faults counts them.
  * mogt_rank1_coupled_scan_fwd_cfg: the same with the path forced (0 = by
- *   length as above, 1 = one launch, 2 = three launches); no counterpart in
- *   the reference -- for tests and benchmarks of both paths.                */
+ *   length as above, 1 = one launch, 2 = three launches, 3 = a test of the
+ *   give-up handling: the one-launch kernel with super-chunk 0 withholding
+ *   its aggregate, and each work-group's wait on it giving up after 64 polls,
+ *   so every super-chunk after the first comes back NaN and the count grows by
+ *   exactly B * H * ceil(L / 256); needs L > 256); no counterpart in the
+ *   reference -- for tests and
+ *   benchmarks of both paths.
+ * mogt_rank1_check_ranges: host-only self-check, no device work: evaluates
+ *   every buffer range the rank-1 kernels build over a [B, L, H, 64] tensor of
+ *   `elem_bytes` elements (2 or 4) -- each lies inside the tensor, covers the
+ *   rows before L of its 64-row tile and none after -- and returns 0, or
+ *   MOGT_E_INVALID naming the first violation.  No counterpart in the
+ *   reference.                                                              */
 size_t mogt_rank1_coupled_scan_workspace_bytes(int64_t batch, int64_t length, int64_t heads,
                                                int64_t head_dim);
 int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const void* v, const void* q,
@@ -333,6 +348,7 @@ int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, const void* v,
                                     void* y, int64_t batch, int64_t length, int64_t heads,
                                     int64_t head_dim, int f_dtype, int kvq_dtype, int out_dtype,
                                     void* workspace, size_t workspace_bytes, int path, void* stream);
+int mogt_rank1_check_ranges(int64_t batch, int64_t length, int64_t heads, int elem_bytes);
 
 /* ------------------------------------------------------------------------- */
 /* Row-wise kernels of the MOGT block (one wave per row, rows of `dim`

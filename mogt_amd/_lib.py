@@ -159,6 +159,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_int, _c_int, _c_int, _c_void_p, _c_size, _c_int, _c_void_p]),
+    "mogt_rank1_check_ranges": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
 }
 
 _lock = threading.Lock()

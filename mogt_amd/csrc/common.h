@@ -96,10 +96,14 @@ __device__ __forceinline__ float sigmoid_hw(float a) {
 // look-back how far back to read.
 //
 // Reuse without clearing: the last work-group waits until every chunk flag
-// carries the current epoch (each work-group writes its flag right after it
-// read the epoch), then advances the epoch.  Stale words of older launches can
-// never match a newer tag, so the buffer needs zero-filling only once, and the
-// scheme holds inside a captured HIP graph.
+// carries the current epoch's tag (each work-group writes its flag right after
+// it read the epoch), then advances the epoch.  Tagged words of older launches
+// of the same layout can never match a newer tag, so repeated launches of one
+// layout never clear the buffer, also inside a captured HIP graph.  Words of
+// another layout, or plain data of other kernels, could in principle hold a
+// current tag's bit pattern: the host keeps look-back workspaces apart from
+// plain-data scratch and clears the region past the header whenever the
+// layout of a buffer's launches changes (mogt_amd/ops.py, workspace()).
 // ---------------------------------------------------------------------------
 constexpr uint32_t ST_AGG = 1u;   // chunk aggregate published
 constexpr uint32_t ST_INC = 2u;   // inclusive prefix published
@@ -160,16 +164,17 @@ __device__ __forceinline__ uint32_t ws_epoch(uint32_t* hdr, uint32_t* s_epoch) {
     return *s_epoch;
 }
 
-// Last work-group of the grid: once all n_flags chunk flags carry `epoch`,
-// advance the epoch for the next launch.
+// Last work-group of the grid: once all n_flags chunk flags carry the tag
+// `want` (make_tag(epoch, status): never 0, so a zero-filled word never
+// passes), advance the epoch for the next launch.
 __device__ __forceinline__ void ws_finish(uint32_t* hdr, const uint32_t* flags, int64_t n_flags,
-                                          uint32_t epoch) {
+                                          uint32_t epoch, uint32_t want) {
     const uint64_t lin = blockIdx.x + static_cast<uint64_t>(gridDim.x) *
                                           (blockIdx.y + static_cast<uint64_t>(gridDim.y) * blockIdx.z);
     if (lin != static_cast<uint64_t>(gridDim.x) * gridDim.y * gridDim.z - 1) return;
     for (int64_t i = threadIdx.x; i < n_flags; i += blockDim.x) {
         uint32_t n = 0;
-        while ((ld_relaxed(&flags[i]) >> 2) != epoch) {
+        while (ld_relaxed(&flags[i]) != want) {
             if (++n > MAX_SPIN) {
                 note_timeout(hdr);
                 break;

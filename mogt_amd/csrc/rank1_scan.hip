@@ -125,18 +125,29 @@ struct Tile8 {
 __device__ __forceinline__ int tile_m() { return static_cast<int>(threadIdx.x) >> 3; }
 __device__ __forceinline__ int tile_sg() { return static_cast<int>(threadIdx.x) & 7; }
 
-// Descriptor over the rows t0 .. L - 1 of one (batch, head) sequence of a
-// [B, L, H, n] tensor with n elements of T per row.  For t0 >= L (a padding
-// sub-chunk past the end, which the summary kernel still prefetches) the range
-// is empty and the base stays at the sequence's first row: loads read 0.
+// Byte range of the rows t0 .. L - 1 of one (batch, head) sequence of a
+// [B, L, H, n] tensor with n elements of `elem` bytes per row: the first
+// element of row t0 and the span up to the end of row L - 1.  For t0 >= L (a
+// padding sub-chunk past the end, which the summary kernel still prefetches)
+// the span is empty and the base stays at the sequence's first row, so loads
+// through it read 0 and stores are dropped.  Host and device share it, so
+// mogt_rank1_check_ranges can check every range the kernels build.
+struct RowsRange {
+    int64_t base;   // element offset of the range's first byte
+    int64_t span;   // bytes
+};
+__host__ __device__ inline RowsRange rows_range(int64_t rowbase, int64_t t0, int64_t L, int H, int n, int elem) {
+    const int64_t strideB = static_cast<int64_t>(H) * n * elem;
+    const bool live = t0 < L;
+    int64_t span = live ? (L - 1 - t0) * strideB + static_cast<int64_t>(n) * elem : 0;
+    if (span > 0x7fffffff) span = 0x7fffffff;
+    return {(rowbase + (live ? t0 : 0) * H) * n, span};
+}
 template <typename T>
 __device__ __forceinline__ auto seq_rsrc(const T* base, int64_t rowbase, int64_t t0, int64_t L, int H, int n) {
-    const int64_t strideB = static_cast<int64_t>(H) * n * sizeof(T);
-    const bool live = t0 < L;
-    int64_t span = live ? (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T) : 0;
-    if (span > 0x7fffffff) span = 0x7fffffff;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + (live ? t0 : 0) * H) * n, 0,
-                                             static_cast<int>(span), 0x00020000);
+    const RowsRange r = rows_range(rowbase, t0, L, H, n, static_cast<int>(sizeof(T)));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + r.base, 0, static_cast<int>(r.span),
+                                             0x00020000);
 }
 
 template <typename TI>
@@ -552,6 +563,8 @@ struct Rank1SParams {
     float* sin;        // [n_seq][nsc][DH*DH] carried-in states (same order)
     int64_t L;
     int H, nsc;
+    int skip_agg0;       // test path: super-chunk 0 withholds its aggregate, and waits
+                         // on it give up after 64 polls (every other wait: MAX_SPIN)
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -582,16 +595,10 @@ __device__ __forceinline__ bf16x8 tr_op(bf16_t* tile, int kk, int cb) {
     return __builtin_bit_cast(bf16x8, (u32x4{a[0], a[1], b[0], b[1]}));
 }
 
-// Descriptor over rows t0 .. L - 1 of one (batch, head) sequence of a
-// [B, L, H, n] tensor; an empty range when t0 >= L (loads read 0, stores drop).
+// Descriptor over rows t0 .. L - 1 of one (batch, head) sequence (rows_range).
 template <typename T>
 __device__ __forceinline__ auto rows_rsrc(const T* base, int64_t rowbase, int64_t t0, int64_t L, int H, int n) {
-    const int64_t strideB = static_cast<int64_t>(H) * n * sizeof(T);
-    int64_t span = t0 < L ? (L - 1 - t0) * strideB + static_cast<int64_t>(n) * sizeof(T) : 0;
-    if (span > 0x7fffffff) span = 0x7fffffff;
-    const int64_t tb = t0 < L ? t0 : 0;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base) + (rowbase + tb * H) * n, 0,
-                                             static_cast<int>(span), 0x00020000);
+    return seq_rsrc(base, rowbase, t0, L, H, n);
 }
 
 // Register operand of row `row` of a [64][64] tile in global memory, head-dim
@@ -849,7 +856,7 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
     const auto rSin = __builtin_amdgcn_make_buffer_rsrc(sinSeq, 0, nsc * R1_DH * R1_DH * 4, 0x00020000);
     // wave m reads X_m = S_m^loc and writes X_{m+1} = 2^LcT_m X_m + dS_m in place;
     // wave 3 turns X_4 into the super-chunk's aggregate and publishes it
-    const bool publish = c + 1 < nsc;
+    const bool publish = c + 1 < nsc && !(p.skip_agg0 && c == 0);
 #pragma unroll
     for (int m = 0; m < R1_SUB; ++m) {
         if (j == m) {
@@ -889,10 +896,11 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
         if (j == 0 && lane < nsc - 1) {   // every aggregate of the sequence but the last
             const uint32_t tag = make_tag(epoch, ST_AGG);
             uint64_t wd = ld_relaxed(&p.flag1[fbase + lane]);
+            const uint32_t limit = p.skip_agg0 && lane == 0 ? 64u : MAX_SPIN;
             uint32_t n = 0;
             bool ok = true;
             while (word_tag(wd) != tag) {
-                if (++n > MAX_SPIN) {
+                if (++n > limit) {
                     note_timeout(p.hdr);
                     ok = false;
                     break;
@@ -1030,7 +1038,7 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
             }
         }
     }
-    ws_finish(p.hdr, p.flag2, static_cast<int64_t>(gridDim.x), epoch);
+    ws_finish(p.hdr, p.flag2, static_cast<int64_t>(gridDim.x), epoch, make_tag(epoch, ST_INC));
 }
 
 namespace {
@@ -1113,14 +1121,16 @@ extern "C" int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, con
     if (head_dim != R1_DH) return set_error(MOGT_E_INVALID, "head_dim %lld not supported (64)", (long long)head_dim);
     for (int d : {f_dtype, kvq_dtype, out_dtype})
         if (d != MOGT_F32 && d != MOGT_BF16) return set_error(MOGT_E_INVALID, "unsupported dtype code");
-    if (path < 0 || path > 2) return set_error(MOGT_E_INVALID, "path %d not in {0, 1, 2}", path);
+    if (path < 0 || path > 3) return set_error(MOGT_E_INVALID, "path %d not in {0, 1, 2, 3}", path);
     if (batch == 0 || length == 0) return MOGT_OK;
     if (!f || !k || !v || !q || !y) return set_error(MOGT_E_INVALID, "null tensor pointer");
     if (batch * heads > 65535) return set_error(MOGT_E_INVALID, "batch * heads > 65535");
     if (length > (int64_t(1) << 40)) return set_error(MOGT_E_INVALID, "length too large");
     const R1Geo g = r1_geometry(batch, length, heads);
     const bool bf16_io = kvq_dtype == MOGT_BF16;
-    const bool single = path == 1 || (path == 0 && g.nsc <= R1S_MAX_SC && bf16_io);
+    const bool single = path == 1 || path == 3 || (path == 0 && g.nsc <= R1S_MAX_SC && bf16_io);
+    if (path == 3 && g.nsc < 2)
+        return set_error(MOGT_E_INVALID, "the give-up test path needs at least 2 super-chunks (L > %d)", R1_RS);
     if (single && g.nsc > R1S_MAX_SC)
         return set_error(MOGT_E_INVALID, "single-pass rank-1 scan takes at most %d super-chunks (L <= %d)",
                          R1S_MAX_SC, R1S_MAX_SC * R1_RS);
@@ -1143,6 +1153,9 @@ extern "C" int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, con
     p1.agg = reinterpret_cast<float*>(base + g.s_agg);
     p1.sin = reinterpret_cast<float*>(base + g.s_sin);
     p1.L = length; p1.H = static_cast<int>(heads); p1.nsc = g.nsc;
+    // path 3 (tests): super-chunk 0 withholds its aggregate; each work-group's
+    // wait on it gives up after 64 polls and is counted once
+    p1.skip_agg0 = path == 3;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n_seq = static_cast<int>(batch * heads);
     const bool fb = f_dtype == MOGT_BF16, ib = kvq_dtype == MOGT_BF16, ob = out_dtype == MOGT_BF16;
@@ -1162,4 +1175,40 @@ extern "C" int mogt_rank1_coupled_scan_fwd(const void* f, const void* k, const v
                                            void* workspace, size_t workspace_bytes, void* stream) {
     return mogt_rank1_coupled_scan_fwd_cfg(f, k, v, q, y, batch, length, heads, head_dim, f_dtype, kvq_dtype,
                                            out_dtype, workspace, workspace_bytes, 0, stream);
+}
+
+extern "C" int mogt_rank1_check_ranges(int64_t batch, int64_t length, int64_t heads, int elem_bytes) {
+    clear_error();
+    if (batch <= 0 || length <= 0 || heads <= 0 || (elem_bytes != 2 && elem_bytes != 4))
+        return set_error(MOGT_E_INVALID, "batch, length, heads > 0 and elem_bytes 2 or 4 expected");
+    const R1Geo g = r1_geometry(batch, length, heads);
+    const int64_t total = batch * length * heads * R1_DH * elem_bytes;   // bytes of one [B, L, H, 64] tensor
+    const int64_t strideB = heads * R1_DH * elem_bytes;
+    if (63 * strideB + R1_DH * elem_bytes > 0x7fffffff)
+        return set_error(MOGT_E_INVALID, "a 64-row tile spans more than 2 GiB");
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t h = 0; h < heads; ++h) {
+            const int64_t rowbase = b * length * heads + h;
+            // every sub-chunk start the kernels build a descriptor for: K_A's
+            // prefetches, K_C's and the one-launch kernel's sub-chunks, and the
+            // tiles of a padding super-chunk past the end
+            for (int64_t t0 = 0; t0 <= (static_cast<int64_t>(g.nsc) + 1) * R1_RS; t0 += R1_T) {
+                const RowsRange r = rows_range(rowbase, t0, length, static_cast<int>(heads), R1_DH, elem_bytes);
+                const int64_t start = r.base * elem_bytes;
+                if (r.span < 0 || start < 0 || start + r.span > total)
+                    return set_error(MOGT_E_INVALID,
+                                     "b %lld h %lld t0 %lld: range [%lld, %lld) outside the %lld-byte tensor",
+                                     (long long)b, (long long)h, (long long)t0, (long long)start,
+                                     (long long)(start + r.span), (long long)total);
+                // rows t0 .. min(L, t0 + 64) - 1 are read in full inside the
+                // range; every later row of the tile starts past its end
+                const int64_t live = t0 < length ? (length - t0 < R1_T ? length - t0 : R1_T) : 0;
+                if (live > 0 && (live - 1) * strideB + R1_DH * elem_bytes > r.span)
+                    return set_error(MOGT_E_INVALID, "t0 %lld: live rows cut off by the range", (long long)t0);
+                if (live < R1_T && live * strideB < r.span)
+                    return set_error(MOGT_E_INVALID, "t0 %lld: row %lld past L inside the range",
+                                     (long long)t0, (long long)live);
+            }
+        }
+    return MOGT_OK;
 }

@@ -11,6 +11,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import warnings
 
 import torch
 import torch.nn.functional as F
@@ -20,16 +21,20 @@ from . import _lib
 _DTYPE_CODE = {torch.float32: _lib.MOGT_F32, torch.bfloat16: _lib.MOGT_BF16}
 
 _ws_lock = threading.Lock()
-_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+_ws_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 # Workspaces replaced by a larger one.  They are kept alive for the life of the
 # process: a HIP graph captured earlier still holds their address, and freeing
 # them would let the allocator hand the memory to another tensor that the
 # graph's replays would then overwrite.  Growth is geometric, so the retired
 # buffers together are smaller than the live one.
 _ws_retired: list[torch.Tensor] = []
+# layout of the last launch on each look-back workspace, and whether it was
+# recorded into a captured graph
+_ws_layout: dict[tuple[int, int, str], tuple] = {}
+WS_HDR_BYTES = 256   # epoch and give-up counter (common.h); never cleared
 
 # Checked mode: after every single-pass scan, read the workspace's give-up
-# counter (a device synchronisation) and raise if it is non-zero.
+# counter (a device synchronisation) and raise if it counted a new give-up.
 CHECK_WORKSPACE = os.environ.get("MOGT_CHECK_WORKSPACE", "0") not in ("", "0")
 
 
@@ -48,15 +53,35 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+# Workspace families.  "plain" holds data that the kernels read back only in
+# launches that wrote it (dense / generic / three-launch rank-1 scans: chunk
+# products, carries, states).  The others hold tagged words of the look-back
+# protocol, which a launch accepts when their tag carries the workspace's
+# current epoch; a family never shares its buffer with plain data, and a
+# launch whose layout differs from the buffer's previous one clears everything
+# past the header first, so a word it reads is either zero, an older tag or
+# its own.
+LOOKBACK_FAMILIES = frozenset({"diag", "diag_rev", "coupled", "coupled_rev", "rank1"})
+
+
+def workspace(nbytes: int, device: torch.device, family: str = "plain", layout: tuple | None = None
+              ) -> torch.Tensor:
     """Zero-initialised scratch of at least ``nbytes`` for the current stream.
 
-    Kernels using the look-back protocol restore the buffer's reusable state at
-    the end of every launch, so it is zero-filled only when first allocated or
-    grown.  One buffer per (device, stream) keeps concurrent streams apart.
+    One buffer per (device, stream, family) keeps concurrent streams and the
+    kernel families apart.  Look-back families (``LOOKBACK_FAMILIES``) pass the
+    launch's ``layout`` (its shape, dtypes and tile): kernels using the
+    look-back protocol restore the buffer's reusable state at the end of every
+    launch, so repeated launches of one layout never clear it; a different
+    layout clears bytes ``[256, nbytes)`` with a fill kernel (also when the
+    first look-back launch of a captured graph is recorded, so every replay
+    starts from that state).
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
-           _stream_handle(device))
+           _stream_handle(device), family)
+    lookback = family in LOOKBACK_FAMILIES
+    if lookback and layout is None:
+        raise ValueError(f"workspace family {family!r} needs the launch's layout")
     with _ws_lock:
         buf = _ws_cache.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -64,8 +89,18 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
             if buf is not None:
                 size = max(size, 2 * buf.numel())
                 _ws_retired.append(buf)
+            # a new buffer starts from epoch 0 with every word zero
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
+            _ws_layout.pop(key, None)
+        if lookback:
+            state = (tuple(layout), torch.cuda.is_current_stream_capturing())
+            last = _ws_layout.get(key)
+            if last is not None and last != state and nbytes > WS_HDR_BYTES:
+                buf[WS_HDR_BYTES:nbytes].zero_()
+            elif last is None and state[1] and nbytes > WS_HDR_BYTES:
+                buf[WS_HDR_BYTES:nbytes].zero_()
+            _ws_layout[key] = state
         return buf
 
 
@@ -88,11 +123,23 @@ def workspace_faults() -> int:
     return sum(_faults_of(b) for b in bufs)
 
 
+_ws_faults_seen: dict[int, int] = {}
+
+
+def _new_faults(ws: torch.Tensor) -> int:
+    """Give-ups counted on ``ws`` since the last call for it (synchronises)."""
+    n = _faults_of(ws)
+    with _ws_lock:
+        seen = _ws_faults_seen.get(ws.data_ptr(), 0)
+        _ws_faults_seen[ws.data_ptr()] = n
+    return n - seen
+
+
 def _checked(ws: torch.Tensor, what: str) -> None:
     """In checked mode (MOGT_CHECK_WORKSPACE=1) raise if the launch that just
     used ``ws`` gave up a look-back wait."""
     if CHECK_WORKSPACE and not torch.cuda.is_current_stream_capturing():
-        n = _faults_of(ws)
+        n = _new_faults(ws)
         if n:
             raise WorkspaceFault(f"{what}: {n} look-back wait(s) gave up; the output is invalid (NaN)")
 
@@ -117,7 +164,7 @@ def _diag_scan_launch(a: torch.Tensor, b: torch.Tensor, h: torch.Tensor,
         nbytes = lib.mogt_diag_scan_workspace_bytes(B, L, D, in_code)
     else:
         nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, D, *cfg)
-    ws = workspace(nbytes, a.device)
+    ws = workspace(nbytes, a.device, "diag", (B, L, D, in_code, cfg))
     pre = prefix.data_ptr() if prefix is not None else None
     stream = _stream_handle(a.device)
     if cfg is None:
@@ -181,7 +228,7 @@ def _diag_scan_rev_op(a: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
     g = g.to(torch.float32).contiguous()
     B, L, D = a.shape
     out = torch.empty(a.shape, dtype=torch.float32, device=a.device)
-    ws = workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, _lib.MOGT_F32), a.device)
+    ws = workspace(lib.mogt_diag_scan_workspace_bytes(B, L, D, _lib.MOGT_F32), a.device, "diag_rev", (B, L, D))
     rc = lib.mogt_diag_scan_rev_fwd(a.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, D,
                                     ws.data_ptr(), ws.numel(), _stream_handle(a.device))
     _lib.check(rc, "mogt_diag_scan_rev_fwd")
@@ -258,7 +305,7 @@ def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: 
     vc = dtype_code(v.dtype, "coupled_rank_scan")
     oc = dtype_code(out_dtype, "coupled_rank_scan")
     nbytes = lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, vc)
-    ws = workspace(nbytes, v.device)
+    ws = workspace(nbytes, v.device, "coupled", ("plain", B, L, rank, C, vc))
     rc = lib.mogt_coupled_rank_scan_fwd(z.data_ptr(), v.data_ptr(), h.data_ptr(), B, L, rank, C,
                                         float(damping), zc, vc, oc, ws.data_ptr(), ws.numel(),
                                         _stream_handle(v.device))
@@ -282,7 +329,7 @@ def _coupled_scan_rev_op(z: torch.Tensor, grad_h: torch.Tensor, rank: int, dampi
     B, L, D = g.shape
     out = torch.empty_like(g)
     nbytes = lib.mogt_coupled_rank_scan_rev_workspace_bytes(B, L, rank, D // rank)
-    ws = workspace(nbytes, g.device)
+    ws = workspace(nbytes, g.device, "coupled_rev", (B, L, rank, D // rank))
     rc = lib.mogt_coupled_rank_scan_rev_fwd(z.data_ptr(), g.data_ptr(), out.data_ptr(), B, L, rank, D // rank,
                                             float(damping), dtype_code(z.dtype, "coupled_scan_rev"), ws.data_ptr(),
                                             ws.numel(), _stream_handle(g.device))
@@ -380,7 +427,8 @@ def _coupled_rank_scan_stats_op(z: torch.Tensor, v: torch.Tensor, rank: int, dam
     h = torch.empty(v.shape, dtype=out_dtype, device=v.device)
     stats = torch.empty((B, L, -(-D // STAT_GROUP)), dtype=torch.float32, device=v.device)
     vc = dtype_code(v.dtype, "coupled_rank_scan_stats")
-    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, vc), v.device)
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, vc), v.device, "coupled",
+                   ("stats", B, L, rank, C, vc))
     rc = lib.mogt_coupled_rank_scan_stats_fwd(z.data_ptr(), v.data_ptr(), h.data_ptr(), stats.data_ptr(), B, L,
                                               rank, C, float(damping), vc,
                                               dtype_code(out_dtype, "coupled_rank_scan_stats"), ws.data_ptr(),
@@ -425,7 +473,8 @@ def _coupled_rank_scan_proj_op(proj: torch.Tensor, features: int, gate_prev: boo
     gc = None
     if gate_const is not None:
         gc = gate_const.to(torch.float32).expand(B, rank).contiguous()
-    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device)
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device, "coupled",
+                   ("proj", B, L, rank, C, code, ld, int(bool(gate_prev))))
     rc = lib.mogt_coupled_rank_scan_proj_fwd(proj.data_ptr(), ld, D, int(bool(gate_prev)),
                                              gc.data_ptr() if gc is not None else None, h.data_ptr(),
                                              stats.data_ptr(), None, B, L, rank, C, float(damping), code, code,
@@ -475,7 +524,8 @@ def _coupled_proj_scan_op(proj: torch.Tensor, gate_const: torch.Tensor | None, f
     z = torch.empty((B, L, rank), dtype=torch.float32, device=proj.device)
     code = dtype_code(proj.dtype, "coupled_proj_scan")
     gc = gate_const.to(torch.float32).contiguous() if gate_const is not None else None
-    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device)
+    ws = workspace(lib.mogt_coupled_rank_scan_workspace_bytes(B, L, rank, C, code), proj.device, "coupled",
+                   ("proj", B, L, rank, C, code, ld, int(bool(gate_prev))))
     rc = lib.mogt_coupled_rank_scan_proj_fwd(proj.data_ptr(), ld, D, int(bool(gate_prev)),
                                              gc.data_ptr() if gc is not None else None, h.data_ptr(), None,
                                              z.data_ptr(), B, L, rank, C, float(damping), code, _lib.MOGT_F32,
@@ -1579,24 +1629,52 @@ def connection_map(A: torch.Tensor, impl: str, *, scale: float = 1.0, damping: f
 # rank-1 coupled write-forget scan with readout
 # ---------------------------------------------------------------------------
 RANK1_PATHS = {"auto": 0, "single": 1, "three": 2}
+# path 3 of the C entry point: the one-launch kernel with super-chunk 0
+# withholding its aggregate and short bounded waits (a test of the give-up
+# handling and of the fallback below); not a public choice
+_RANK1_GIVEUP_TEST = 3
+R1_SUPER = 256        # steps per super-chunk
+R1_SINGLE_MAX = 64    # super-chunks per sequence the one-launch kernel takes
+
+
+def _rank1_single(path: int, L: int, kvq: torch.dtype) -> bool:
+    """Whether the C entry point runs the one-launch kernel for this call."""
+    if path in (1, _RANK1_GIVEUP_TEST):
+        return True
+    return path == 0 and kvq == torch.bfloat16 and -(-L // R1_SUPER) <= R1_SINGLE_MAX
+
+
+def _rank1_launch(f, k, v, q, y, path: int) -> torch.Tensor:
+    lib = _lib.load()
+    B, L, H, d = k.shape
+    single = _rank1_single(path, L, k.dtype)
+    nbytes = lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d)
+    ws = workspace(nbytes, k.device, "rank1", (B, L, H)) if single else workspace(nbytes, k.device)
+    rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
+                                             y.data_ptr(), B, L, H, d,
+                                             dtype_code(f.dtype, "rank1_coupled_scan"),
+                                             dtype_code(k.dtype, "rank1_coupled_scan"),
+                                             dtype_code(y.dtype, "rank1_coupled_scan"),
+                                             ws.data_ptr(), ws.numel(), int(path), _stream_handle(k.device))
+    _lib.check(rc, "mogt_rank1_coupled_scan_fwd_cfg")
+    return ws if single else None
 
 
 @torch.library.custom_op("mogt::rank1_coupled_scan", mutates_args=())
 def _rank1_op(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
               out_dtype: torch.dtype, path: int) -> torch.Tensor:
-    lib = _lib.load()
     f, k, v, q = (t.contiguous() for t in (f, k, v, q))
-    B, L, H, d = k.shape
     y = torch.empty(k.shape, dtype=out_dtype, device=k.device)
-    ws = workspace(lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d), k.device)
-    rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
-                                             y.data_ptr(), B, L, H, d,
-                                             dtype_code(f.dtype, "rank1_coupled_scan"),
-                                             dtype_code(k.dtype, "rank1_coupled_scan"),
-                                             dtype_code(out_dtype, "rank1_coupled_scan"),
-                                             ws.data_ptr(), ws.numel(), int(path), _stream_handle(k.device))
-    _lib.check(rc, "mogt_rank1_coupled_scan_fwd_cfg")
-    _checked(ws, "mogt_rank1_coupled_scan_fwd")
+    ws = _rank1_launch(f, k, v, q, y, path)
+    if ws is not None and CHECK_WORKSPACE and not torch.cuda.is_current_stream_capturing():
+        # the one-launch kernel needs every super-chunk of a sequence resident
+        # at once; if work on another stream held the GPU its waits gave up
+        # and y holds NaN: take the three-launch path, which waits on nothing
+        n = _new_faults(ws)
+        if n:
+            warnings.warn(f"rank1_coupled_scan: {n} wait(s) of the one-launch kernel gave up; "
+                          "recomputed with the three-launch path", RuntimeWarning, stacklevel=2)
+            _rank1_launch(f, k, v, q, y, RANK1_PATHS["three"])
     return y
 
 

@@ -195,7 +195,8 @@ def test_every_coupled_reverse_tile(gpu, tile):
     dht = torch.from_numpy(dh).to(gpu)
     G = torch.empty_like(dht)
     lib = _lib.load()
-    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes_cfg(B, L, r * c, *tile), gpu)
+    ws = ops.workspace(lib.mogt_diag_scan_workspace_bytes_cfg(B, L, r * c, *tile), gpu, "coupled_rev",
+                       ("cfg-test", B, L, r, c, tile))
     rc = lib.mogt_coupled_rank_scan_rev_fwd_cfg(zt.data_ptr(), dht.data_ptr(), G.data_ptr(), B, L, r, c, 0.995,
                                                 ops.dtype_code(zt.dtype, "z"), *tile, ws.data_ptr(), ws.numel(),
                                                 ops._stream_handle(gpu))

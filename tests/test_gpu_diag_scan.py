@@ -310,7 +310,7 @@ def test_every_coupled_tile(gpu, tile, vdt):
     h = torch.empty(B, L, r * c, device=gpu, dtype=torch.bfloat16 if ob else torch.float32)
     lib = _lib.load()
     nbytes = lib.mogt_diag_scan_workspace_bytes_cfg(B, L, r * c, *tile)
-    ws = ops.workspace(nbytes, zt.device)
+    ws = ops.workspace(nbytes, zt.device, "coupled", ("cfg-test", B, L, r, c, tile))
     rc = lib.mogt_coupled_rank_scan_fwd_cfg(zt.data_ptr(), vt.data_ptr(), h.data_ptr(), B, L, r, c, 0.999,
                                             ops.dtype_code(zt.dtype, "z"), ops.dtype_code(vt.dtype, "v"),
                                             ops.dtype_code(h.dtype, "h"), *tile, ws.data_ptr(), ws.numel(),
@@ -325,7 +325,8 @@ def test_every_coupled_tile(gpu, tile, vdt):
 
 def test_mixed_modes_share_workspace(gpu):
     """Forward (fp32, bf16), coupled and both reverse-time scans of different shapes
-    interleaved on one stream share one workspace (as a training step does):
+    interleaved on one stream (as a training step runs them), each family on
+    its look-back workspace and the forward scans switching layouts on theirs:
     every result stays exact."""
     announce("diag / coupled / reverse / coupled reverse interleaved x25")
     import mogt_amd

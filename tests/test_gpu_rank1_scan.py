@@ -126,3 +126,107 @@ def test_fp32_inputs(gpu, L, H):
     assert rel_err(to_np(y), ref) <= 1e-2
     with pytest.raises(ValueError):
         mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, path="single")
+
+
+@pytest.mark.parametrize("L,H", [(700, 2), (3000, 1)])
+def test_fp32_gate_bf16_operands_one_launch(gpu, L, H):
+    """fp32 f with bf16 k, v, q (the default path's one-launch kernel at these
+    lengths; several super-chunks, so the carry exchange runs): against the
+    oracle, and no wait gave up."""
+    announce(f"rank1 fp32 f, bf16 k v q, one launch, L={L} H={H}")
+    import mogt_amd
+    from mogt_amd import ops
+
+    f, k, v, q = synthetic.rank1_inputs(1, L, H, 64, seed=40 + L)
+    ft = torch.from_numpy(f).to(gpu).float()
+    kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (k, v, q))
+    ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
+    before = ops.workspace_faults()
+    for path in ("auto", "single"):
+        y = mogt_amd.ops.rank1_coupled_scan(ft, kt, vt, qt, out_dtype=torch.float32, path=path)
+        torch.cuda.synchronize()
+        assert rel_err(to_np(y), ref) <= 5e-3, path
+    assert ops.workspace_faults() == before == 0
+
+
+def _launch_path(gpu, ws, f, k, v, q, path):
+    """One call of mogt_rank1_coupled_scan_fwd_cfg through the C ABI on the
+    workspace ``ws``; returns y and the workspace's give-up count."""
+    import ctypes
+
+    from mogt_amd import _lib, ops
+
+    lib = _lib.load()
+    B, L, H, d = k.shape
+    y = torch.empty(k.shape, dtype=torch.float32, device=gpu)
+    sh = ops._stream_handle(gpu)
+    rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(), y.data_ptr(),
+                                             B, L, H, d, _lib.MOGT_BF16, _lib.MOGT_BF16, _lib.MOGT_F32,
+                                             ws.data_ptr(), ws.numel(), path, sh)
+    _lib.check(rc, "mogt_rank1_coupled_scan_fwd_cfg")
+    count = ctypes.c_uint32(0)
+    _lib.check(lib.mogt_workspace_faults(ws.data_ptr(), ws.numel(), ctypes.byref(count), sh), "faults")
+    return y, int(count.value)
+
+
+def test_giveup_poisons_and_counts(gpu):
+    """The give-up handling of the one-launch kernel, forced from the host
+    (path 3: super-chunk 0 withholds its aggregate and waits end after 64
+    polls; every kernel exits normally).  Every work-group waits on that
+    aggregate once, so the count grows by B*H*nsc; the first super-chunk's
+    outputs (which need no carry) stay right and every later one is NaN; a
+    normal launch afterwards on the same workspace is right and counts
+    nothing."""
+    announce("rank1 forced give-up (path 3) B=1 L=700 H=2")
+    B, L, H = 1, 700, 2
+    nsc = -(-L // 256)
+    f, k, v, q = synthetic.rank1_inputs(B, L, H, 64, seed=77)
+    ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
+    ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
+    from mogt_amd import _lib
+
+    # a private zero-filled workspace: the give-ups stay out of the cached ones
+    ws = torch.zeros(_lib.load().mogt_rank1_coupled_scan_workspace_bytes(B, L, H, 64), dtype=torch.uint8,
+                     device=gpu)
+    _, c0 = _launch_path(gpu, ws, ft, kt, vt, qt, 1)
+    y, c1 = _launch_path(gpu, ws, ft, kt, vt, qt, 3)
+    torch.cuda.synchronize()
+    assert c1 - c0 == B * H * nsc
+    yn = to_np(y)
+    assert np.isnan(yn[:, 256:]).all()
+    assert np.isfinite(yn[:, :256]).all()
+    assert rel_err(yn[:, :256], ref[:, :256]) <= 5e-3
+    y2, c2 = _launch_path(gpu, ws, ft, kt, vt, qt, 1)
+    torch.cuda.synchronize()
+    assert c2 == c1
+    assert rel_err(to_np(y2), ref) <= 5e-3
+
+
+def test_checked_mode_falls_back_to_three_launches(gpu, monkeypatch):
+    """In checked mode a one-launch call whose waits gave up (forced as above)
+    is recomputed on the three-launch path, with a warning, and its result is
+    right."""
+    announce("rank1 checked-mode fallback")
+    from mogt_amd import ops
+
+    monkeypatch.setattr(ops, "CHECK_WORKSPACE", True)
+    # a registry of workspaces for this test only: the forced give-ups stay
+    # out of the process's cached workspaces
+    for name in ("_ws_cache", "_ws_layout", "_ws_faults_seen"):
+        monkeypatch.setattr(ops, name, {})
+    monkeypatch.setattr(ops, "_ws_retired", [])
+    f, k, v, q = synthetic.rank1_inputs(1, 900, 2, 64, seed=78)
+    ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
+    ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))
+    with pytest.warns(RuntimeWarning, match="three-launch"):
+        y = torch.ops.mogt.rank1_coupled_scan(ft, kt, vt, qt, torch.float32, ops._RANK1_GIVEUP_TEST)
+    torch.cuda.synchronize()
+    assert np.isfinite(to_np(y)).all()
+    assert rel_err(to_np(y), ref) <= 5e-3
+    # a normal call in checked mode afterwards: no new give-up, no warning
+    import warnings
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        y = ops.rank1_coupled_scan(ft, kt, vt, qt, out_dtype=torch.float32, path="single")
+    assert rel_err(to_np(y), ref) <= 5e-3

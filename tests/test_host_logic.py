@@ -162,3 +162,74 @@ def test_rocprof_summary_groups_and_calibrates(tmp_path):
     per, copy = rs.counter_table(rows, "FETCH_SIZE")
     assert copy == 131072.0                      # the later, larger copy is not the calibration
     assert per[("k<1>", 8, 256)] == 150.0
+
+
+def test_rank1_buffer_ranges_stay_in_bounds():
+    """Every buffer range the rank-1 kernels build (K_A's prefetches, the
+    output and one-launch tiles, padding tiles past L) lies inside its tensor,
+    covers the rows before L and no row after, for ragged lengths and both
+    element sizes -- evaluated by the same helper the kernels call."""
+    from mogt_amd import _lib
+
+    lib = _lib.load()
+    for L in (1, 2, 63, 64, 65, 255, 256, 257, 700, 1000, 3000, 8192, 16383, 16385):
+        for B, H in ((1, 1), (2, 3), (1, 12)):
+            for elem in (2, 4):
+                rc = lib.mogt_rank1_check_ranges(B, L, H, elem)
+                assert rc == 0, (B, L, H, elem, lib.mogt_last_error())
+    assert lib.mogt_rank1_check_ranges(1, 100, 1, 3) == -1
+    assert lib.mogt_rank1_check_ranges(0, 100, 1, 2) == -1
+
+
+def _fake_device_workspace(monkeypatch):
+    """ops.workspace on host tensors: one fake stream, no capture."""
+    from mogt_amd import ops
+
+    monkeypatch.setattr(ops, "_stream_handle", lambda device: 7)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(ops, "_ws_cache", {})
+    monkeypatch.setattr(ops, "_ws_layout", {})
+    monkeypatch.setattr(ops, "_ws_retired", [])
+    return ops, torch.device("cpu", 0)
+
+
+def test_lookback_workspaces_are_kept_apart_and_cleared_on_layout_change(monkeypatch):
+    import pytest
+
+    ops, dev = _fake_device_workspace(monkeypatch)
+    a = ops.workspace(4096, dev, "diag", (1, 2, 3))
+    a[:8] = 5          # header: epoch and give-up count
+    a[256:4096] = 9    # tagged words of the launch
+    assert ops.workspace(4096, dev, "diag", (1, 2, 3)) is a          # same layout: kept as is
+    assert int(a[300]) == 9
+    p = ops.workspace(4096, dev)                                       # plain data: its own buffer
+    assert p is not a
+    r = ops.workspace(4096, dev, "rank1", (1,))
+    assert r is not a and r is not p
+    b = ops.workspace(2048, dev, "diag", (4, 5, 6))                    # another layout: cleared past the header
+    assert b is a
+    assert int(a[0]) == 5 and int(a[256:2048].max()) == 0 and int(a[3000]) == 9
+    with pytest.raises(ValueError):
+        ops.workspace(64, dev, "coupled")                              # look-back families name their layout
+    # growth: a new zeroed buffer, the old one kept for captured graphs
+    c = ops.workspace(1 << 20, dev, "diag", (4, 5, 6))
+    assert c is not a and c.numel() >= 1 << 20 and int(c.max()) == 0 and a in ops._ws_retired
+
+
+def test_checked_mode_reports_each_give_up_once(monkeypatch):
+    import pytest
+
+    from mogt_amd import ops
+
+    counts = iter([0, 2, 2, 3])
+    monkeypatch.setattr(ops, "_faults_of", lambda buf: next(counts))
+    monkeypatch.setattr(ops, "CHECK_WORKSPACE", True)
+    monkeypatch.setattr(ops, "_ws_faults_seen", {})
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    ws = torch.zeros(512, dtype=torch.uint8)
+    ops._checked(ws, "scan")                      # 0: fine
+    with pytest.raises(ops.WorkspaceFault, match="2 look-back"):
+        ops._checked(ws, "scan")                  # 2 new give-ups
+    ops._checked(ws, "scan")                      # still 2: nothing new
+    with pytest.raises(ops.WorkspaceFault, match="1 look-back"):
+        ops._checked(ws, "scan")                  # one more
