@@ -1,6 +1,10 @@
 """Host-side logic that needs no GPU: the GEMM-weight cache of the MOGT
 blocks (built from parameters, reused only while no gradient is recorded and
-no parameter changed)."""
+no parameter changed), the workspace families and checked-mode accounting,
+bench.py's profile provenance, the rocprof summariser, the rank-1 kernels'
+buffer ranges, and the m0 use of the fused SwiGLU GEMM's generated code."""
+from pathlib import Path
+
 import torch
 import torch.nn as nn
 
@@ -233,3 +237,40 @@ def test_checked_mode_reports_each_give_up_once(monkeypatch):
     ops._checked(ws, "scan")                      # still 2: nothing new
     with pytest.raises(ops.WorkspaceFault, match="1 look-back"):
         ops._checked(ws, "scan")                  # one more
+
+
+def test_swiglu_m0_only_feeds_lds_dma(tmp_path):
+    """The fused SwiGLU GEMM sets m0 in inline assembly for its direct-to-LDS
+    loads (clang warns that m0 is reserved).  On the code this build generates
+    for gfx950: every write of m0 is one of those asm blocks, immediately
+    followed by the load that reads it, and no other instruction of the kernel
+    reads m0 (no LDS-direct, interpolation, GWS, movrel or message
+    instructions), so no compiler-held m0 value is overwritten."""
+    import re
+    import shutil
+    import subprocess
+
+    import pytest
+
+    from mogt_amd import _build
+
+    if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
+        pytest.skip("hipcc not available")
+    out = tmp_path / "swiglu.s"
+    flags = [f for f in _build.HIPCC_FLAGS if f != "-fPIC"]
+    cmd = [_build.hipcc(), *flags, f"-I{_build.INCLUDE}", "--cuda-device-only", "-S",
+           str(_build.CSRC / "swiglu_gemm.hip"), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    lines = [ln.split(";")[0].strip() for ln in out.read_text().splitlines()]
+    code = [ln for ln in lines if ln and not ln.startswith((".", "//")) and not ln.endswith(":")]
+    writes = [i for i, ln in enumerate(code) if re.match(r"s_mov_b32\s+m0\b", ln)]
+    dma = [i for i, ln in enumerate(code) if re.match(r"buffer_load_dword\w*\s.*\blds$", ln)]
+    assert writes and len(writes) == len(dma)
+    for i in writes:
+        assert code[i + 1] == "s_nop 0" and code[i + 2] in [code[j] for j in dma], code[i:i + 3]
+    others = [ln for ln in code if "m0" in ln and not re.match(r"s_mov_b32\s+m0, s\d+$", ln)]
+    assert not others, others[:5]
+    implicit = [ln for ln in code if re.match(r"(s_sendmsg|s_movrel|v_movrel|ds_gws|ds_append|ds_consume|"
+                                              r"ds_ordered|v_interp|ds_param|ds_direct|lds_param|lds_direct)", ln)]
+    assert not implicit, implicit[:5]
