@@ -28,8 +28,8 @@ _ws_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 # graph's replays would then overwrite.  Growth is geometric, so the retired
 # buffers together are smaller than the live one.
 _ws_retired: list[torch.Tensor] = []
-# layout of the last launch on each look-back workspace, and whether it was
-# recorded into a captured graph
+# layout of the launches on each look-back workspace, and whether a captured
+# graph uses the buffer (pinned to that layout)
 _ws_layout: dict[tuple[int, int, str], tuple] = {}
 WS_HDR_BYTES = 256   # epoch and give-up counter (common.h); never cleared
 
@@ -59,8 +59,8 @@ def _stream_handle(device: torch.device) -> int:
 # protocol, which a launch accepts when their tag carries the workspace's
 # current epoch; a family never shares its buffer with plain data, and a
 # launch whose layout differs from the buffer's previous one clears everything
-# past the header first, so a word it reads is either zero, an older tag or
-# its own.
+# past the header first (or, if a captured graph uses the buffer, takes a new
+# one), so a word it reads is either zero, an older tag or its own.
 LOOKBACK_FAMILIES = frozenset({"diag", "diag_rev", "coupled", "coupled_rev", "rank1"})
 
 
@@ -70,37 +70,41 @@ def workspace(nbytes: int, device: torch.device, family: str = "plain", layout: 
 
     One buffer per (device, stream, family) keeps concurrent streams and the
     kernel families apart.  Look-back families (``LOOKBACK_FAMILIES``) pass the
-    launch's ``layout`` (its shape, dtypes and tile): kernels using the
-    look-back protocol restore the buffer's reusable state at the end of every
-    launch, so repeated launches of one layout never clear it; a different
-    layout clears bytes ``[256, nbytes)`` with a fill kernel (also when the
-    first look-back launch of a captured graph is recorded, so every replay
-    starts from that state).
+    launch's ``layout`` (its shape, dtypes and tile).  Kernels using the
+    look-back protocol leave the buffer reusable after every launch, so
+    launches of one layout never clear it; a launch of another layout first
+    clears bytes ``[256, nbytes)`` with a fill kernel.  A buffer that a graph
+    capture used is pinned to that layout: a later launch of another layout on
+    the stream gets a new buffer, and the pinned one stays alive (and
+    untouched by other layouts) for the graph's replays.
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            _stream_handle(device), family)
     lookback = family in LOOKBACK_FAMILIES
     if lookback and layout is None:
         raise ValueError(f"workspace family {family!r} needs the launch's layout")
+    capturing = lookback and torch.cuda.is_current_stream_capturing()
     with _ws_lock:
         buf = _ws_cache.get(key)
-        if buf is None or buf.numel() < nbytes:
+        state = _ws_layout.get(key)          # (layout, pinned) of the buffer's launches
+        want = tuple(layout) if lookback else None
+        moved = lookback and buf is not None and state is not None and state[0] != want and state[1]
+        if buf is None or buf.numel() < nbytes or moved:
             size = max(int(nbytes), 1 << 16)
             if buf is not None:
-                size = max(size, 2 * buf.numel())
+                if buf.numel() >= nbytes:
+                    size = buf.numel()
+                else:
+                    size = max(size, 2 * buf.numel())
                 _ws_retired.append(buf)
             # a new buffer starts from epoch 0 with every word zero
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
-            _ws_layout.pop(key, None)
+            state = None
         if lookback:
-            state = (tuple(layout), torch.cuda.is_current_stream_capturing())
-            last = _ws_layout.get(key)
-            if last is not None and last != state and nbytes > WS_HDR_BYTES:
+            if state is not None and state[0] != want and nbytes > WS_HDR_BYTES:
                 buf[WS_HDR_BYTES:nbytes].zero_()
-            elif last is None and state[1] and nbytes > WS_HDR_BYTES:
-                buf[WS_HDR_BYTES:nbytes].zero_()
-            _ws_layout[key] = state
+            _ws_layout[key] = (want, capturing or (state is not None and state[0] == want and state[1]))
         return buf
 
 

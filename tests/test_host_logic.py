@@ -220,6 +220,32 @@ def test_lookback_workspaces_are_kept_apart_and_cleared_on_layout_change(monkeyp
     assert c is not a and c.numel() >= 1 << 20 and int(c.max()) == 0 and a in ops._ws_retired
 
 
+def test_captured_workspace_is_pinned_to_its_layout(monkeypatch):
+    """A look-back buffer used under graph capture keeps serving its layout
+    (no clearing fill recorded when the capture repeats the warm-up's layout);
+    a launch of another layout afterwards gets a new buffer, and the pinned
+    one stays alive and untouched."""
+    ops, dev = _fake_device_workspace(monkeypatch)
+    capturing = [False]
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing[0])
+    a = ops.workspace(4096, dev, "coupled", ("A",))     # eager warm-up
+    a[256:] = 7
+    capturing[0] = True
+    assert ops.workspace(4096, dev, "coupled", ("A",)) is a
+    assert int(a[300]) == 7                               # not cleared for the capture
+    capturing[0] = False
+    assert ops.workspace(4096, dev, "coupled", ("A",)) is a   # eager, same layout: shared
+    b = ops.workspace(4096, dev, "coupled", ("B",))       # another layout: a new buffer
+    assert b is not a and a in ops._ws_retired and int(a[300]) == 7 and int(b.max()) == 0
+    assert ops.workspace(4096, dev, "coupled", ("C",)) is b   # b is not pinned: cleared in place
+    # a first capture with another layout than the eager one clears in place and pins
+    b[256:] = 3
+    capturing[0] = True
+    assert ops.workspace(4096, dev, "coupled", ("D",)) is b and int(b[256:4096].max()) == 0
+    capturing[0] = False
+    assert ops.workspace(4096, dev, "coupled", ("E",)) is not b
+
+
 def test_checked_mode_reports_each_give_up_once(monkeypatch):
     import pytest
 
