@@ -467,6 +467,57 @@ def measure_dense(torch, lib, ops, B, L, R, C, steps, warmup, cayley=False, sets
             "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def measure_dense_backward(torch, lib, ops, B, L, R, C, steps, warmup, sets=2):
+    """Backward of the dense scan (triton_scan.py:359-426, affine_scan.py:65-124)
+    at one shape: the reverse-time scan G_t = X_t + U_{t+1}^T G_{t+1} alone
+    (mogt_affine_scan_rev_fwd via the C ABI), and the whole gradient
+    (forward recompute, reverse scan, dU_t = G_t H_{t-1}^T) through
+    ops.affine_scan_grad; beside them the construction the reverse scan used
+    to be built from (the reference's U_back = [I, flip(U^T[1:])], flipped
+    inputs and outputs, the forward scan, dU by a batched matmul of copies)."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    bufs = []
+    for _ in range(sets):
+        U = _unit_spectral(torch, torch.eye(R, device=dev) + 0.05 * torch.randn(B, L, R, R, generator=gen,
+                                                                                   device=dev))
+        bufs.append((U, torch.randn(B, L, R, C, generator=gen, device=dev),
+                     torch.randn(B, L, R, C, generator=gen, device=dev), torch.empty(B, L, R, C, device=dev)))
+    ws = ops.workspace(lib.mogt_affine_scan_workspace_bytes(B, L, R, C), dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def rev(i):
+        U, _, X, G = bufs[i % sets]
+        rc = lib.mogt_affine_scan_rev_fwd(U.data_ptr(), X.data_ptr(), G.data_ptr(), B, L, R, C, ws.data_ptr(),
+                                          ws.numel(), sh)
+        if rc:
+            raise RuntimeError(lib.mogt_last_error().decode())
+
+    def full(i):
+        U, V, X, _ = bufs[i % sets]
+        ops.affine_scan_grad(U, V, X)
+
+    eye = torch.eye(R, device=dev).view(1, 1, R, R).expand(B, 1, R, R)
+    zeros = torch.zeros(B, 1, R, C, device=dev)
+
+    def glue(i):
+        U, V, X, _ = bufs[i % sets]
+        U_back = torch.cat([eye, U.transpose(-2, -1)[:, 1:].flip(1)], dim=1)
+        G = ops.affine_scan(U_back, X.flip(1).contiguous()).flip(1)
+        H = ops.affine_scan(U, V)
+        M_prev = torch.cat([zeros, H[:, :-1]], dim=1)
+        torch.matmul(G, M_prev.transpose(-2, -1).contiguous())
+
+    t = EventTimer(torch, stream)
+    ms_rev = t.time(rev, steps, warmup)
+    ms_full = t.time(full, steps, warmup)
+    ms_glue = t.time(glue, steps, warmup)
+    rev_bytes = B * L * (R * R + 2 * R * C) * 4
+    return {"rev_ms": ms_rev, "rev_gbs": rev_bytes / (ms_rev * 1e-3) / 1e9, "grad_ms": ms_full,
+            "glue_ms": ms_glue}
+
+
 def measure_generic(torch, lib, ops, B, L, R, C, steps, warmup, f64=True, sets=2):
     """The generic affine scan (mogt_affine_scan_generic_fwd): U, V, H in the
     state dtype (float64 or fp32), U = I + small noise scaled to norm <= 1."""
@@ -819,6 +870,15 @@ def main():
                 "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
                         "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
         if full or "dense" in only:
+            r = measure_dense_backward(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
+            extras["dense_affine_r16_c48_L32768_backward"] = {
+                "reverse_scan_us": round(r["rev_ms"] * 1e3, 2), "reverse_scan_GB/s": round(r["rev_gbs"], 1),
+                "reverse_scan_frac": round(r["rev_gbs"] / HBM_PEAK_GBS, 4),
+                "grad_us": round(r["grad_ms"] * 1e3, 2), "previous_glue_path_us": round(r["glue_ms"] * 1e3, 2),
+                "note": "backward of the core-operator shape: reverse_scan = G_t = dH_t + U_{t+1}^T G_{t+1} "
+                        "alone (U, dH in, G out: 7168 B/step); grad = forward recompute + reverse scan + "
+                        "dU_t = G_t H_{t-1}^T (affine_scan_grad); previous_glue_path = the reversed-copy "
+                        "construction it replaces (cat/flip of U^T and dH, forward scan, flip, batched matmul)"}
             r = measure_generic(torch, lib, ops, 1, 32768, 16, 48, max(3, args.steps // 10), 1)
             extras["generic_affine_f64_r16_c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),

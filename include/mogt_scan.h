@@ -298,6 +298,25 @@ size_t mogt_fused_scan_workspace_bytes(int64_t batch, int64_t length, int64_t ra
 int mogt_fused_scan_fwd(const void* U, void* Y, int64_t batch, int64_t length, int64_t rank,
                         int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Reverse-time scan of the backward, G_t = X_t + U_{t+1}^T G_{t+1},
+ * G_{L-1} = X_{L-1}: the carry recursion of affine_scan_sequential_backward
+ * (affine_scan.py:110-118) and of _triton_affine_scan_hybrid_backward
+ * (triton_scan.py:397-416), on the matrix-core pipeline of
+ * mogt_affine_scan_fwd walking time backwards and reading U_{t+1} transposed
+ * (no reversed or transposed copy is built).  U [B,L,R,R], X, G [B,L,R,C]
+ * fp32; R <= 32, C > 0; workspace of mogt_affine_scan_workspace_bytes.     */
+int mogt_affine_scan_rev_fwd(const void* U, const void* X, void* G, int64_t batch, int64_t length,
+                             int64_t rank, int64_t channels, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* dU_t = G_t M_{t-1}^T of the backward (affine_scan.py:119-124 and
+ * triton_scan.py:417-418), M the forward state: M = H [B,L,R,C], or with P
+ * (the prefix products [B,L,R,R], when G carries their gradient too) the
+ * augmented M = [H | P]; M_{-1} = [0 | I].  G [B,L,R,C (+R)], dU [B,L,R,R];
+ * all fp32, R <= 32.  No workspace.                                        */
+int mogt_affine_scan_grad_u(const void* G, const void* H, const void* P, void* dU, int64_t batch,
+                            int64_t length, int64_t rank, int64_t channels, void* stream);
+
 /* Block-local affine scan: per block of `block_size` steps, the local prefixes
  * U_prefix/H_prefix [B, L, ...] and the per-block summaries U_summary
  * [B, nb, R, R] / H_summary [B, nb, R, C], nb = ceil(L / block_size); all

@@ -102,6 +102,10 @@ SIGNATURES: dict[str, tuple] = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
          _c_int, _c_void_p, _c_size, _c_void_p],
     ),
+    "mogt_affine_scan_rev_fwd": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p, _c_size, _c_void_p]),
+    "mogt_affine_scan_grad_u": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_void_p]),
     "mogt_affine_scan_generic_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "mogt_affine_scan_generic_fwd": (
         _c_int,

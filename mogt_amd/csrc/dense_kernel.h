@@ -20,6 +20,14 @@
 //   OUTPUT   X_0 = the chunk's carry; writes H_t (and P_t) after every step.
 // SUMMARY, EXCL and OUTPUT run chunks of exactly kDenseChunk steps (the last
 // one ragged), which fixes the trip count of the step loop at compile time.
+//
+// REV (level-0 SUMMARY and OUTPUT): the reverse-time recurrence of the
+// backward, G_t = X_t + U_{t+1}^T G_{t+1} (affine_scan.py:110-118), run as a
+// forward scan in reversed time s = L - 1 - t: the operands of step s are
+// X at memory step L - 1 - s and U at memory step L - s read transposed (zero
+// at s = 0, where the state before is zero), and outputs go to memory step
+// L - 1 - s.  The chunk summaries are then in reversed order already, so the
+// upper levels run unchanged.
 #pragma once
 
 #include "common.h"
@@ -75,8 +83,10 @@ constexpr int64_t kDenseNarrowWaves = 256;
 // of rows.  Otherwise V is read and H written one element at a time.
 // All global accesses of the step loop go through buffer descriptors, whose
 // range check zero-fills padding (see the addressing comment in the body).
-template <int RT, int CTW, bool WITHP, bool U4, bool W16, typename TV, typename TO, int MODE, bool VK>
+template <int RT, int CTW, bool WITHP, bool U4, bool W16, typename TV, typename TO, int MODE, bool VK, bool REV>
 __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
+    static_assert(!REV || (!U4 && !VK && (MODE == CM_SUMMARY || MODE == CM_OUTPUT)),
+                  "the reverse form reads U transposed, level 0 only");
     constexpr bool FIXED = MODE != CM_LOCAL;   // trip count kDenseChunk
     // OUTPUT passes write H (and P) non-temporally: lines left dirty in the
     // caches are otherwise written back while the next pass streams its
@@ -172,7 +182,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
 #pragma unroll
             for (int kk = 0; kk < (U4 ? 1 : 4); ++kk) {
                 const int r = 16 * rt + n, c = 16 * kt + 4 * g + kk;
-                offA[rt][kt][kk] = (r < R && c < R) ? (r * R + c) * 4 : kOOB;
+                offA[rt][kt][kk] = (r < R && c < R) ? (REV ? c * R + r : r * R + c) * 4 : kOOB;
             }
     // V: 16-byte pieces of the ROWS x VW block (VBLOCK) or one element per tile
     // register; VK: element i of v per tile row group and one element of k per
@@ -249,8 +259,12 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
         float kk[VK ? CTW : 1];  // VK: k columns of the column tiles
     };
     const int64_t seqStep = static_cast<int64_t>(b) * p.L;
+    // memory step of the operands / outputs of step t (REV: reversed time)
+    auto vrow = [&](int64_t t) { return REV ? p.L - 1 - t : t; };
     auto load_ops = [&](int64_t t, bool valid, Ops& o) {
-        const auto ru = rsrc(p.U + (seqStep + t) * RR, valid ? uBytes : 0u);
+        const int64_t tu = REV ? p.L - t : t;   // REV: U_{t'+1} of memory step t' = L - 1 - t
+        const auto ru = rsrc(p.U + (seqStep + (REV && t == 0 ? 0 : tu)) * RR,
+                             valid && !(REV && t == 0) ? uBytes : 0u);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -264,7 +278,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
                 }
             }
         if (!VBLOCK && !Vg) return;   // C == 0: no V (VBLOCK implies V)
-        const auto rv = rsrc(static_cast<const char*>(p.V) + (seqStep + t) * vBytes, valid ? vBytes : 0u);
+        const auto rv = rsrc(static_cast<const char*>(p.V) + (seqStep + vrow(t)) * vBytes, valid ? vBytes : 0u);
         auto ld1 = [](__amdgpu_buffer_rsrc_t r, int off) {   // one element as fp32 bits (bf16: raw)
             if constexpr (sizeof(TV) == 4) return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
             else return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
@@ -373,7 +387,7 @@ __global__ __launch_bounds__(64) void dense_chunk_kernel(ChunkParams p) {
     // Per-step output of the state X to row `t` (P columns when WITHP; H
     // columns); `valid` false (a padding step) stores nothing.
     auto store_state = [&](int64_t t, bool valid) {
-        const int64_t row = seqStep + t;
+        const int64_t row = seqStep + vrow(t);
         if constexpr (WITHP) {
             const auto rp = rsrc(static_cast<char*>(p.outP) + row * RR * ES, valid && p.outP ? pBytes : 0u);
 #pragma unroll
@@ -488,7 +502,7 @@ inline int dense_col_blocks(int64_t C, int ctw) {
     return C == 0 ? 1 : static_cast<int>((C + 16 * ctw - 1) / (16 * ctw));
 }
 
-template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE, bool VK>
+template <int RT, int CTW, bool U4, typename TV, typename TO, int MODE, bool VK, bool REV>
 int dense_launch_ct(const ChunkParams& c, int64_t B, hipStream_t st) {
     const dim3 grid(c.nb, dense_col_blocks(c.C, CTW), static_cast<unsigned>(B));
     auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
@@ -498,38 +512,43 @@ int dense_launch_ct(const ChunkParams& c, int64_t B, hipStream_t st) {
     constexpr bool alwaysP = MODE == CM_SUMMARY || MODE == CM_LOCAL;
     constexpr bool anyW16 = !(VK && MODE == CM_SUMMARY);   // VK summaries use neither path
     const bool wp = alwaysP || c.withP;
-    if (wp && w16 && anyW16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, anyW16, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
-    else if (wp) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, false, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
+    if (wp && w16 && anyW16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, anyW16, TV, TO, MODE, VK, REV>), grid, dim3(64), 0, st, c);
+    else if (wp) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, true, U4, false, TV, TO, MODE, VK, REV>), grid, dim3(64), 0, st, c);
     else if constexpr (!alwaysP) {
-        if (w16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, true, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
-        else hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, false, TV, TO, MODE, VK>), grid, dim3(64), 0, st, c);
+        if (w16) hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, true, TV, TO, MODE, VK, REV>), grid, dim3(64), 0, st, c);
+        else hipLaunchKernelGGL((dense_chunk_kernel<RT, CTW, false, U4, false, TV, TO, MODE, VK, REV>), grid, dim3(64), 0, st, c);
     }
     return check_launch("dense_chunk_kernel");
 }
 
-template <int RT, bool U4, typename TV, typename TO, int MODE, bool VK>
+template <int RT, bool U4, typename TV, typename TO, int MODE, bool VK, bool REV>
 int dense_launch_c(const ChunkParams& c, int64_t B, hipStream_t st) {
     const int ctw = dense_col_tiles(c.C);
     if (ctw > 1 && B * c.nb * dense_col_blocks(c.C, ctw) < kDenseNarrowWaves)
-        return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK>(c, B, st);
+        return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK, REV>(c, B, st);
     switch (ctw) {
-        case 1: return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK>(c, B, st);
-        case 2: return dense_launch_ct<RT, 2, U4, TV, TO, MODE, VK>(c, B, st);
-        case 3: return dense_launch_ct<RT, 3, U4, TV, TO, MODE, VK>(c, B, st);
-        default: return dense_launch_ct<RT, 4, U4, TV, TO, MODE, VK>(c, B, st);
+        case 1: return dense_launch_ct<RT, 1, U4, TV, TO, MODE, VK, REV>(c, B, st);
+        case 2: return dense_launch_ct<RT, 2, U4, TV, TO, MODE, VK, REV>(c, B, st);
+        case 3: return dense_launch_ct<RT, 3, U4, TV, TO, MODE, VK, REV>(c, B, st);
+        default: return dense_launch_ct<RT, 4, U4, TV, TO, MODE, VK, REV>(c, B, st);
     }
 }
 
 // One pass over a level.  U4: R % 4 == 0 and 16-byte aligned rows of U (level
 // >= 1 products live in the 256-byte aligned workspace).  The FIXED passes
 // require c.T == kDenseChunk.  VK: V_t = v_t k_t^T from c.V = v, c.K = k.
-template <typename TV, typename TO, int MODE, bool VK = false>
+template <typename TV, typename TO, int MODE, bool VK = false, bool REV = false>
 int dense_launch_pass(const ChunkParams& c, int64_t B, hipStream_t st) {
     if (MODE != CM_LOCAL && c.T != kDenseChunk)
         return set_error(MOGT_E_INVALID, "dense pass: chunk length %d, expected %d", c.T, kDenseChunk);
-    const bool u4 = c.R % 4 == 0 && reinterpret_cast<uintptr_t>(c.U) % 16 == 0;
-    if (c.R <= 16) return u4 ? dense_launch_c<1, true, TV, TO, MODE, VK>(c, B, st) : dense_launch_c<1, false, TV, TO, MODE, VK>(c, B, st);
-    return u4 ? dense_launch_c<2, true, TV, TO, MODE, VK>(c, B, st) : dense_launch_c<2, false, TV, TO, MODE, VK>(c, B, st);
+    if constexpr (REV) {   // transposed U: element loads
+        if (c.R <= 16) return dense_launch_c<1, false, TV, TO, MODE, VK, true>(c, B, st);
+        return dense_launch_c<2, false, TV, TO, MODE, VK, true>(c, B, st);
+    } else {
+        const bool u4 = c.R % 4 == 0 && reinterpret_cast<uintptr_t>(c.U) % 16 == 0;
+        if (c.R <= 16) return u4 ? dense_launch_c<1, true, TV, TO, MODE, VK, false>(c, B, st) : dense_launch_c<1, false, TV, TO, MODE, VK, false>(c, B, st);
+        return u4 ? dense_launch_c<2, true, TV, TO, MODE, VK, false>(c, B, st) : dense_launch_c<2, false, TV, TO, MODE, VK, false>(c, B, st);
+    }
 }
 
 // Instantiated once each in dense_pass_*.hip (parallel compilation).
@@ -553,5 +572,8 @@ int dense_launch_pass(const ChunkParams& c, int64_t B, hipStream_t st) {
     extern template int dense_launch_pass<TV, TO, M, VK>(const ChunkParams&, int64_t, hipStream_t);
 MOGT_DENSE_PASSES(MOGT_DENSE_EXTERN)
 #undef MOGT_DENSE_EXTERN
+// the reverse-time level-0 passes (dense_pass_rev.hip)
+extern template int dense_launch_pass<float, float, CM_SUMMARY, false, true>(const ChunkParams&, int64_t, hipStream_t);
+extern template int dense_launch_pass<float, float, CM_OUTPUT, false, true>(const ChunkParams&, int64_t, hipStream_t);
 
 }  // namespace mogt

@@ -110,6 +110,85 @@ int run_levels(const float* U, const void* V, const void* K, void* H, void* P, i
     return dense_launch_pass<TV, TO, CM_OUTPUT, VK>(c, B, st);
 }
 
+// The backward's reverse-time recurrence G_t = X_t + U_{t+1}^T G_{t+1}
+// (affine_scan.py:110-118): level 0 in reversed time with U read transposed
+// (the REV passes), the carries of its chunk summaries by the ordinary
+// recursion (they are already in reversed order), then G once.
+int run_rev(const float* U, const float* X, float* G, int64_t B, int64_t L, int64_t R, int64_t C, char* ws,
+            const DenseGeo& geo, hipStream_t st) {
+    ChunkParams c{};
+    c.U = U; c.V = X;
+    c.L = L; c.R = static_cast<int>(R); c.C = static_cast<int>(C); c.T = kDenseChunk;
+    c.nb = static_cast<int>((L + c.T - 1) / c.T);
+    c.withP = 0;
+    c.outH = G;
+    if (c.nb > 1) {
+        const Level& v = geo.lv[0];
+        ChunkParams s = c;
+        s.sumP = reinterpret_cast<float*>(ws + v.sumP);
+        s.sumH = reinterpret_cast<float*>(ws + v.sumH);
+        int rc = dense_launch_pass<float, float, CM_SUMMARY, false, true>(s, B, st);
+        if (rc) return rc;
+        rc = excl_scan<float>(s.sumP, s.sumH, c.nb, reinterpret_cast<float*>(ws + v.carP),
+                              reinterpret_cast<float*>(ws + v.carH), B, R, C, false, ws, geo, 1, st);
+        if (rc) return rc;
+        c.carH = reinterpret_cast<float*>(ws + v.carH);
+    }
+    return dense_launch_pass<float, float, CM_OUTPUT, false, true>(c, B, st);
+}
+
+// dU_t = G_t M_{t-1}^T for the augmented state M = [H | P] of the forward
+// scan (P: the prefix products, only when their gradient is part of G), with
+// M_{-1} = [0 | I]: the dU of affine_scan_sequential_backward
+// (affine_scan.py:119-124) on the augmented state.  One work-group per step
+// (b, t); G_t and M_{t-1} are staged through LDS 64 columns at a time (rows
+// padded by one float: the 16 or 32 rows a wave reads at one column fall in
+// distinct banks), and thread o accumulates elements o, o + 256, ... of the
+// R x R output.
+constexpr int kGuCols = 64;
+__global__ __launch_bounds__(256) void dense_grad_u_kernel(const float* __restrict__ G, const float* __restrict__ H,
+                                                           const float* __restrict__ P, float* __restrict__ dU,
+                                                           int64_t L, int R, int C, int CG) {
+    __shared__ float sG[32][kGuCols + 1];
+    __shared__ float sM[32][kGuCols + 1];
+    const int64_t row = blockIdx.x;            // b * L + t
+    const int64_t t = row % L;
+    const int tid = threadIdx.x;
+    const int RR = R * R;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < CG; c0 += kGuCols) {
+        for (int e = tid; e < R * kGuCols; e += 256) {
+            const int i = e / kGuCols, cc = e - i * kGuCols, c = c0 + cc;
+            float gv = 0.0f, mv = 0.0f;
+            if (c < CG) {
+                gv = G[(row * R + i) * CG + c];
+                if (c < C) mv = t > 0 ? H[((row - 1) * R + i) * C + c] : 0.0f;
+                else mv = t > 0 ? P[((row - 1) * R + i) * R + (c - C)] : (i == c - C ? 1.0f : 0.0f);
+            }
+            sG[i][cc] = gv;
+            sM[i][cc] = mv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int o = tid + 256 * k;
+            if (o < RR) {
+                const int i = o / R, j = o - (o / R) * R;
+                float a = acc[k];
+#pragma unroll 8
+                for (int cc = 0; cc < kGuCols; ++cc) a = fmaf(sG[i][cc], sM[j][cc], a);
+                acc[k] = a;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int o = tid + 256 * k;
+        if (o < RR) dU[row * RR + o] = acc[k];
+    }
+}
+
 int check_dense_shapes(int64_t B, int64_t L, int64_t R, int64_t C) {
     if (B < 0 || L < 0 || R <= 0 || C < 0)
         return set_error(MOGT_E_INVALID, "U must be [B, L, R, R] and V must be [B, L, R, C]");
@@ -218,4 +297,41 @@ extern "C" int mogt_affine_local_scan(const void* U, const void* V, void* U_pref
     hipStream_t st = static_cast<hipStream_t>(stream);
     return v_dtype == MOGT_BF16 ? dense_launch_pass<bf16_t, float, CM_LOCAL>(c, batch, st)
                                 : dense_launch_pass<float, float, CM_LOCAL>(c, batch, st);
+}
+
+extern "C" int mogt_affine_scan_rev_fwd(const void* U, const void* X, void* G, int64_t batch, int64_t length,
+                                        int64_t rank, int64_t channels, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+    clear_error();
+    int rc = check_dense_shapes(batch, length, rank, channels);
+    if (rc) return rc;
+    if (channels == 0) return set_error(MOGT_E_INVALID, "the reverse scan needs C > 0");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!U || !X || !G) return set_error(MOGT_E_INVALID, "null tensor pointer");
+    if (batch > 65535 || (length + kDenseChunk - 1) / kDenseChunk > 0x7fffffffLL)
+        return set_error(MOGT_E_INVALID, "problem too large for one launch");
+    const DenseGeo g = dense_geometry(batch, length, rank, channels);
+    if (!workspace || workspace_bytes < g.bytes)
+        return set_error(MOGT_E_WORKSPACE, "workspace of %zu bytes required, got %zu", g.bytes, workspace_bytes);
+    return run_rev(static_cast<const float*>(U), static_cast<const float*>(X), static_cast<float*>(G), batch, length,
+                   rank, channels, static_cast<char*>(workspace), g, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mogt_affine_scan_grad_u(const void* G, const void* H, const void* P, void* dU, int64_t batch,
+                                       int64_t length, int64_t rank, int64_t channels, void* stream) {
+    clear_error();
+    if (batch < 0 || length < 0 || rank <= 0 || channels < 0)
+        return set_error(MOGT_E_INVALID, "G must be [B, L, R, C (+ R)], H [B, L, R, C]");
+    if (rank > 32) return set_error(MOGT_E_INVALID, "R = %lld not supported (R <= 32)", (long long)rank);
+    if (channels > (1 << 22)) return set_error(MOGT_E_INVALID, "C too large");
+    if (batch == 0 || length == 0) return MOGT_OK;
+    if (!G || !dU || (channels > 0 && !H) || (channels == 0 && !P))
+        return set_error(MOGT_E_INVALID, "null tensor pointer");
+    if (batch * length > 0x7fffffffLL) return set_error(MOGT_E_INVALID, "problem too large for one launch");
+    const int CG = static_cast<int>(channels + (P ? rank : 0));
+    hipLaunchKernelGGL(dense_grad_u_kernel, dim3(static_cast<unsigned>(batch * length)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const float*>(G),
+                       static_cast<const float*>(H), static_cast<const float*>(P), static_cast<float*>(dU),
+                       length, static_cast<int>(rank), static_cast<int>(channels), CG);
+    return check_launch("dense_grad_u_kernel");
 }

@@ -773,21 +773,54 @@ def _forward_state(U: torch.Tensor, V: torch.Tensor, state_dtype: torch.dtype, p
     return (P, H) if prefix else H
 
 
+@torch.library.custom_op("mogt::affine_scan_rev", mutates_args=())
+def _affine_scan_rev_op(U: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
+    """G_t = X_t + U_{t+1}^T G_{t+1} on the matrix-core pipeline (fp32, R <= 32):
+    time walked backwards and U_{t+1} read transposed inside the kernels."""
+    lib = _lib.load()
+    U, X = U.contiguous(), X.contiguous()
+    B, L, R, C = X.shape
+    G = torch.empty_like(X)
+    ws = workspace(lib.mogt_affine_scan_workspace_bytes(B, L, R, C), X.device)
+    rc = lib.mogt_affine_scan_rev_fwd(U.data_ptr(), X.data_ptr(), G.data_ptr(), B, L, R, C, ws.data_ptr(),
+                                      ws.numel(), _stream_handle(X.device))
+    _lib.check(rc, "mogt_affine_scan_rev_fwd")
+    return G
+
+
+@_affine_scan_rev_op.register_fake
+def _(U, X):
+    return torch.empty_like(X)
+
+
+@torch.library.custom_op("mogt::affine_scan_grad_u", mutates_args=())
+def _affine_scan_grad_u_op(G: torch.Tensor, H: torch.Tensor, P: torch.Tensor | None) -> torch.Tensor:
+    """dU_t = G_t M_{t-1}^T with M = H or [H | P], M_{-1} = [0 | I] (fp32)."""
+    lib = _lib.load()
+    G, H = G.contiguous(), H.contiguous()
+    P = P.contiguous() if P is not None else None
+    B, L, R, C = H.shape
+    dU = torch.empty(B, L, R, R, dtype=torch.float32, device=G.device)
+    rc = lib.mogt_affine_scan_grad_u(G.data_ptr(), H.data_ptr(), P.data_ptr() if P is not None else None,
+                                     dU.data_ptr(), B, L, R, C, _stream_handle(G.device))
+    _lib.check(rc, "mogt_affine_scan_grad_u")
+    return dU
+
+
+@_affine_scan_grad_u_op.register_fake
+def _(G, H, P):
+    B, L, R, _ = H.shape
+    return H.new_empty(B, L, R, R)
+
+
 def _reverse_scan(U: torch.Tensor, X: torch.Tensor, state_dtype: torch.dtype) -> torch.Tensor:
     """G_t = X_t + U_{t+1}^T G_{t+1}, G_{L-1} = X_{L-1}, in the state dtype
-    (the carry recursion of affine_scan.py:110-118)."""
-    B, L, R, _ = U.shape
+    (the carry recursion of affine_scan.py:110-118): the matrix-core
+    pipeline's reverse mode for fp32 and R <= 32, the generic scan's
+    otherwise."""
+    R = U.shape[-1]
     if _use_mfma(R, state_dtype, state_dtype):
-        # the matrix-core pipeline scans forward: reversed sequence with
-        # U_back = [I, flip(U^T[1:])] (the construction of triton_scan.py:398-416)
-        Uf = U.to(torch.float32)
-        eye = torch.eye(R, device=U.device, dtype=torch.float32).view(1, 1, R, R).expand(B, 1, R, R)
-        if L > 1:
-            U_back = torch.cat([eye, Uf.transpose(-2, -1)[:, 1:].flip(1)], dim=1)
-        else:
-            U_back = eye.contiguous()
-        G_rev = torch.ops.mogt.affine_scan(U_back, X.to(torch.float32).flip(1).contiguous(), torch.float32)
-        return G_rev.flip(1)
+        return torch.ops.mogt.affine_scan_rev(U.to(torch.float32), X.to(torch.float32))
     _, G = torch.ops.mogt.affine_scan_generic(U, X, state_dtype, state_dtype, False, True)
     return G
 
@@ -809,6 +842,14 @@ def affine_scan_grad(U: torch.Tensor, V: torch.Tensor, grad_H: torch.Tensor | No
     grad_v = G[..., :C].to(V.dtype) if need_grad_v else None
     grad_u = None
     if need_grad_u:
+        if _use_mfma(R, state_dtype, state_dtype):
+            # dU from the recomputed forward state read in place (shifted by a step)
+            if grad_P is not None:
+                P, H = _forward_state(U, V, state_dtype, True)
+                grad_u = torch.ops.mogt.affine_scan_grad_u(G, H, P)
+            else:
+                grad_u = torch.ops.mogt.affine_scan_grad_u(G, _forward_state(U, V, state_dtype, False), None)
+            return grad_u.to(U.dtype), grad_v
         zeros = torch.zeros(B, 1, R, C, dtype=state_dtype, device=V.device)
         if grad_P is not None:
             P, H = _forward_state(U, V, state_dtype, True)

@@ -174,6 +174,38 @@ def test_backward_matches_oracle(gpu, R, C):
     assert rel_err(to_np(Ut.grad), gU_ref) <= FP32_TOL
 
 
+@pytest.mark.parametrize("B,L,R,C", [(1, 1, 4, 3), (2, 33, 16, 8), (1, 1000, 16, 48), (2, 3000, 5, 7),
+                                     (1, 5000, 32, 32), (1, 1100, 32, 40), (1, 32768, 16, 48)])
+def test_native_reverse_scan_and_grad_u(gpu, B, L, R, C):
+    """The backward on the matrix-core pipeline through the C ABI: the
+    reverse-time scan G_t = X_t + U_{t+1}^T G_{t+1} (mogt_affine_scan_rev_fwd,
+    time walked backwards, U read transposed; one step, ragged lengths, up to
+    three recursion levels, R = 32, C with and without 16-byte rows, the
+    core-operator shape) and dU_t = G_t H_{t-1}^T (mogt_affine_scan_grad_u)
+    against the oracle's backward recursion (affine_scan.py:110-124)."""
+    announce(f"dense native reverse scan B={B} L={L} R={R} C={C}")
+    from mogt_amd import _lib, ops
+
+    lib = _lib.load()
+    U, V = _stable_affine(B, L, R, C, seed=L + R)
+    X = synthetic.rng(L + C).standard_normal(V.shape, dtype=np.float32)
+    gU_ref, gV_ref = so.affine_scan_sequential_backward(U.astype(np.float64), V.astype(np.float64),
+                                                        X.astype(np.float64))
+    Ut, Vt, Xt = (torch.from_numpy(a).to(gpu) for a in (U, V, X))
+    G = torch.empty_like(Xt)
+    ws = ops.workspace(lib.mogt_affine_scan_workspace_bytes(B, L, R, C), gpu)
+    sh = ops._stream_handle(gpu)
+    _lib.check(lib.mogt_affine_scan_rev_fwd(Ut.data_ptr(), Xt.data_ptr(), G.data_ptr(), B, L, R, C,
+                                            ws.data_ptr(), ws.numel(), sh), "rev")
+    H = ops.affine_scan(Ut, Vt)
+    dU = torch.empty(B, L, R, R, device=gpu)
+    _lib.check(lib.mogt_affine_scan_grad_u(G.data_ptr(), H.data_ptr(), None, dU.data_ptr(), B, L, R, C, sh),
+               "grad_u")
+    torch.cuda.synchronize()
+    assert rel_err(to_np(G), gV_ref) <= FP32_TOL
+    assert rel_err(to_np(dU), gU_ref) <= FP32_TOL
+
+
 def test_core_operator_shape_full_length(gpu):
     """The reference's core-operator benchmark shape (U [1, 32768, 16, 16],
     V [1, 32768, 16, 48], fp32; the bench's dense_affine_r16_c48_L32768 line)
