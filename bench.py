@@ -168,14 +168,29 @@ def measure_diag_op(torch, L, steps, warmup, graph, D=768, B=1, sets=3):
                     mogt_amd.diag_scan(a, b)
             cur.wait_stream(s)
             torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
+            g = torch.cuda.CUDAGraph(keep_graph=True)
             with torch.cuda.graph(g, stream=s):
                 out = mogt_amd.diag_scan(a, b)
+            g.instantiate()
             graphs.append((g, out))
         torch.cuda.synchronize()
         fn = lambda i: graphs[i % sets][0].replay()
     ms = EventTimer(torch, cur).time(fn, steps, warmup)
-    return {"ms": ms}
+    return {"ms": ms, "graph_nodes": [graph_nodes(g) for g, _ in graphs] if graph else None}
+
+
+def graph_nodes(g):
+    """Number of nodes of a captured graph (hipGraphGetNodes on its raw
+    hipGraph_t), so a replay's cost can be told apart from extra captured work."""
+    import ctypes
+
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+    except OSError:
+        return None
+    n = ctypes.c_size_t(0)
+    rc = hip.hipGraphGetNodes(ctypes.c_void_p(g.raw_cuda_graph()), None, ctypes.byref(n))
+    return int(n.value) if rc == 0 else None
 
 
 def measure_diag_rev(torch, lib, ops, L, steps, warmup, D=768, B=1, sets=3):
@@ -825,20 +840,24 @@ def main():
                 rg_ = measure_diag_op(torch, L, args.steps, args.warmup, graph=True)
                 extras[f"diag_fp32_L{L}_op_level"] = {
                     "eager_us": round(re_["ms"] * 1e3, 2), "graph_us": round(rg_["ms"] * 1e3, 2),
-                    "note": "mogt_amd.diag_scan per call (custom-op dispatch, output allocation, launch), "
-                            "and the same call replayed from a HIP graph"}
+                    "graph_nodes": rg_["graph_nodes"],
+                    "note": "mogt_amd.diag_scan per call (eager: input checks, output allocation, C-ABI launch; "
+                            "the custom-op dispatch is taken only under autograd or tracing), and the same call "
+                            "captured in a HIP graph and replayed (graph_nodes: nodes per captured graph)"}
             r = measure_diag_rev(torch, lib, ops, 32768, args.steps, args.warmup)
             extras["diag_rev_fp32_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                 "note": "backward reverse scan G_t = dH_t + a_{t+1} G_{t+1} at the headline shape"}
         if full or "coupled" in only:
+            log("extras: coupled mixer scan")
             r = measure_coupled(torch, lib, ops, 32768, args.steps, args.warmup)
             extras["coupled_rank_scan_r16c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                 "note": "z fp32 [1,L,16] + v bf16 [1,L,768] -> h fp32; model-shaped 2' case"}
         if full or "rank1" in only:
+            log("extras: rank-1 scan (configs[2])")
             r = measure_rank1(torch, lib, ops, args.steps, args.warmup)
             r3 = measure_rank1(torch, lib, ops, args.steps, args.warmup, path=2)
             extras["rank1_coupled_cfg3_b2_h12_d64_L8192_bf16"] = {
@@ -848,6 +867,7 @@ def main():
                 "note": "BASELINE configs[2]; algorithmic bytes 101.1 MB (f,k,v,q in, y out); us: one launch "
                         "(carries exchanged between work-groups), three_launch_us: summaries, carries, outputs"}
         if full or "dense" in only:
+            log("extras: dense scan (core shape, configs[3])")
             r = measure_dense(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
             extras["dense_affine_r16_c48_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
@@ -870,6 +890,7 @@ def main():
                 "note": "configs[3] with B_t = v_t k_t^T formed in registers (dense_scan(A, v, k)): "
                         "U [8,L,32,32] + v, k [8,L,32] in, S fp32 out"}
         if full or "dense" in only:
+            log("extras: dense backward, generic scan")
             r = measure_dense_backward(torch, lib, ops, 1, 32768, 16, 48, max(5, args.steps // 5), 2)
             extras["dense_affine_r16_c48_L32768_backward"] = {
                 "reverse_scan_us": round(r["rev_ms"] * 1e3, 2), "reverse_scan_GB/s": round(r["rev_gbs"], 1),
@@ -889,6 +910,7 @@ def main():
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),
                 "note": "R = 64 (above the matrix-core pipeline's 32): fp32 on the generic scan"}
         if full:
+            log("extras: connection maps, cross-entropy rows")
             for impl in ("matrix_exp", "cayley"):
                 r = measure_connection_map(torch, lib, ops, impl, 32768, 16, args.steps, args.warmup)
                 extras[f"connection_map_{impl}_r16_n32768"] = {
@@ -909,6 +931,7 @@ def main():
                         "the GEMMs are the BLAS library's in both; reference = chunked_lm_loss.py's "
                         "torch ops on the same GPU"}
         if full or "swiglu" in only:
+            log("extras: fused SwiGLU GEMM")
             r = measure_swiglu(torch, args.steps, args.warmup)
             extras["swiglu_gate_gemm_32768x768_to_3072_bf16"] = {
                 "us": round(r["ms"] * 1e3, 2), "TFLOP/s": round(r["tflops"], 1),
@@ -921,10 +944,13 @@ def main():
 
             # the libraries' default GEMM choice first, then the tuned table
             # (mogt_amd/tuning/gemm_gfx950.csv); both are reported
+            log("extras: backbone forward (default GEMMs)")
             d4 = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3)
             d2 = measure_backbone(torch, 2, None, 4096, 32768, 10, 3)
+            log("extras: backbone training step (default GEMMs)")
             dt = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True)
             tuned = gemm_tuning.use_tuned_gemms()
+            log(f"extras: backbone forward, tuned GEMM table {tuned}")
             r = measure_backbone(torch, 4, 3072, 32000, 32768, 10, 3) if tuned else d4
             extras["mogt_backbone_4layer_d768_L32768_bf16_ms"] = dict(
                 r, ffn_hidden=3072, vocab=32000, default_gemms_ms=d4["ms"], tuned_gemm_table=tuned,
@@ -936,6 +962,7 @@ def main():
             extras["mogt_backbone_2layer_refffn_L32768_bf16_ms"] = dict(
                 r, ffn_hidden=2048, vocab=4096, default_gemms_ms=d2["ms"], tuned_gemm_table=tuned,
                 note="like-for-like with the reference's 77.56 ms (2 layers, FFN 2048, NVIDIA L4)")
+            log("extras: backbone length sweep")
             extras["mogt_backbone_length_sweep"] = {
                 "4layer_ffn3072_vocab32000": backbone_lengths(torch, 4, 3072, 32000),
                 "2layer_refffn_vocab4096": backbone_lengths(torch, 2, None, 4096),
@@ -947,6 +974,7 @@ def main():
             # 10 warm-up steps: the first training steps of a process run slow for
             # ~0.2 s of wall time (measured 27 ms/step with 2-5 warm-up steps, 14.5
             # with 10-20), independent of which path runs first
+            log("extras: backbone training step (tuned GEMMs, generic path)")
             rf = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=True) if tuned else dt
             rg = measure_backbone_train(torch, 4, 3072, 32000, 32768, 5, 10, fused=False)
             extras["mogt_backbone_4layer_d768_L32768_bf16_train_step_ms"] = dict(

@@ -148,6 +148,18 @@ def _checked(ws: torch.Tensor, what: str) -> None:
             raise WorkspaceFault(f"{what}: {n} look-back wait(s) gave up; the output is invalid (NaN)")
 
 
+def _direct(*tensors: torch.Tensor) -> bool:
+    """Whether a public op may call its implementation directly: a plain eager
+    call on real tensors with no autograd recording and no compiler tracing,
+    where the custom-op dispatch would only add host time (about 13 us per
+    call, more than a short scan's kernel).  Everything else goes through
+    ``torch.ops.mogt.*`` (autograd, fake tensors, torch.compile)."""
+    if torch.compiler.is_compiling():
+        return False
+    grad = torch.is_grad_enabled()
+    return all(type(t) is torch.Tensor and not (grad and t.requires_grad) for t in tensors)
+
+
 def require_cuda(what: str, *tensors: torch.Tensor) -> None:
     for t in tensors:
         if t.device.type != "cuda":
@@ -193,8 +205,7 @@ def _check_diag_inputs(a: torch.Tensor, b: torch.Tensor) -> None:
     dtype_code(a.dtype, "diag_scan")
 
 
-@torch.library.custom_op("mogt::diag_scan", mutates_args=())
-def _diag_scan_op(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+def _diag_scan_impl(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     a = a.contiguous()
     b = b.contiguous()
     h = torch.empty(a.shape, dtype=out_dtype, device=a.device)
@@ -202,20 +213,25 @@ def _diag_scan_op(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype) -> t
     return h
 
 
+_diag_scan_op = torch.library.custom_op("mogt::diag_scan", _diag_scan_impl, mutates_args=())
+
+
 @_diag_scan_op.register_fake
 def _(a, b, out_dtype):
     return a.new_empty(a.shape, dtype=out_dtype)
 
 
-@torch.library.custom_op("mogt::diag_scan_prefix", mutates_args=())
-def _diag_scan_prefix_op(a: torch.Tensor, b: torch.Tensor,
-                         out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+def _diag_scan_prefix_impl(a: torch.Tensor, b: torch.Tensor,
+                           out_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
     a = a.contiguous()
     b = b.contiguous()
     h = torch.empty(a.shape, dtype=out_dtype, device=a.device)
     pre = torch.empty(a.shape, dtype=out_dtype, device=a.device)
     _diag_scan_launch(a, b, h, pre)
     return pre, h
+
+
+_diag_scan_prefix_op = torch.library.custom_op("mogt::diag_scan_prefix", _diag_scan_prefix_impl, mutates_args=())
 
 
 @_diag_scan_prefix_op.register_fake
@@ -288,6 +304,8 @@ def diag_scan(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype | None
     _check_diag_inputs(a, b)
     out_dtype = out_dtype or b.dtype
     dtype_code(out_dtype, "diag_scan")
+    if _direct(a, b):
+        return _diag_scan_prefix_impl(a, b, out_dtype) if return_prefix else _diag_scan_impl(a, b, out_dtype)
     if return_prefix:
         return torch.ops.mogt.diag_scan_prefix(a, b, out_dtype)
     return torch.ops.mogt.diag_scan(a, b, out_dtype)
@@ -296,9 +314,8 @@ def diag_scan(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype | None
 # ---------------------------------------------------------------------------
 # coupled_rank_scan: MOGT mixer scan with identity connection and rank gate
 # ---------------------------------------------------------------------------
-@torch.library.custom_op("mogt::coupled_rank_scan", mutates_args=())
-def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: float,
-                          out_dtype: torch.dtype) -> torch.Tensor:
+def _coupled_rank_scan_impl(z: torch.Tensor, v: torch.Tensor, rank: int, damping: float,
+                            out_dtype: torch.dtype) -> torch.Tensor:
     lib = _lib.load()
     z = z.contiguous()
     v = v.contiguous()
@@ -316,6 +333,10 @@ def _coupled_rank_scan_op(z: torch.Tensor, v: torch.Tensor, rank: int, damping: 
     _lib.check(rc, "mogt_coupled_rank_scan_fwd")
     _checked(ws, "mogt_coupled_rank_scan_fwd")
     return h
+
+
+_coupled_rank_scan_op = torch.library.custom_op("mogt::coupled_rank_scan", _coupled_rank_scan_impl,
+                                                mutates_args=())
 
 
 @_coupled_rank_scan_op.register_fake
@@ -636,6 +657,8 @@ def coupled_rank_scan(gate_logits: torch.Tensor, v_raw: torch.Tensor, *, damping
     B, L, r = gate_logits.shape
     if v_raw.shape[:2] != (B, L) or v_raw.shape[2] % r != 0:
         raise ValueError("gate_logits must be [B, L, r] and v_raw [B, L, r*c]")
+    if _direct(gate_logits, v_raw):
+        return _coupled_rank_scan_impl(gate_logits, v_raw, r, float(damping), out_dtype)
     return torch.ops.mogt.coupled_rank_scan(gate_logits, v_raw, r, float(damping), out_dtype)
 
 
@@ -1705,9 +1728,8 @@ def _rank1_launch(f, k, v, q, y, path: int) -> torch.Tensor:
     return ws if single else None
 
 
-@torch.library.custom_op("mogt::rank1_coupled_scan", mutates_args=())
-def _rank1_op(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
-              out_dtype: torch.dtype, path: int) -> torch.Tensor:
+def _rank1_impl(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor,
+                out_dtype: torch.dtype, path: int) -> torch.Tensor:
     f, k, v, q = (t.contiguous() for t in (f, k, v, q))
     y = torch.empty(k.shape, dtype=out_dtype, device=k.device)
     ws = _rank1_launch(f, k, v, q, y, path)
@@ -1721,6 +1743,9 @@ def _rank1_op(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: torch.Tensor
                           "recomputed with the three-launch path", RuntimeWarning, stacklevel=2)
             _rank1_launch(f, k, v, q, y, RANK1_PATHS["three"])
     return y
+
+
+_rank1_op = torch.library.custom_op("mogt::rank1_coupled_scan", _rank1_impl, mutates_args=())
 
 
 @_rank1_op.register_fake
@@ -1746,6 +1771,8 @@ def rank1_coupled_scan(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: tor
         raise ValueError("k, v and q must share a dtype")
     if k.shape[-1] != 64:
         raise ValueError(f"head dim {k.shape[-1]} not supported (64)")
+    if _direct(f, k, v, q):
+        return _rank1_impl(f, k, v, q, out_dtype or q.dtype, RANK1_PATHS[path])
     return torch.ops.mogt.rank1_coupled_scan(f, k, v, q, out_dtype or q.dtype, RANK1_PATHS[path])
 
 
