@@ -399,6 +399,30 @@ int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, in
  *   ldy % 4 == 0; x and weights 16-byte aligned, y 8-byte aligned.           */
 int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
                          int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, void* stream);
+/* mogt_linear_wgrad: dW = dY^T X, the weight gradient of a bias-free
+ *   nn.Linear (model_mogt.py:25-27 w1, w2, w3, :57 phi_val, :61 theta_read;
+ *   the grad_weight torch's linear backward forms), as a split-K GEMM on the
+ *   matrix cores: the tokens are cut into `splits` slices, fp32 partials of
+ *   every slice go to the workspace, and a second kernel sums them in slice
+ *   order (deterministic) and rounds once.  dY [tokens, d_out] (row stride
+ *   ldd) and X [tokens, d_in] (row stride ldx) bf16; dW [d_out, d_in] (row
+ *   stride ldw) in out_dtype (MOGT_BF16 or MOGT_F32); fp32 accumulation.
+ *   d_out, d_in and the strides multiples of 8; dY, X, dW and the workspace
+ *   16-byte aligned.  splits <= 0 picks enough slices to give each CU one
+ *   work-group.  tokens == 0 writes zeros.  A slice's bytes (slice tokens x
+ *   row stride x 2) must stay under 2 GiB (MOGT_E_INVALID asks for more
+ *   splits).
+ * mogt_linear_wgrad_splits: the slice count a launch with these arguments
+ *   uses (cus: the device's CU count, or <= 0 to query the current device);
+ *   -1 for a bad shape.
+ * mogt_linear_wgrad_workspace_bytes: splits x d_out x d_in x 4 for that
+ *   count (0 without tokens).                                                 */
+int mogt_linear_wgrad(const void* dy, const void* x, void* dw, int64_t tokens, int64_t d_out, int64_t d_in,
+                      int64_t ldd, int64_t ldx, int64_t ldw, int64_t splits, int out_dtype, void* workspace,
+                      size_t workspace_bytes, void* stream);
+int64_t mogt_linear_wgrad_splits(int64_t tokens, int64_t d_out, int64_t d_in, int64_t splits, int64_t cus);
+size_t mogt_linear_wgrad_workspace_bytes(int64_t tokens, int64_t d_out, int64_t d_in, int64_t splits,
+                                         int64_t cus);
 /* mogt_add_rmsnorm_fwd for a read-out of an unnormalised row: z = W diag(w) h
  * (theta_read with norm_out's weight folded in), row_stats [rows, n_stats] the
  * partial sums of squares of h (mogt_coupled_rank_scan_stats_fwd).  With r =

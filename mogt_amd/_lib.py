@@ -18,7 +18,7 @@ MOGT_F64 = 2
 MOGT_F16 = 3
 MOGT_CONN_EXP = 0
 MOGT_CONN_CAYLEY = 1
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _c_void_p = ctypes.c_void_p
 _c_i64 = ctypes.c_int64
@@ -135,6 +135,11 @@ SIGNATURES: dict[str, tuple] = {
     "mogt_swiglu_gate_fwd": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
                  _c_void_p]),
+    "mogt_linear_wgrad": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+                 _c_void_p, _c_size, _c_void_p]),
+    "mogt_linear_wgrad_splits": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "mogt_linear_wgrad_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "mogt_add_rmsnorm_rowscale_fwd": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_float, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_i64,

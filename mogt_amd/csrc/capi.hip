@@ -31,7 +31,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* mogt_last_error(void) { return mogt::g_last_error; }
 
-extern "C" int mogt_abi_version(void) { return 10; }
+extern "C" int mogt_abi_version(void) { return 11; }
 
 // "name:sha256[:12];..." of the sources and compiler flags this library was
 // built from, passed in by the build script (mogt_amd/_build.py).

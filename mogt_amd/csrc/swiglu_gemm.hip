@@ -37,7 +37,7 @@
 // rows of those 8 blocks while it sweeps the weight blocks.
 #include <type_traits>
 
-#include "common.h"
+#include "lds_dma.h"
 
 namespace mogt {
 namespace {
@@ -45,7 +45,6 @@ namespace {
 typedef __bf16 sg_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sg_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t sg_u32x2 __attribute__((ext_vector_type(2)));
-typedef int sg_i32x4 __attribute__((ext_vector_type(4)));
 typedef float sg_f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 sg_bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -84,31 +83,6 @@ __device__ __forceinline__ void sg_round2(float lo, float hi, float& rlo, float&
     rhi = __uint_as_float(w & 0xffff0000u);
 }
 
-// 64 lanes x 16 bytes from (rsrc, voff + soff) into LDS at lds .. lds + 1023
-__device__ __forceinline__ void sg_dma16(sg_i32x4 rsrc, int voff, int soff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-                 : "memory", "m0");
-}
-
-// wait until at most N vector memory operations of this wave are outstanding
-template <int N>
-__device__ __forceinline__ void sg_wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-__device__ __forceinline__ sg_i32x4 sg_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    sg_i32x4 r;
-    r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-    r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));   // stride 0
-    r[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-    r[3] = 0x00020000;
-    return r;
-}
-
 // block id -> (row block, output block)
 __device__ __forceinline__ void sg_tile(const SwigluParams& p, int& mb, int& nb) {
     const int n = p.n_mb * p.n_nb;
@@ -134,15 +108,14 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, hb = lane >> 5;
-    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-        (__attribute__((address_space(3))) char*)smem));
+    const uint32_t lds0 = lds_addr(smem);
 
     // loads: wave w fills rows 64 w .. 64 w + 63 of each operand, 16 rows
     // (1 KB) per instruction; lane L takes row 16 i + L / 4 of its block and
     // the global chunk that lands in LDS slot L % 4 under the swizzle
     const int64_t mrows = p.rows - m0 < SG_BM ? p.rows - m0 : SG_BM;
-    const sg_i32x4 rx = sg_rsrc(p.x + m0 * p.ldx, static_cast<uint32_t>(mrows * p.ldx * 2));
-    const sg_i32x4 rw = sg_rsrc((wave < 2 ? p.wg : p.wu) + static_cast<int64_t>(n0) * p.K,
+    const lds_i32x4 rx = lds_rsrc(p.x + m0 * p.ldx, static_cast<uint32_t>(mrows * p.ldx * 2));
+    const lds_i32x4 rw = lds_rsrc((wave < 2 ? p.wg : p.wu) + static_cast<int64_t>(n0) * p.K,
                                 static_cast<uint32_t>(SG_BN * p.K * 2));
     const int lc = (lane & 3) ^ (((lane >> 3) ^ (lane >> 4)) & 3);
     int vx[4], vw[4];
@@ -159,9 +132,9 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
         const uint32_t st = (s & (SG_NST - 1)) * SG_STB;
         const int kb = s * SG_ROWB;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sg_dma16(rx, vx[i], kb, ldx_dst + st + i * 1024);
+        for (int i = 0; i < 4; ++i) lds_dma16(rx, vx[i], kb, ldx_dst + st + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sg_dma16(rw, vw[i], kb, ldw_dst + st + i * 1024);
+        for (int i = 0; i < 4; ++i) lds_dma16(rw, vw[i], kb, ldw_dst + st + i * 1024);
     };
 
     // fragment rows: x rows wm*128 + 32 i + l32; weight rows (gate) 64 wn + 32 j
@@ -216,7 +189,7 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     auto steady = [&](int s, const sg_bf16x8 (&cur)[8], sg_bf16x8 (&next)[8], auto first) {
         mfma_half(a, first);
         __builtin_amdgcn_sched_barrier(0);
-        sg_wait_vm<8>();
+        lds_wait_vm<8>();
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t dst = ((s + 3) & (SG_NST - 1)) * SG_STB;
@@ -227,9 +200,9 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
             const int j = t >> 2, i = t & 3;
             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[4 + j], cur[i], acc[j][i], 0, 0, 0);
             if (t < 4)
-                sg_dma16(rx, vx[t], kb, ldx_dst + dst + t * 1024);
+                lds_dma16(rx, vx[t], kb, ldx_dst + dst + t * 1024);
             else if (t < 8)
-                sg_dma16(rw, vw[t - 4], kb, ldw_dst + dst + (t - 4) * 1024);
+                lds_dma16(rw, vw[t - 4], kb, ldw_dst + dst + (t - 4) * 1024);
             if (t < 8)
                 a[t] = *frag_ptr(stn, 0, t);
             else
@@ -242,11 +215,11 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     if (nk > 1) issue(1);
     if (nk > 2) issue(2);
     if (nk > 2)
-        sg_wait_vm<16>();
+        lds_wait_vm<16>();
     else if (nk > 1)
-        sg_wait_vm<8>();
+        lds_wait_vm<8>();
     else
-        sg_wait_vm<0>();
+        lds_wait_vm<0>();
     __syncthreads();
     read_stage(0, a, b);
     int s = 0;
@@ -277,9 +250,9 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
         __builtin_amdgcn_sched_barrier(0);
         if (s + 1 < nk) {
             if (s + 2 < nk)
-                sg_wait_vm<8>();
+                lds_wait_vm<8>();
             else
-                sg_wait_vm<0>();
+                lds_wait_vm<0>();
             __syncthreads();
             read_stage(s + 1, a, c);
         }

@@ -1328,6 +1328,102 @@ def swiglu_gate(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> to
     return y.reshape(*lead, w_gate.shape[0])
 
 
+# weight gradient of the training path's linear layers ---------------------
+WGRAD_MULTIPLE = 8   # d_out, d_in and row strides of mogt_linear_wgrad
+
+
+def _wgrad_rows(t: torch.Tensor) -> torch.Tensor:
+    """``t`` as [tokens, features] rows the kernel takes (unit column stride,
+    row stride a multiple of 8, 16-byte aligned), copying only if needed."""
+    r = t.reshape(-1, t.shape[-1])
+    if r.stride(-1) != 1 or r.stride(0) % WGRAD_MULTIPLE != 0 or r.data_ptr() % 16 != 0 or r.stride(0) < r.shape[1]:
+        r = r.contiguous()
+    return r
+
+
+def _linear_wgrad_impl(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype, splits: int = 0) -> torch.Tensor:
+    lib = _lib.load()
+    d2, x2 = _wgrad_rows(dy), _wgrad_rows(x)
+    T, O = d2.shape
+    I = x2.shape[1]
+    dw = torch.empty((O, I), dtype=out_dtype, device=dy.device)
+    nbytes = int(lib.mogt_linear_wgrad_workspace_bytes(T, O, I, splits, 0))
+    ws = workspace(nbytes, dy.device)
+    rc = lib.mogt_linear_wgrad(d2.data_ptr(), x2.data_ptr(), dw.data_ptr(), T, O, I, d2.stride(0), x2.stride(0),
+                               dw.stride(0), splits, dtype_code(out_dtype, "linear_wgrad"), ws.data_ptr(), ws.numel(),
+                               _stream_handle(dy.device))
+    _lib.check(rc, "mogt_linear_wgrad")
+    return dw
+
+
+@torch.library.custom_op("mogt::linear_wgrad", mutates_args=())
+def _linear_wgrad_op(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype, splits: int = 0) -> torch.Tensor:
+    """dW = dY^T X over the flattened leading dimensions."""
+    return _linear_wgrad_impl(dy, x, out_dtype, splits)
+
+
+@_linear_wgrad_op.register_fake
+def _(dy, x, out_dtype, splits=0):
+    return dy.new_empty((dy.shape[-1], x.shape[-1]), dtype=out_dtype)
+
+
+def linear_wgrad_supported(dy: torch.Tensor, x: torch.Tensor) -> bool:
+    """Whether ``linear_wgrad`` takes these operands: bf16 CUDA tensors with
+    the same leading shape and both feature sizes multiples of 8."""
+    return (dy.is_cuda and x.is_cuda and dy.dtype == torch.bfloat16 and x.dtype == torch.bfloat16
+            and dy.ndim >= 1 and dy.shape[:-1] == x.shape[:-1] and dy.shape[-1] % WGRAD_MULTIPLE == 0
+            and x.shape[-1] % WGRAD_MULTIPLE == 0 and dy.shape[-1] > 0 and x.shape[-1] > 0)
+
+
+def linear_wgrad(dy: torch.Tensor, x: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16,
+                 splits: int = 0) -> torch.Tensor:
+    """``dy.reshape(-1, O).T @ x.reshape(-1, I)``, the weight gradient of a
+    bias-free linear layer ``y = x @ W.T`` (model_mogt.py:25-27, 57, 61), as
+    the HIP split-K GEMM: fp32 partials per token slice, summed in slice order
+    and rounded once to ``out_dtype`` (bf16 or float32).  ``splits`` <= 0
+    picks the slice count that gives every CU one work-group.  No autograd."""
+    require_cuda("linear_wgrad", dy, x)
+    if not linear_wgrad_supported(dy, x):
+        raise ValueError("linear_wgrad needs bf16 dy [..., O] and x [..., I] with equal leading shapes and "
+                         "O % 8 == 0, I % 8 == 0")
+    if _direct(dy, x):
+        return _linear_wgrad_impl(dy, x, out_dtype, int(splits))
+    return torch.ops.mogt.linear_wgrad(dy, x, out_dtype, int(splits))
+
+
+class _Linear(torch.autograd.Function):
+    """``y = x @ w.T`` (a bias-free nn.Linear, F.linear's own GEMM); backward:
+    ``dx = dy @ w`` with the same library GEMM autograd would call, and ``dw``
+    by the split-K weight-gradient kernel in ``w``'s dtype."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        dx = g.matmul(w) if ctx.needs_input_grad[0] else None
+        dw = None
+        if ctx.needs_input_grad[1]:
+            dw = torch.ops.mogt.linear_wgrad(g, x, w.dtype, 0) if linear_wgrad_supported(g, x) \
+                else g.reshape(-1, g.shape[-1]).t().mm(x.reshape(-1, x.shape[-1]))
+        return dx, dw
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, w)`` whose weight gradient, when ``w`` needs one and the
+    operands are bf16 on the GPU with feature sizes that are multiples of 8,
+    comes from ``linear_wgrad`` instead of the library GEMM (whose d_out x
+    d_in output has too few tiles to fill the GPU at the model's widths)."""
+    if (torch.is_grad_enabled() and w.requires_grad and x.is_cuda and x.dtype == torch.bfloat16
+            and w.dtype == torch.bfloat16 and w.ndim == 2 and x.shape[-1] == w.shape[1]
+            and w.shape[0] % WGRAD_MULTIPLE == 0 and w.shape[1] % WGRAD_MULTIPLE == 0):
+        return _Linear.apply(x, w)
+    return F.linear(x, w)
+
+
 # token embedding with a deterministic HIP backward -------------------------
 EMBEDDING_BLOCK = 16   # sorted positions per block of mogt_embedding_bwd
 

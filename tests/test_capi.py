@@ -106,6 +106,44 @@ def test_argument_errors_without_device(lib):
     assert rc == -1 and b"align" in lib.mogt_last_error()
 
 
+def test_linear_wgrad_plan_and_checks_without_device(lib):
+    """The split-K weight-gradient GEMM's slice plan and argument checks are
+    host-only.  Plan: enough slices to give each CU one 256 x 256 work-group
+    tile (256 CUs), whole 32-token stages per slice, no empty slice."""
+    plan = lib.mogt_linear_wgrad_splits
+    assert plan(32768, 768, 768, 0, 256) == 28        # 9 tiles
+    assert plan(32768, 800, 768, 0, 256) == 21        # 12 tiles (a partial row of tiles)
+    assert plan(32768, 768, 3072, 0, 256) == 7        # 36 tiles
+    assert plan(32768, 6144, 768, 0, 256) == 3        # 72 tiles
+    assert plan(32768, 8192, 8192, 0, 256) == 1       # more tiles than CUs
+    assert plan(200, 768, 768, 0, 256) == 1           # under two minimum slices of 128 tokens
+    assert plan(0, 768, 768, 0, 256) == 0
+    assert plan(4096, 16, 16, 4096, 256) == 128       # explicit: capped at one stage per slice
+    assert plan(4097, 16, 16, 3, 256) == 3            # slices of 1376 tokens, the last one 1345
+    assert plan(10, 8, 8, 0, 256) == 1
+    assert plan(-1, 8, 8, 0, 256) == -1 and plan(8, 0, 8, 0, 256) == -1
+    assert lib.mogt_linear_wgrad_workspace_bytes(32768, 768, 768, 0, 256) == 28 * 768 * 768 * 4
+    assert lib.mogt_linear_wgrad_workspace_bytes(0, 768, 768, 0, 256) == 0
+    N = None
+    # dW dtype, feature multiples of 8, strides, alignment, workspace size:
+    # all rejected before any HIP call (explicit splits: no device query)
+    call = lib.mogt_linear_wgrad
+    assert call(16, 16, 16, 64, 16, 16, 16, 16, 16, 1, 2, 16, 1 << 20, N) == -1
+    rc = call(16, 16, 16, 64, 12, 16, 16, 16, 16, 1, 1, 16, 1 << 20, N)
+    assert rc == -1 and b"multiples of 8" in lib.mogt_last_error()
+    rc = call(16, 16, 16, 64, 16, 16, 8, 16, 16, 1, 1, 16, 1 << 20, N)
+    assert rc == -1 and b"stride" in lib.mogt_last_error()
+    rc = call(8, 16, 16, 64, 16, 16, 16, 16, 16, 1, 1, 16, 1 << 20, N)
+    assert rc == -1 and b"align" in lib.mogt_last_error()
+    rc = call(16, 16, 16, 64, 16, 16, 16, 16, 16, 2, 1, 16, 16 * 16 * 4, N)
+    assert rc == -2 and b"workspace" in lib.mogt_last_error()
+    rc = call(16, N, 16, 64, 16, 16, 16, 16, 16, 1, 1, 16, 1 << 20, N)
+    assert rc == -1 and b"null" in lib.mogt_last_error()
+    # a slice whose rows span 2 GiB asks for more splits
+    rc = call(16, 16, 16, 1 << 20, 1024, 1024, 1024, 1024, 1024, 1, 1, 16, 1 << 62, N)
+    assert rc == -1 and b"splits" in lib.mogt_last_error()
+
+
 def test_empty_problems_are_noops_without_device(lib):
     """Zero batch, length or rows: every compute entry point returns success
     before it needs a pointer or the device."""

@@ -2,9 +2,10 @@
 blocks (built from parameters, reused only while no gradient is recorded and
 no parameter changed), the workspace families and checked-mode accounting,
 bench.py's profile provenance, the rocprof summariser, the rank-1 kernels'
-buffer ranges, and the m0 use of the fused SwiGLU GEMM's generated code."""
+buffer ranges, and the m0 use of the bf16 GEMMs' generated code."""
 from pathlib import Path
 
+import pytest
 import torch
 import torch.nn as nn
 
@@ -265,13 +266,15 @@ def test_checked_mode_reports_each_give_up_once(monkeypatch):
         ops._checked(ws, "scan")                  # one more
 
 
-def test_swiglu_m0_only_feeds_lds_dma(tmp_path):
-    """The fused SwiGLU GEMM sets m0 in inline assembly for its direct-to-LDS
-    loads (clang warns that m0 is reserved).  On the code this build generates
-    for gfx950: every write of m0 is one of those asm blocks, immediately
-    followed by the load that reads it, and no other instruction of the kernel
-    reads m0 (no LDS-direct, interpolation, GWS, movrel or message
-    instructions), so no compiler-held m0 value is overwritten."""
+@pytest.mark.parametrize("source", ["swiglu_gemm.hip", "wgrad_gemm.hip"])
+def test_gemm_m0_only_feeds_lds_dma(tmp_path, source):
+    """The bf16 GEMMs (fused SwiGLU, split-K weight gradient) set m0 in inline
+    assembly for their direct-to-LDS loads (clang warns that m0 is reserved).
+    On the code this build generates for gfx950: every write of m0 is one of
+    those asm blocks, immediately followed by the load that reads it, and no
+    other instruction of the kernel reads m0 (no LDS-direct, interpolation,
+    GWS, movrel or message instructions), so no compiler-held m0 value is
+    overwritten."""
     import re
     import shutil
     import subprocess
@@ -282,10 +285,10 @@ def test_swiglu_m0_only_feeds_lds_dma(tmp_path):
 
     if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
         pytest.skip("hipcc not available")
-    out = tmp_path / "swiglu.s"
+    out = tmp_path / "gemm.s"
     flags = [f for f in _build.HIPCC_FLAGS if f != "-fPIC"]
     cmd = [_build.hipcc(), *flags, f"-I{_build.INCLUDE}", "--cuda-device-only", "-S",
-           str(_build.CSRC / "swiglu_gemm.hip"), "-o", str(out)]
+           str(_build.CSRC / source), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
     lines = [ln.split(";")[0].strip() for ln in out.read_text().splitlines()]
