@@ -125,12 +125,13 @@ class SwiGLU(nn.Module):
         # silu_mul backward kernel and torch.cat back to w1, w2)
         w12 = _gemm_weight(self, "w12", (self.w1.weight, self.w2.weight),
                            lambda: torch.cat([self.w1.weight, self.w2.weight], dim=0))
-        return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
+        return self.forward_with(x, w12, w3)
 
     def forward_with(self, x, w12, w3):
         """The differentiable path on operands the caller built: ``w12`` =
-        [w1; w2] and ``w3`` in the GEMM dtype."""
-        return F.linear(ops.silu_mul(F.linear(x, w12)), w3)
+        [w1; w2] and ``w3`` in the GEMM dtype (bf16 weight gradients from the
+        split-K kernel, ``ops.linear``)."""
+        return ops.linear(ops.silu_mul(ops.linear(x, w12)), w3)
 
 
 def reference_ffn_hidden(d_model: int) -> int:
@@ -447,7 +448,7 @@ class MOGTBlock(_WeightCacheOwner):
             stacked = [self.phi_val.weight, cols["cur"]] + ([cols["prev"]] if "prev" in cols else [])
             W_all = _gemm_weight(self, "value_and_gate", (self.phi_val.weight, W),
                                  lambda: torch.cat(stacked, dim=0))
-        proj = F.linear(xn, W_all)
+        proj = ops.linear(xn, W_all)
         if const_given:
             return proj, "prev" in cols, const
         const = gate.bias.float() if gate.bias is not None else None
@@ -500,7 +501,7 @@ class MOGTBlock(_WeightCacheOwner):
             hn = ops.rmsnorm(h, self.norm_out.weight, self.norm_out.eps, out_dtype=gemm_dtype)
             Wr = packed["theta"] if packed is not None else _gemm_weight(self, "theta_read", (self.theta_read.weight,),
                                                                            lambda: self.theta_read.weight)
-            Z = F.linear(hn, Wr)
+            Z = ops.linear(hn, Wr)
         return ops.add_rmsnorm(x, Z, self._residual_scale(Z), self.norm_ffn.weight, self.norm_ffn.eps,
                                out_dtype=gemm_dtype)
 

@@ -28,6 +28,7 @@ _ws_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 # graph's replays would then overwrite.  Growth is geometric, so the retired
 # buffers together are smaller than the live one.
 _ws_retired: list[torch.Tensor] = []
+_ws_retired_lookback: list[torch.Tensor] = []   # the look-back family ones among them
 # layout of the launches on each look-back workspace, and whether a captured
 # graph uses the buffer (pinned to that layout)
 _ws_layout: dict[tuple[int, int, str], tuple] = {}
@@ -97,8 +98,13 @@ def workspace(nbytes: int, device: torch.device, family: str = "plain", layout: 
                 else:
                     size = max(size, 2 * buf.numel())
                 _ws_retired.append(buf)
-            # a new buffer starts from epoch 0 with every word zero
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                if lookback:
+                    _ws_retired_lookback.append(buf)
+            # a new buffer starts from epoch 0 with every word zero; it is a
+            # normal tensor even when made under inference mode, so that later
+            # calls outside that mode may still clear it in place
+            with torch.inference_mode(False):
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
             state = None
         if lookback:
@@ -119,11 +125,12 @@ def _faults_of(buf: torch.Tensor) -> int:
 
 def workspace_faults() -> int:
     """Number of bounded look-back waits that gave up, summed over every cached
-    workspace (read through ``mogt_workspace_faults``).  Always 0 unless the
-    protocol was violated, in which case the affected outputs also hold NaN.
-    Synchronises the streams involved."""
+    look-back workspace, live or retired (read through
+    ``mogt_workspace_faults``; plain buffers have no header, their first bytes
+    are data).  Always 0 unless the protocol was violated, in which case the
+    affected outputs also hold NaN.  Synchronises the streams involved."""
     with _ws_lock:
-        bufs = list(_ws_cache.values()) + list(_ws_retired)
+        bufs = [b for k, b in _ws_cache.items() if k[2] in LOOKBACK_FAMILIES] + list(_ws_retired_lookback)
     return sum(_faults_of(b) for b in bufs)
 
 

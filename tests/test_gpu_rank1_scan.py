@@ -215,6 +215,7 @@ def test_checked_mode_falls_back_to_three_launches(gpu, monkeypatch):
     for name in ("_ws_cache", "_ws_layout", "_ws_faults_seen"):
         monkeypatch.setattr(ops, name, {})
     monkeypatch.setattr(ops, "_ws_retired", [])
+    monkeypatch.setattr(ops, "_ws_retired_lookback", [])
     f, k, v, q = synthetic.rank1_inputs(1, 900, 2, 64, seed=78)
     ft, kt, vt, qt = (torch.from_numpy(x).to(gpu).bfloat16() for x in (f, k, v, q))
     ref = so.rank1_coupled_scan(*(to_np(x) for x in (ft, kt, vt, qt)))

@@ -195,6 +195,7 @@ def _fake_device_workspace(monkeypatch):
     monkeypatch.setattr(ops, "_ws_cache", {})
     monkeypatch.setattr(ops, "_ws_layout", {})
     monkeypatch.setattr(ops, "_ws_retired", [])
+    monkeypatch.setattr(ops, "_ws_retired_lookback", [])
     return ops, torch.device("cpu", 0)
 
 
@@ -245,6 +246,41 @@ def test_captured_workspace_is_pinned_to_its_layout(monkeypatch):
     assert ops.workspace(4096, dev, "coupled", ("D",)) is b and int(b[256:4096].max()) == 0
     capturing[0] = False
     assert ops.workspace(4096, dev, "coupled", ("E",)) is not b
+
+
+def test_workspace_made_under_inference_mode_is_cleared_outside_it(monkeypatch):
+    """A buffer first made inside torch.inference_mode() (an inference-mode
+    forward) is still cleared in place when a later launch of another layout
+    runs outside that mode (a no-grad or training call)."""
+    ops, dev = _fake_device_workspace(monkeypatch)
+    with torch.inference_mode():
+        a = ops.workspace(4096, dev, "coupled", ("A",))
+        a[256:] = 7
+    assert not a.is_inference()
+    with torch.no_grad():
+        assert ops.workspace(4096, dev, "coupled", ("B",)) is a
+    assert int(a[256:4096].max()) == 0
+    with torch.inference_mode():
+        a[256:] = 7
+        assert ops.workspace(4096, dev, "coupled", ("C",)) is a and int(a[256:4096].max()) == 0
+
+
+def test_fault_count_reads_only_lookback_headers(monkeypatch):
+    """Only look-back buffers carry the give-up counter in their header; a
+    plain buffer's first bytes are data (e.g. the weight-gradient GEMM's fp32
+    partials) and are never read as a count, live or retired."""
+    ops, dev = _fake_device_workspace(monkeypatch)
+    read = []
+    monkeypatch.setattr(ops, "_faults_of", lambda buf: read.append(buf) or 0)
+    plain = ops.workspace(4096, dev)
+    plain[:] = 255
+    diag = ops.workspace(4096, dev, "diag", (1,))
+    assert ops.workspace_faults() == 0 and len(read) == 1 and read[0] is diag
+    ops.workspace(1 << 20, dev)                      # plain grows: old one retired
+    ops.workspace(1 << 20, dev, "diag", (1,))        # diag grows: old one retired
+    read.clear()
+    ops.workspace_faults()
+    assert len(read) == 2 and any(b is diag for b in read) and not any(b is plain for b in read)
 
 
 def test_checked_mode_reports_each_give_up_once(monkeypatch):
