@@ -48,14 +48,15 @@ def parse_args():
     p.add_argument("--only", default="all",
                    help="after the headline: every extra (all), none (diag), or a comma list of "
                         "coupled (the mixer scan), rank1 (configs[2]), dense (core shape and configs[3]), "
-                        "swiglu, backbone (configs[4] forward and training step)")
+                        "swiglu, wgrad (the training path's weight-gradient GEMMs), backbone (configs[4] "
+                        "forward and training step)")
     p.add_argument("--tile", default=None,
                    help="vec,lanes,steps,waves override for the headline diag scan")
     p.add_argument("--sweep", action="store_true", help="time every compiled diag tile")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (PMC calibration)")
     args = p.parse_args()
-    groups = {"diag", "coupled", "rank1", "dense", "swiglu", "backbone", "all"}
+    groups = {"diag", "coupled", "rank1", "dense", "swiglu", "wgrad", "backbone", "all"}
     args.only = set(args.only.split(","))
     if not args.only <= groups:
         p.error(f"--only takes a comma list of {sorted(groups)}")
@@ -305,6 +306,41 @@ def measure_swiglu(torch, steps, warmup, rows=32768, d_in=768, hidden=3072):
     ms_fused, ms_unfused, ms_gemm = best["fused"], best["unfused"], best["gemm"]
     flop = 2.0 * rows * d_in * 2 * hidden
     return {"ms": ms_fused, "ms_unfused": ms_unfused, "ms_gemm_only": ms_gemm, "tflops": flop / ms_fused / 1e9}
+
+
+WGRAD_SHAPES = ((768, 768, "theta_read"), (800, 768, "phi_val + value gate"), (768, 3072, "w3"),
+                (6144, 768, "w1; w2"))
+
+
+def measure_wgrad(torch, steps, warmup, tokens=32768):
+    """Weight gradients of the training path's linear layers (model_mogt.py:
+    25-27, 57, 61) at configs[4]'s T = B * L: the split-K HIP GEMM
+    (csrc/wgrad_gemm.hip, both of its launches) against the library GEMM that
+    autograd calls for F.linear's weight (dY^T X), bf16 in, bf16 out.  With
+    the tuned GEMM table when the caller activated it."""
+    from mogt_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(43)
+    stream = torch.cuda.current_stream(dev)
+    timer = EventTimer(torch, stream)
+    out = {}
+    for d_out, d_in, what in WGRAD_SHAPES:
+        dy = torch.randn(tokens, d_out, generator=gen, device=dev).bfloat16()
+        x = torch.randn(tokens, d_in, generator=gen, device=dev).bfloat16()
+        runs = {"hip": lambda i: ops.linear_wgrad(dy, x), "library": lambda i: dy.t().mm(x)}
+        best = {k: float("inf") for k in runs}
+        for _ in range(3):
+            for k, f in runs.items():
+                best[k] = min(best[k], timer.time(f, steps, warmup))
+        flop = 2.0 * tokens * d_out * d_in
+        splits = int(ops._lib.load().mogt_linear_wgrad_splits(tokens, d_out, d_in, 0, 0))
+        out[f"{d_out}x{d_in}"] = {
+            "layer": what, "us": round(best["hip"] * 1e3, 2), "library_us": round(best["library"] * 1e3, 2),
+            "TFLOP/s": round(flop / best["hip"] / 1e9, 1), "splits": splits,
+            "frac_bf16_mfma_peak": round(flop / best["hip"] / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del dy, x
+    return out
 
 
 def measure_lm_ce(torch, lib, steps, warmup, rows=4096, vocab=32000, L=32768, D=768, chunk=4096):
@@ -939,6 +975,18 @@ def main():
                 "unfused_us": round(r["ms_unfused"] * 1e3, 2), "library_gemm_only_us": round(r["ms_gemm_only"] * 1e3, 2),
                 "note": "FFN gate silu(x w1^T) * (x w2^T) as one GEMM with the gate in its epilogue vs the "
                         "library GEMM against [w1; w2] + the silu_mul row kernel (model_mogt.py:29-30)"}
+        if full or "wgrad" in only:
+            from mogt_amd import gemm_tuning
+
+            log("extras: weight-gradient GEMMs")
+            tuned = gemm_tuning.use_tuned_gemms()
+            extras["linear_wgrad_T32768_bf16"] = dict(
+                measure_wgrad(torch, args.steps, args.warmup), tuned_gemm_table=tuned,
+                note="dW = dY^T X of the training path's linear layers at T = 32768 tokens: the split-K HIP "
+                     "GEMM (fp32 partials per token slice, summed in slice order, rounded once) vs the "
+                     "library GEMM autograd calls (tuned table)")
+            if tuned:
+                gemm_tuning.default_gemms()
         if full or "backbone" in only:
             from mogt_amd import gemm_tuning
 
@@ -981,8 +1029,9 @@ def main():
                 rf, default_gemms_ms=dt["ms"], tuned_gemm_table=tuned,
                 generic_path_ms=rg["ms"], generic_path_peak_mem_mb=rg["peak_mem_mb"],
                 note="forward + backward (mean-square loss on the backbone output, no optimizer), "
-                     "bf16 autocast; fused block path (default_gemms_ms: the libraries' own GEMM choice) "
-                     "vs the generic op-by-op path on the same weights")
+                     "bf16 autocast; fused block path, whose linear layers take their weight gradients from "
+                     "the split-K HIP GEMM (default_gemms_ms: the libraries' own choice for the other "
+                     "GEMMs) vs the generic op-by-op path on the same weights")
             if tuned:
                 gemm_tuning.default_gemms()
         log(f"extras: {json.dumps(extras)}")

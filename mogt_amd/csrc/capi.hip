@@ -1,5 +1,6 @@
 // C ABI plumbing shared by all scan entry points: per-thread error text,
 // launch checking and the ABI version.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -24,6 +25,24 @@ void clear_error() { g_last_error[0] = '\0'; }
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(MOGT_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return MOGT_OK;
+}
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::atomic<int> g_cus[MAX_DEVICES];   // 0: not queried yet
+}
+
+int device_cu_count(int& cus) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(MOGT_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev >= 0 && dev < MAX_DEVICES && (cus = g_cus[dev].load(std::memory_order_relaxed)) > 0) return MOGT_OK;
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return set_error(MOGT_E_LAUNCH, "CU count query: %s", hipGetErrorString(e));
+    cus = n > 0 ? n : 1;
+    if (dev >= 0 && dev < MAX_DEVICES) g_cus[dev].store(cus, std::memory_order_relaxed);
     return MOGT_OK;
 }
 

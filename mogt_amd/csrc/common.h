@@ -20,6 +20,9 @@ namespace mogt {
 int set_error(int code, const char* fmt, ...);
 void clear_error();
 int check_launch(const char* what);
+// compute units of the current device (queried once per device); MOGT_OK or
+// MOGT_E_LAUNCH with the HIP error
+int device_cu_count(int& cus);
 
 // ---------------------------------------------------------------------------
 // bf16 <-> f32.  Storage is the raw 16-bit pattern.  f32 -> bf16 rounds to

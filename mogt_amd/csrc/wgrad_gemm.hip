@@ -345,12 +345,10 @@ WgradPlan wgrad_plan(int64_t tokens, int64_t d_out, int64_t d_in, int64_t splits
 }
 
 int device_cus(int64_t& cus) {
-    int dev = 0, n = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return set_error(MOGT_E_LAUNCH, "linear_wgrad: device query: %s", hipGetErrorString(e));
-    cus = n > 0 ? n : 1;
-    return MOGT_OK;
+    int n = 0;
+    const int rc = device_cu_count(n);
+    cus = n;
+    return rc;
 }
 
 }  // namespace
