@@ -32,6 +32,7 @@ import csv
 import shlex
 import sys
 import json
+import re
 import statistics
 from collections import defaultdict
 from pathlib import Path
@@ -52,6 +53,8 @@ def _csv(dirpath: str | None, suffix: str) -> list[dict]:
 
 def short_name(name: str) -> str:
     """Kernel name without the parameter list (template arguments kept)."""
+    # the parenthesis of an anonymous namespace is not a parameter list
+    name = name.replace("(anonymous namespace)::", "")
     depth = 0
     for i, ch in enumerate(name):
         if ch == "<":
@@ -65,6 +68,15 @@ def short_name(name: str) -> str:
         if name.startswith(prefix):
             name = name[len(prefix):]
     return name.replace("mogt::", "").replace("(anonymous namespace)::", "").strip()
+
+
+def display_name(name: str) -> str:
+    """Table label: library GEMM kernels (Tensile names, hundreds of
+    characters) by their macro tile, everything else as is."""
+    if name.startswith(("Cijk_", "Custom_Cijk_")):
+        m = re.search(r"_MT(\d+x\d+x\d+)_", name)
+        return f"library GEMM MT{m.group(1)}" if m else "library GEMM"
+    return name
 
 
 def trace_table(rows: list[dict]) -> dict:
@@ -167,7 +179,7 @@ def summarize(args) -> str:
     for k in mine:
         e = trace[k]
         d = e["us"]
-        row = (f"| `{k[0]}` | {k[1]} | {k[2]} | {e['vgpr']} | {e['agpr']} | {e['lds']} | {e['scratch']} | "
+        row = (f"| `{display_name(k[0])}` | {k[1]} | {k[2]} | {e['vgpr']} | {e['agpr']} | {e['lds']} | {e['scratch']} | "
                f"{len(d)} | {statistics.mean(d):.2f} | {statistics.median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
         if fscale and wscale:
             rd = fetch.get(k)

@@ -155,6 +155,13 @@ def test_rocprof_summary_groups_and_calibrates(tmp_path):
 
     assert rs.short_name("void mogt::diag_scan_kernel<0, float, 2>(float const*, int)") == \
         "diag_scan_kernel<0, float, 2>"
+    assert rs.display_name("Cijk_Ailk_Bjlk_BBS_BH_UserArgs_MT192x192x64_MI16x16x1_SN") == "library GEMM MT192x192x64"
+    assert rs.display_name("diag_scan_kernel<0, float, 2>") == "diag_scan_kernel<0, float, 2>"
+    # kernels in an anonymous namespace: its parenthesis is not the parameter list
+    assert rs.short_name("mogt::(anonymous namespace)::wgrad_gemm_kernel(mogt::(anonymous namespace)::"
+                         "WgradParams)") == "wgrad_gemm_kernel"
+    assert rs.short_name("void mogt::(anonymous namespace)::wgrad_reduce_kernel<false>(float const*, void*, "
+                         "long, int, int, int)") == "wgrad_reduce_kernel<false>"
     rows = []
     for i in range(5):      # calibration: 256 MiB copied, counter reads half of it
         rows.append(dict(Counter_Name="FETCH_SIZE", Counter_Value="131072", Dispatch_Id=str(i + 1),
