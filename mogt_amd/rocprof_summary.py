@@ -175,7 +175,10 @@ def summarize(args) -> str:
         sep += "---|---|"
     lines += [hdr, sep]
     keys = sorted(trace, key=lambda k: -sum(trace[k]["us"]))
-    mine = [k for k in keys if any(m in k[0] for m in args.match)]
+    mine = [k for k in keys if not args.match or any(m in k[0] for m in args.match)]
+    rest = mine[args.top:] if args.top else []
+    if args.top:
+        mine = mine[:args.top]
     for k in mine:
         e = trace[k]
         d = e["us"]
@@ -192,6 +195,14 @@ def summarize(args) -> str:
             row += f" {c['SQ_INSTS_MFMA']:.0f} |" if "SQ_INSTS_MFMA" in c else " - |"
             row += f" {fr:.1%} |" if fr is not None else " - |"
         lines.append(row)
+    if rest:
+        lines.append(f"| {len(rest)} more kernels / launch shapes | | | | | | | "
+                     f"{sum(len(trace[k]['us']) for k in rest)} | | | | |"
+                     + (" | |" if fscale and wscale else "") + (" | |" if mfma else ""))
+        lines.append("")
+        lines.append(f"(The table lists the {args.top} kernels / launch shapes with the most total time; the "
+                     f"other {len(rest)} add {sum(sum(trace[k]['us']) for k in rest) / 1e3:.1f} ms of the "
+                     f"{sum(sum(v['us']) for v in trace.values()) / 1e3:.1f} ms traced.)")
     lines.append("")
 
     if args.kernel:
@@ -246,6 +257,7 @@ def main(argv=None) -> None:
     p.add_argument("--match", action="append", default=[],
                    help="substrings of the kernel names listed in the table (default: every kernel)")
     p.add_argument("--kernel", help="full short name of the kernel the key=value block describes")
+    p.add_argument("--top", type=int, default=0, help="list only this many kernels (most total time first)")
     p.add_argument("--algorithmic-bytes", type=int, default=0)
     p.add_argument("--sources", default="")
     p.add_argument("--bench-log")
