@@ -146,10 +146,12 @@ def measure_diag(torch, lib, ops, L, dtype, out_dtype, steps, warmup, tile=None,
     return {"ms": ms, "bytes": total, "gbs": total / (ms * 1e-3) / 1e9}
 
 
-def measure_diag_op(torch, L, steps, warmup, graph, D=768, B=1, sets=3):
+def measure_diag_op(torch, L, steps, warmup, graph, D=768, B=1, sets=3, per_graph=1):
     """Op-level time of ``mogt_amd.diag_scan`` (fp32): per call through the
     Python boundary (custom-op dispatch, output allocation, C-ABI launch), or
-    the same call captured once per input set in a HIP graph and replayed."""
+    the same call captured in a HIP graph and replayed: ``per_graph`` calls
+    (cycling through the input sets) per graph, one graph per input set, time
+    per call."""
     import mogt_amd
 
     dev = torch.device("cuda:0")
@@ -170,13 +172,14 @@ def measure_diag_op(torch, L, steps, warmup, graph, D=768, B=1, sets=3):
             cur.wait_stream(s)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph(keep_graph=True)
+            k0 = len(graphs)
             with torch.cuda.graph(g, stream=s):
-                out = mogt_amd.diag_scan(a, b)
+                out = [mogt_amd.diag_scan(*bufs[(k0 + n) % sets]) for n in range(per_graph)]
             g.instantiate()
             graphs.append((g, out))
         torch.cuda.synchronize()
         fn = lambda i: graphs[i % sets][0].replay()
-    ms = EventTimer(torch, cur).time(fn, steps, warmup)
+    ms = EventTimer(torch, cur).time(fn, steps, warmup) / (per_graph if graph else 1)
     return {"ms": ms, "graph_nodes": [graph_nodes(g) for g, _ in graphs] if graph else None}
 
 
@@ -874,12 +877,16 @@ def main():
             for L in (8192, 32768):
                 re_ = measure_diag_op(torch, L, args.steps, args.warmup, graph=False)
                 rg_ = measure_diag_op(torch, L, args.steps, args.warmup, graph=True)
+                rg16 = measure_diag_op(torch, L, args.steps, args.warmup, graph=True, per_graph=16)
                 extras[f"diag_fp32_L{L}_op_level"] = {
                     "eager_us": round(re_["ms"] * 1e3, 2), "graph_us": round(rg_["ms"] * 1e3, 2),
-                    "graph_nodes": rg_["graph_nodes"],
+                    "graph_nodes": rg_["graph_nodes"], "graph16_us": round(rg16["ms"] * 1e3, 2),
+                    "graph16_nodes": rg16["graph_nodes"],
                     "note": "mogt_amd.diag_scan per call (eager: input checks, output allocation, C-ABI launch; "
-                            "the custom-op dispatch is taken only under autograd or tracing), and the same call "
-                            "captured in a HIP graph and replayed (graph_nodes: nodes per captured graph)"}
+                            "the custom-op dispatch is taken only under autograd or tracing), the same call "
+                            "captured alone in a HIP graph and replayed (graph_nodes: nodes per captured graph; "
+                            "the replay pays the runtime's graph launch), and 16 calls captured in one graph "
+                            "(graph16_us: replay time per call)"}
             r = measure_diag_rev(torch, lib, ops, 32768, args.steps, args.warmup)
             extras["diag_rev_fp32_L32768"] = {
                 "us": round(r["ms"] * 1e3, 2), "GB/s": round(r["gbs"], 1),

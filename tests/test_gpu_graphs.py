@@ -167,3 +167,66 @@ def test_generic_scan_graph_replays(gpu):
         P_ref, H_ref = so.affine_scan_sequential(Un, Vn, return_prefix=True)
         assert rel_err(H_rep.cpu().numpy(), H_ref) <= 1e-12
         assert rel_err(P_rep.cpu().numpy(), P_ref) <= 1e-12
+
+
+def test_diag_scan_graph_of_chained_calls(gpu):
+    """Three dependent scans captured in one graph (each later scan reads the
+    previous output), so consecutive launches inside one replay share the
+    look-back workspace; every replay matches the same chain run eagerly."""
+    import mogt_amd
+
+    B, L, D = 1, 8192, 768
+    a0, b0 = synthetic.diag_inputs(B, L, D, seed=80)
+    a = torch.from_numpy(a0).to(gpu)
+    b = torch.from_numpy(b0).to(gpu)
+    a2 = torch.flip(a, dims=[1]).contiguous()
+
+    def chain():
+        h1 = mogt_amd.ops.diag_scan(a, b)
+        h2 = mogt_amd.ops.diag_scan(a2, h1)
+        return mogt_amd.ops.diag_scan(a, h2)
+
+    announce(f"graph diag chain B={B} L={L} D={D}: capture")
+    g, out = _capture(chain)
+    for i in range(REPLAYS):
+        an, bn = synthetic.diag_inputs(B, L, D, seed=81 + i)
+        a.copy_(torch.from_numpy(an))
+        b.copy_(torch.from_numpy(bn))
+        a2.copy_(torch.flip(a, dims=[1]))
+        announce(f"graph diag chain replay {i}")
+        g.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = chain()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager)
+        ref = so.diag_scan(an, so.diag_scan(np.ascontiguousarray(an[:, ::-1]), so.diag_scan(an, bn)))
+        assert rel_err(to_np(replayed), ref) <= 1e-4
+    assert mogt_amd.ops.workspace_faults() == 0
+
+
+def test_linear_wgrad_graph_replays(gpu):
+    """The split-K weight-gradient GEMM (its partial-sum workspace and both
+    launches) under capture: replays match eager launches bit for bit."""
+    from mogt_amd import ops
+
+    T, O, I = 8192, 768, 800
+    gen = torch.Generator(device="cpu").manual_seed(90)
+    mk = lambda: (torch.randn(T, O, generator=gen).bfloat16(), torch.randn(T, I, generator=gen).bfloat16())
+    dy0, x0 = mk()
+    dy, x = dy0.to(gpu), x0.to(gpu)
+    announce(f"graph linear_wgrad T={T} O={O} I={I}: capture")
+    g, out = _capture(lambda: ops.linear_wgrad(dy, x))
+    for i in range(REPLAYS):
+        dyn, xn = mk()
+        dy.copy_(dyn)
+        x.copy_(xn)
+        announce(f"graph linear_wgrad replay {i}")
+        g.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = ops.linear_wgrad(dy, x)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager)
+        ref = dy.double().t() @ x.double()
+        assert rel_err(to_np(replayed), to_np(ref)) <= 2e-2
