@@ -334,17 +334,18 @@ int mogt_affine_local_scan(const void* U, const void* V, void* U_prefix, void* H
  * V_t = (1 - f_t) v_t k_t^T, read out through q_t, without materialising S_t.
  * f: [B, L, H]; k, v, q, y: [B, L, H, head_dim]; head_dim = 64.  Products run
  * on bf16 MFMA with fp32 accumulation and fp32 carried state (inputs are
- * rounded to bf16).  With bf16 k, v, q and sequences of at most 64
- * super-chunks of 256 steps (L <= 16384) it runs as one launch whose
- * work-groups exchange the carried states through the workspace; otherwise
- * as three launches (chunk states, carries, outputs).  The workspace query
- * covers both.
+ * rounded to bf16).  With bf16 k, v, q, sequences of at most 64
+ * super-chunks of 256 steps (L <= 16384) and at most three work-groups per
+ * compute unit (B * H * ceil(L / 256) <= 3 * CUs, i.e. all resident at once)
+ * it runs as one launch whose work-groups exchange the carried states
+ * through the workspace; otherwise as three launches (chunk states, carries,
+ * outputs).  The workspace query covers both.
  * The one-launch form needs every super-chunk of a sequence resident at
  * once (in-order dispatch guarantees it on an otherwise idle GPU); if a
  * kernel on another stream holds the compute units its bounded waits give
  * up, the affected outputs are NaN and mogt_workspace_faults counts them.
  * mogt_rank1_coupled_scan_fwd_cfg: the same with the path forced (0 = by
- *   length as above, 1 = one launch, 2 = three launches, 3 = a test of the
+ *   shape as above, 1 = one launch, 2 = three launches, 3 = a test of the
  *   give-up handling: the one-launch kernel with super-chunk 0 withholding
  *   its aggregate, and each work-group's wait on it giving up after 64 polls,
  *   so every super-chunk after the first comes back NaN and the count grows by

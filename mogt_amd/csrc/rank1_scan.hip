@@ -547,6 +547,7 @@ __global__ __launch_bounds__(R1_THREADS) void rank1_output_kernel(Rank1Params p)
 // most R1S_MAX_SC of them.
 // ---------------------------------------------------------------------------
 constexpr int R1S_MAX_SC = 64;
+constexpr int R1S_GROUPS_PER_CU = 3;   // resident one-launch work-groups per CU (registers and LDS)
 constexpr int R1S_NB = 16;            // aggregates loaded per batch of the slice scan
 constexpr int R1_SC1 = 16;            // buffer cache policy: agent-coherent (sc1)
 
@@ -586,8 +587,8 @@ __device__ __forceinline__ u32x2 ds_tr(bf16_t* p) {
 // 8-bf16 MFMA operand whose contraction runs over the rows of a natural tile:
 // lane l gets column cb + l % 32 and rows 16 kk + 4 (l / 32) + 0..3 (slots
 // 0-3) and the same + 8 (slots 4-7).
-__device__ __forceinline__ bf16x8 tr_op(bf16_t* tile, int kk, int cb) {
-    const int l = threadIdx.x & 63, i = l & 15;
+__device__ __forceinline__ bf16x8 tr_op(bf16_t* tile, int kk, int cb, int l = threadIdx.x & 63) {
+    const int i = l & 15;
     const int col = cb + 16 * ((l >> 4) & 1) + 4 * (i & 3);
     const int r0 = 16 * kk + 4 * (l >> 5) + (i >> 2);
     const u32x2 a = ds_tr(tile + noff(r0, col));
@@ -993,6 +994,18 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
         }
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib) {
+        // The lane index made opaque here, so the LDS addresses below are
+        // formed where they are used: otherwise the compiler keeps the same
+        // addresses of the earlier phases alive across the carry exchange,
+        // spills them and reloads them one scratch round trip at a time.
+        int ol = lane;
+        asm volatile("" : "+v"(ol));
+        // staging offset of accumulator row group q (row t = 32 tb + 8 g4 +
+        // 4 (lane / 32) + q, chunk (i / 8) ^ (t % 4)): 4 registers for all 16 rows
+        int qoff[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            qoff[q] = (4 * (ol >> 5) + q) * 32 + 8 * (((ol & 31) >> 3) ^ q) + (ol & 7);
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
             f32x16 acc = zero16();
@@ -1014,13 +1027,11 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
 #pragma unroll
                 for (int kh = 0; kh < 2; ++kh)
                     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pb[tb == 0 ? 0 : 1 + sb][kh],
-                                                                  tr_op(sV[j], 2 * sb + kh, 32 * ib), acc, 0, 0, 0);
+                                                                  tr_op(sV[j], 2 * sb + kh, 32 * ib, ol), acc, 0, 0, 0);
             if constexpr (SO == 2) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int t = 32 * tb + mrow(r), i = lane & 31;
-                    sy[t * 32 + 8 * ((i >> 3) ^ (t & 3)) + (i & 7)] = f32_to_bf16(acc[r]);
-                }
+                for (int r = 0; r < 16; ++r)
+                    sy[(32 * tb + 8 * (r >> 2)) * 32 + qoff[r & 3]] = f32_to_bf16(acc[r]);
             } else {
                 const int colB = (32 * ib + (lane & 31)) * SO;
 #pragma unroll
@@ -1032,7 +1043,7 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
         if constexpr (SO == 2) {   // this wave's [64 t][32 i] block as 16-byte row pieces
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
-                const int t = (lane >> 2) + 16 * n, ch = lane & 3;
+                const int t = (ol >> 2) + 16 * n, ch = ol & 3;
                 const u32x4 x = *reinterpret_cast<const u32x4*>(&sy[t * 32 + 8 * (ch ^ (t & 3))]);
                 __builtin_amdgcn_raw_buffer_store_b128(x, ry, t * strideO + (32 * ib + 8 * ch) * SO, 0, 2);
             }
@@ -1128,7 +1139,15 @@ extern "C" int mogt_rank1_coupled_scan_fwd_cfg(const void* f, const void* k, con
     if (length > (int64_t(1) << 40)) return set_error(MOGT_E_INVALID, "length too large");
     const R1Geo g = r1_geometry(batch, length, heads);
     const bool bf16_io = kvq_dtype == MOGT_BF16;
-    const bool single = path == 1 || path == 3 || (path == 0 && g.nsc <= R1S_MAX_SC && bf16_io);
+    // By default the one-launch form runs when all its work-groups are resident
+    // together (three per CU): every further generation of work-groups pays the
+    // whole carry exchange again, and the three launches then win (B = 2,
+    // L = 16384, H = 12: 97 vs 94 us).
+    int cus = 0;
+    const int64_t n_groups = batch * heads * g.nsc;
+    const bool one_gen = device_cu_count(cus) == MOGT_OK && n_groups <= int64_t(R1S_GROUPS_PER_CU) * cus;
+    clear_error();
+    const bool single = path == 1 || path == 3 || (path == 0 && g.nsc <= R1S_MAX_SC && bf16_io && one_gen);
     if (path == 3 && g.nsc < 2)
         return set_error(MOGT_E_INVALID, "the give-up test path needs at least 2 super-chunks (L > %d)", R1_RS);
     if (single && g.nsc > R1S_MAX_SC)

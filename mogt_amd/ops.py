@@ -1861,8 +1861,10 @@ def rank1_coupled_scan(f: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q: tor
     """``y_t = S_t q_t`` with ``S_t = f_t S_{t-1} + (1 - f_t) v_t k_t^T`` per
     (batch, head); f ``[B, L, H]``, k/v/q ``[B, L, H, 64]``.  Products on bf16
     MFMA (inputs rounded to bf16), fp32 state; ``out_dtype`` defaults to
-    ``q.dtype``.  ``path``: "auto" (one launch up to L = 16384, three beyond),
-    "single" or "three" to force one."""
+    ``q.dtype``.  ``path``: "auto" (one launch for bf16 k, v, q when
+    L <= 16384 and the B * H * ceil(L / 256) work-groups fit the GPU at three
+    per compute unit; three launches otherwise), "single" or "three" to force
+    one."""
     if path not in RANK1_PATHS:
         raise ValueError(f"path must be one of {sorted(RANK1_PATHS)}")
     require_cuda("rank1_coupled_scan", f, k, v, q)
