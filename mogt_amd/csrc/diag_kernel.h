@@ -415,39 +415,60 @@ void diag_scan_kernel(DiagParams p) {
             Ap[v] = cwA * s_inA[flane + v];
         }
         const int64_t wbase = (rbase + (REV ? -tw : tw)) * p.D + fbase;
-        TOut* ph = static_cast<TOut*>(p.h) + wbase;
-        TOut* pp = PREFIX ? static_cast<TOut*>(p.aprefix) + wbase : nullptr;
+        // The stores walk a row pointer from this lane's first step.  Its step
+        // offset comes from a value made opaque here: otherwise the compiler
+        // keeps the load phase's per-step row offsets alive until these stores,
+        // or spills them and reloads each one behind a wait for every store
+        // issued before it.
+        int qs = q * S;
+        asm volatile("" : "+v"(qs));
+        const int64_t roff = static_cast<int64_t>(qs) * Ds + flane;
+        TOut* const ph = static_cast<TOut*>(p.h) + wbase + roff;
+        TOut* const pp = PREFIX ? static_cast<TOut*>(p.aprefix) + wbase + roff : nullptr;
+        // FULL: every step of every lane of the wave is in the problem (every
+        // chunk but a chain's last when D is a multiple of the chunk width), so
+        // the stores need no per-step lane mask
+        auto emit = [&](auto full_tag) {
+            constexpr bool FULL = decltype(full_tag)::value;
+            TOut* rh = ph;
+            TOut* rp = pp;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            float o[VEC];
+            for (int s = 0; s < S; ++s) {
+                float o[VEC];
 #pragma unroll
-            for (int v = 0; v < VEC; ++v) {
-                const float av = step_a(s, v);
-                hh[v] = fmaf(av, hh[v], step_b(s, v));
-                if constexpr (PREFIX) Ap[v] *= av;
-                o[v] = hh[v];
-            }
-            if constexpr (ROWSTAT) {
-                // features past D hold h = 0 (identity steps); every lane of the
-                // row takes part, the row's first lane (always a valid feature)
-                // stores the group's sum
-                float sq = 0.0f;
-#pragma unroll
-                for (int v = 0; v < VEC; ++v) sq = fmaf(o[v], o[v], sq);
-                sq = row_lanes_sum<FWL>(sq);
-                if ((lane % FWL) == 0 && s < nv)
-                    p.rowstat[(row0 + t0 + s) * p.n_fg + fg] = sq;
-            }
-            if (s < nv) {
-                const int off = (q * S + s) * Ds + flane;
-                store_stream<TOut, VEC>(ph + off, o);
-                if constexpr (PREFIX) {
-#pragma unroll
-                    for (int v = 0; v < VEC; ++v) o[v] = Ap[v];
-                    store_stream<TOut, VEC>(pp + off, o);
+                for (int v = 0; v < VEC; ++v) {
+                    const float av = step_a(s, v);
+                    hh[v] = fmaf(av, hh[v], step_b(s, v));
+                    if constexpr (PREFIX) Ap[v] *= av;
+                    o[v] = hh[v];
                 }
+                if constexpr (ROWSTAT) {
+                    // features past D hold h = 0 (identity steps); every lane of
+                    // the row takes part, the row's first lane (always a valid
+                    // feature) stores the group's sum
+                    float sq = 0.0f;
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) sq = fmaf(o[v], o[v], sq);
+                    sq = row_lanes_sum<FWL>(sq);
+                    if ((lane % FWL) == 0 && (FULL || s < nv))
+                        p.rowstat[(row0 + t0 + s) * p.n_fg + fg] = sq;
+                }
+                if (FULL || s < nv) {
+                    store_stream<TOut, VEC>(rh, o);
+                    if constexpr (PREFIX) {
+#pragma unroll
+                        for (int v = 0; v < VEC; ++v) o[v] = Ap[v];
+                        store_stream<TOut, VEC>(rp, o);
+                    }
+                }
+                rh += Ds;
+                if constexpr (PREFIX) rp += Ds;
             }
-        }
+        };
+        if (__all(nv == S))
+            emit(std::true_type{});
+        else
+            emit(std::false_type{});
     }
 
     // ---- last work-group: advance the epoch once every chunk has read it --
