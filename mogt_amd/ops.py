@@ -1806,19 +1806,27 @@ RANK1_PATHS = {"auto": 0, "single": 1, "three": 2}
 _RANK1_GIVEUP_TEST = 3
 R1_SUPER = 256        # steps per super-chunk
 R1_SINGLE_MAX = 64    # super-chunks per sequence the one-launch kernel takes
+R1_GROUPS_PER_CU = 3  # one-launch work-groups resident per compute unit
 
 
-def _rank1_single(path: int, L: int, kvq: torch.dtype) -> bool:
-    """Whether the C entry point runs the one-launch kernel for this call."""
+def _rank1_single(path: int, B: int, L: int, H: int, kvq: torch.dtype, device: torch.device) -> bool:
+    """Whether the C entry point runs the one-launch kernel for this call (the
+    rule of mogt_rank1_coupled_scan_fwd_cfg: bf16 k, v, q, at most
+    R1_SINGLE_MAX super-chunks per sequence, and every work-group resident at
+    once, R1_GROUPS_PER_CU per compute unit)."""
     if path in (1, _RANK1_GIVEUP_TEST):
         return True
-    return path == 0 and kvq == torch.bfloat16 and -(-L // R1_SUPER) <= R1_SINGLE_MAX
+    nsc = -(-L // R1_SUPER)
+    if path != 0 or kvq != torch.bfloat16 or nsc > R1_SINGLE_MAX:
+        return False
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    return B * H * nsc <= R1_GROUPS_PER_CU * cus
 
 
 def _rank1_launch(f, k, v, q, y, path: int) -> torch.Tensor:
     lib = _lib.load()
     B, L, H, d = k.shape
-    single = _rank1_single(path, L, k.dtype)
+    single = _rank1_single(path, B, L, H, k.dtype, k.device)
     nbytes = lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, H, d)
     ws = workspace(nbytes, k.device, "rank1", (B, L, H)) if single else workspace(nbytes, k.device)
     rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),

@@ -90,6 +90,39 @@ def test_length_switch(gpu):
     assert mogt_amd.ops.workspace_faults() == 0
 
 
+def test_auto_path_follows_residency(gpu):
+    """path 0 ("auto") takes the one-launch kernel only when all of its
+    B * H * ceil(L / 256) work-groups are resident together, three per compute
+    unit.  The one-launch kernel advances the workspace epoch (header word 2);
+    the three launches leave the header alone.  The op's own mirror of the
+    rule (which picks the workspace family) must agree with the C entry
+    point."""
+    announce("rank1 auto path by residency")
+    from mogt_amd import _lib, ops
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    L, H = 16384, 12                                            # 64 super-chunks per sequence
+    b_big = (ops.R1_GROUPS_PER_CU * cus) // (H * 64) + 1       # one generation does not hold them
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for B, heads, expect_single in ((1, 1, True), (b_big, H, False)):
+        g = torch.Generator(device=gpu).manual_seed(B)
+        f = torch.sigmoid(2 + torch.randn(B, L, heads, generator=g, device=gpu)).bfloat16()
+        k, v, q = (torch.randn(B, L, heads, 64, generator=g, device=gpu).bfloat16() for _ in range(3))
+        y = torch.empty_like(q)
+        nbytes = lib.mogt_rank1_coupled_scan_workspace_bytes(B, L, heads, 64)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        rc = lib.mogt_rank1_coupled_scan_fwd_cfg(f.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr(),
+                                                 y.data_ptr(), B, L, heads, 64, 1, 1, 1, ws.data_ptr(),
+                                                 ws.numel(), 0, stream)
+        _lib.check(rc, "mogt_rank1_coupled_scan_fwd_cfg")
+        torch.cuda.synchronize()
+        epoch = int(ws[8:12].view(torch.int32).item())
+        assert (epoch == 1) == expect_single, (B, heads, epoch)
+        assert ops._rank1_single(0, B, L, heads, torch.bfloat16, gpu) == expect_single
+        assert bool(torch.isfinite(y.float()).all())
+
+
 def test_equals_dense_scan_with_scalar_transport(gpu):
     """Same recurrence through the dense pipeline with R = 1: U = f, V = (1-f) vec(v k^T)
     (C = 64*64), then y = S q."""
