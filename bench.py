@@ -298,8 +298,18 @@ def measure_swiglu(torch, steps, warmup, rows=32768, d_in=768, hidden=3072):
     w12 = torch.cat([wg, wu], 0)
     stream = torch.cuda.current_stream(dev)
     timer = EventTimer(torch, stream)
+    from mogt_amd import _lib
+
+    lib = _lib.load()
+    y1 = torch.empty(rows, hidden, device=dev, dtype=torch.bfloat16)
+
+    def one_tile(i):   # the same GEMM with one tile per work-group (schedule 1)
+        _lib.check(lib.mogt_swiglu_gate_fwd_cfg(x.data_ptr(), wg.data_ptr(), wu.data_ptr(), y1.data_ptr(), rows, d_in,
+                                                hidden, d_in, hidden, _lib.MOGT_BF16, 1, stream.cuda_stream),
+                   "mogt_swiglu_gate_fwd_cfg")
+
     runs = {"fused": lambda i: ops.swiglu_gate(x, wg, wu), "unfused": lambda i: ops.silu_mul(F.linear(x, w12)),
-            "gemm": lambda i: F.linear(x, w12)}
+            "gemm": lambda i: F.linear(x, w12), "one_tile": one_tile}
     # the three are timed in turn, three rounds, best of each: the first
     # kernels of a process otherwise run before the clocks have settled
     best = {k: float("inf") for k in runs}
@@ -308,7 +318,8 @@ def measure_swiglu(torch, steps, warmup, rows=32768, d_in=768, hidden=3072):
             best[k] = min(best[k], timer.time(f, steps, warmup))
     ms_fused, ms_unfused, ms_gemm = best["fused"], best["unfused"], best["gemm"]
     flop = 2.0 * rows * d_in * 2 * hidden
-    return {"ms": ms_fused, "ms_unfused": ms_unfused, "ms_gemm_only": ms_gemm, "tflops": flop / ms_fused / 1e9}
+    return {"ms": ms_fused, "ms_unfused": ms_unfused, "ms_gemm_only": ms_gemm, "ms_one_tile": best["one_tile"],
+            "tflops": flop / ms_fused / 1e9}
 
 
 WGRAD_SHAPES = ((768, 768, "theta_read"), (800, 768, "phi_val + value gate"), (768, 3072, "w3"),
@@ -980,7 +991,9 @@ def main():
                 "us": round(r["ms"] * 1e3, 2), "TFLOP/s": round(r["tflops"], 1),
                 "frac_bf16_mfma_peak": round(r["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
                 "unfused_us": round(r["ms_unfused"] * 1e3, 2), "library_gemm_only_us": round(r["ms_gemm_only"] * 1e3, 2),
-                "note": "FFN gate silu(x w1^T) * (x w2^T) as one GEMM with the gate in its epilogue vs the "
+                "one_tile_per_workgroup_us": round(r["ms_one_tile"] * 1e3, 2),
+                "note": "FFN gate silu(x w1^T) * (x w2^T) as one GEMM with the gate in its epilogue (persistent "
+                        "schedule; one_tile_per_workgroup = the same tiles one per work-group) vs the "
                         "library GEMM against [w1; w2] + the silu_mul row kernel (model_mogt.py:29-30)"}
         if full or "wgrad" in only:
             from mogt_amd import gemm_tuning

@@ -400,6 +400,14 @@ int mogt_silu_mul_fwd(const void* y, void* out, int64_t rows, int64_t hidden, in
  *   ldy % 4 == 0; x and weights 16-byte aligned, y 8-byte aligned.           */
 int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
                          int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, void* stream);
+/* mogt_swiglu_gate_fwd_cfg: the same (model_mogt.py:29-30) with the schedule
+ *   forced: 0 = by shape (as mogt_swiglu_gate_fwd: persistent when d_in % 128
+ *   == 0 and d_in >= 640, else one tile per work-group), 1 = one tile per
+ *   work-group, 2 = persistent (MOGT_E_INVALID when d_in does not allow it).
+ *   Outputs are bit-identical across schedules; for tests and the bench.      */
+int mogt_swiglu_gate_fwd_cfg(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
+                             int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, int path,
+                             void* stream);
 /* mogt_linear_wgrad: dW = dY^T X, the weight gradient of a bias-free
  *   nn.Linear (model_mogt.py:25-27 w1, w2, w3, :57 phi_val, :61 theta_read;
  *   the grad_weight torch's linear backward forms), as a split-K GEMM on the

@@ -35,6 +35,12 @@
 // over the 8 XCDs, so block b is renumbered to give each XCD a contiguous run
 // of tiles, walked 8 row blocks at a time, so that one XCD's L2 keeps the x
 // rows of those 8 blocks while it sweeps the weight blocks.
+//
+// Two schedules of the same tiles: one tile per work-group
+// (swiglu_gemm_kernel), and a persistent one (swiglu_gemm_persistent_kernel,
+// the default where K allows it) in which each CU's work-group streams its
+// tiles' stages back to back and runs a tile's epilogue inside the next tile's
+// main loop.  Both give bit-identical outputs.
 #include <type_traits>
 
 #include "lds_dma.h"
@@ -292,15 +298,304 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p)
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Persistent schedule (default when K % 128 == 0 and K >= 640, i.e. a multiple
+// of four stages and at least 20 of them): one work-group per CU walks its
+// XCD's tiles in turn as one continuous stream of stages, so a tile's last
+// three stages load the next tile's first three (no prologue wait, no pipeline
+// drain), and tile k's epilogue runs inside tile k + 1's main loop:
+//   stage 0      each accumulator tile is rounded to bf16 pairs (`pend`, 128
+//                registers: the gate and up values of 32 groups of 4 outputs)
+//                right before the first K-step's MFMA restarts it;
+//   stages 1-16  two groups per stage: gate math in the first K-step, the two
+//                8-byte stores after the stage's loads in the second;
+//   last tile    its epilogue after the loop, as in the kernel above.
+// Stores never let a load wait pass early: every wait counts only the loads
+// issued after the stage it waits for, and loads complete in order, so a wait
+// that passes has that stage's loads done whatever the stores issued after them
+// are doing (it may wait longer for those stores).  The last tile loads its own
+// first stages again (in bounds, never read) so every stage has the same waits;
+// the kernel ends by waiting for them.  Same roundings in the same order as the
+// kernel above: the outputs are bit-identical.
+constexpr int SGP_MIN_STAGES = 20;   // stage 0 + 16 epilogue stages + 3 prefetch stages
+
+struct SgpTile {
+    int64_t m0;
+    int n0;
+    int mrows;
+};
+
+__device__ __forceinline__ void sgp_tile(const SwigluParams& p, int v, SgpTile& t) {
+    const int group = SG_GROUP_M * p.n_nb;
+    const int g = v / group, first = g * SG_GROUP_M;
+    const int gm = min(p.n_mb - first, SG_GROUP_M);
+    const int w = v - g * group;
+    t.m0 = static_cast<int64_t>(first + w % gm) * SG_BM;
+    t.n0 = (w / gm) * SG_BN;
+    const int64_t mr = p.rows - t.m0;
+    t.mrows = static_cast<int>(mr < SG_BM ? mr : SG_BM);
+}
+
+__global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_persistent_kernel(SwigluParams p) {
+    __shared__ __attribute__((aligned(1024))) char smem[SG_NST * SG_STB];   // [stage][x | w][256][64 B]
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, hb = lane >> 5;
+    const uint32_t lds0 = lds_addr(smem);
+
+    // tiles of this work-group: its XCD's contiguous run (ids = xcd mod 8), dealt
+    // to the XCD's work-groups in turn
+    const int n = p.n_mb * p.n_nb;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, loc = bid >> 3;
+    const int nloc = (static_cast<int>(gridDim.x) - xcd + 7) >> 3;
+    const int q8 = n >> 3, rem = n & 7;
+    const int xbase = xcd < rem ? xcd * (q8 + 1) : rem * (q8 + 1) + (xcd - rem) * q8;
+    const int xcount = q8 + (xcd < rem ? 1 : 0);
+    const int ntile = loc < xcount ? (xcount - loc + nloc - 1) / nloc : 0;
+    if (ntile == 0) return;
+
+    const int nk = p.K / SG_BK;
+    const int lc = (lane & 3) ^ (((lane >> 3) ^ (lane >> 4)) & 3);
+    int vw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vw[i] = (((64 * wave + 16 * i + (lane >> 2)) & 127) * p.K) * 2 + lc * 16;
+    const uint32_t ldx_dst = lds0 + wave * 4096, ldw_dst = lds0 + SG_OPB + wave * 4096;
+
+    // a tile's load state: descriptors and x row offsets (rows past `rows`
+    // load the last valid row, as in the kernel above)
+    struct Ld {
+        lds_i32x4 rx, rw;
+        int vx[4];
+    };
+    auto make_ld = [&](const SgpTile& t, Ld& L) {
+        L.rx = lds_rsrc(p.x + t.m0 * p.ldx, static_cast<uint32_t>(static_cast<int64_t>(t.mrows) * p.ldx * 2));
+        L.rw = lds_rsrc((wave < 2 ? p.wg : p.wu) + static_cast<int64_t>(t.n0) * p.K,
+                        static_cast<uint32_t>(SG_BN * p.K * 2));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 64 * wave + 16 * i + (lane >> 2);
+            L.vx[i] = static_cast<int>((r < t.mrows ? r : t.mrows - 1) * p.ldx * 2) + lc * 16;
+        }
+    };
+    // the 8 loads of stage `sl` of a tile into LDS buffer `buf`
+    auto issue = [&](const Ld& L, int sl, int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_dma16(L.rx, L.vx[i], sl * SG_ROWB, ldx_dst + buf * SG_STB + i * 1024);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds_dma16(L.rw, vw[i], sl * SG_ROWB, ldw_dst + buf * SG_STB + i * 1024);
+    };
+
+    const int xrow0 = (wm * 128 + l32) * SG_ROWB;
+    const int wrow0 = SG_OPB + (wn * 64 + l32) * SG_ROWB;
+    const int swz = ((l32 >> 1) ^ (l32 >> 2)) & 3;
+    auto frag_ptr = [&](const char* st, int ks, int f) {
+        const int cb = ((2 * ks + hb) ^ swz) << 4;
+        const int row = f < 4 ? xrow0 + f * 32 * SG_ROWB : wrow0 + (((f - 4) >> 1) * 128 + ((f - 4) & 1) * 32) * SG_ROWB;
+        return reinterpret_cast<const sg_bf16x8*>(st + row + cb);
+    };
+
+    sg_f32x16 acc[4][4];
+    sg_f32x16 zero;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) zero[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] = zero;
+    // the previous tile's linear outputs in bf16, two per word; group
+    // gi = 8 i + 4 j + q (x tile i, gate tile j, register group q):
+    // {gate 0,1 | gate 2,3 | up 0,1 | up 2,3}
+    uint32_t pend[32][4];
+#pragma unroll
+    for (int gi = 0; gi < 32; ++gi)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pend[gi][e] = 0u;
+
+    // where the previous tile's outputs go (nowhere before the first tile)
+    int64_t ym0 = 0;
+    int ybytes = 0, yn0 = 0;
+    const int yrow = (wm * 128 + l32) * static_cast<int>(p.ldy) * 2;
+
+    // a, b, c: fragments as in the kernel above (b and c swap roles stage by stage)
+    sg_bf16x8 a[8], b[8], c[8];
+    sg_u32x2 ow[2];
+    int oo[2];
+    // one group of the previous tile: 4 outputs, kept for one 8-byte store
+    auto epi_group = [&](auto gtag, int slot) {
+        constexpr int gi = decltype(gtag)::value;
+        constexpr int i = gi >> 3, j = (gi >> 2) & 1, q = gi & 3;
+        float g[4], u[4], sg[4], o[4];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            g[2 * e] = __uint_as_float(pend[gi][e] << 16);
+            g[2 * e + 1] = __uint_as_float(pend[gi][e] & 0xffff0000u);
+            u[2 * e] = __uint_as_float(pend[gi][2 + e] << 16);
+            u[2 * e + 1] = __uint_as_float(pend[gi][2 + e] & 0xffff0000u);
+        }
+        sg_round2(sg_silu(g[0]), sg_silu(g[1]), sg[0], sg[1]);
+        sg_round2(sg_silu(g[2]), sg_silu(g[3]), sg[2], sg[3]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = sg[e] * u[e];
+        ow[slot] = sg_u32x2{sg_pack(o[0], o[1]), sg_pack(o[2], o[3])};
+        oo[slot] = yrow + i * 64 * static_cast<int>(p.ldy) + (yn0 + wn * 64 + 32 * j + 8 * q + 4 * hb) * 2;
+    };
+    // first K-step of a stage, with epilogue groups E0 and E0 + 1 when E0 >= 0
+    auto half_a = [&](auto etag) {
+        constexpr int E0 = decltype(etag)::value;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[4 + j], a[i], acc[j][i], 0, 0, 0);
+        if constexpr (E0 >= 0) {
+            epi_group(std::integral_constant<int, E0>{}, 0);
+            epi_group(std::integral_constant<int, E0 + 1>{}, 1);
+        }
+    };
+    // first K-step of a tile's stage 0: each accumulator tile becomes `pend`
+    // just before the MFMA that starts it again from zero
+    auto half_a_first = [&]() {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int gi = 8 * i + 4 * (j & 1) + q, e0 = j < 2 ? 0 : 2;
+                    pend[gi][e0] = sg_pack(acc[j][i][4 * q], acc[j][i][4 * q + 1]);
+                    pend[gi][e0 + 1] = sg_pack(acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]);
+                }
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[4 + j], a[i], zero, 0, 0, 0);
+            }
+    };
+    // second K-step of a stage: wait for the next stage (buffer `bufn`), then
+    // 16 MFMAs interleaved with the 8 loads of stage `sl` of load state L into
+    // buffer `bufl`, the next stage's fragment reads and, with `st`, the first
+    // half's two stores
+    auto half_b = [&](int bufn, const Ld& L, int sl, int bufl, const sg_bf16x8 (&cur)[8], sg_bf16x8 (&next)[8],
+                      auto st, __amdgpu_buffer_rsrc_t ry) {
+        __builtin_amdgcn_sched_barrier(0);
+        lds_wait_vm<8>();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        const char* stn = smem + bufn * SG_STB;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int j = t >> 2, i = t & 3;
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[4 + j], cur[i], acc[j][i], 0, 0, 0);
+            if (t < 4)
+                lds_dma16(L.rx, L.vx[t], sl * SG_ROWB, ldx_dst + bufl * SG_STB + t * 1024);
+            else if (t < 8)
+                lds_dma16(L.rw, vw[t - 4], sl * SG_ROWB, ldw_dst + bufl * SG_STB + (t - 4) * 1024);
+            if (t < 8)
+                a[t] = *frag_ptr(stn, 0, t);
+            else
+                next[t - 8] = *frag_ptr(stn, 1, t - 8);
+            if constexpr (decltype(st)::value) {
+                if (t == 8 || t == 9) __builtin_amdgcn_raw_buffer_store_b64(ow[t - 8], ry, oo[t - 8], 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    SgpTile tc, tn;
+    Ld lcur, lnext;
+    sgp_tile(p, xbase + loc, tc);
+    make_ld(tc, lcur);
+    issue(lcur, 0, 0);
+    issue(lcur, 1, 1);
+    issue(lcur, 2, 2);
+    lds_wait_vm<16>();
+    __syncthreads();
+    {
+        const char* st = smem;
+#pragma unroll
+        for (int f = 0; f < 8; ++f) a[f] = *frag_ptr(st, 0, f);
+#pragma unroll
+        for (int f = 0; f < 8; ++f) b[f] = *frag_ptr(st, 1, f);
+    }
+
+    constexpr std::integral_constant<int, -1> NOEPI{};
+    constexpr std::true_type ST{};
+    constexpr std::false_type NOST{};
+    // nk % 4 == 0: a tile's stage s sits in LDS buffer s % 4
+    for (int k = 0; k < ntile; ++k) {
+        const auto ry = __builtin_amdgcn_make_buffer_rsrc(p.y + ym0 * p.ldy, 0, ybytes, 0x00020000);
+        half_a_first();
+        half_b(1, lcur, 3, 3, b, c, NOST, ry);
+#define SGP_PAIR(S)                                                              \
+        half_a(std::integral_constant<int, 2 * ((S) - 1)>{});                  \
+        half_b(((S) + 1) & 3, lcur, (S) + 3, ((S) + 3) & 3, c, b, ST, ry);     \
+        half_a(std::integral_constant<int, 2 * (S)>{});                        \
+        half_b(((S) + 2) & 3, lcur, (S) + 4, ((S) + 4) & 3, b, c, ST, ry);
+        SGP_PAIR(1) SGP_PAIR(3) SGP_PAIR(5) SGP_PAIR(7) SGP_PAIR(9) SGP_PAIR(11) SGP_PAIR(13) SGP_PAIR(15)
+#undef SGP_PAIR
+        for (int s = 17; s + 1 <= nk - 4; s += 2) {
+            half_a(NOEPI);
+            half_b((s + 1) & 3, lcur, s + 3, (s + 3) & 3, c, b, NOST, ry);
+            half_a(NOEPI);
+            half_b((s + 2) & 3, lcur, s + 4, (s + 4) & 3, b, c, NOST, ry);
+        }
+        // the last three stages load the next tile's first three
+        sgp_tile(p, xbase + loc + (k + 1 < ntile ? k + 1 : k) * nloc, tn);
+        make_ld(tn, lnext);
+        half_a(NOEPI);
+        half_b((nk - 2) & 3, lnext, 0, 0, c, b, NOST, ry);
+        half_a(NOEPI);
+        half_b((nk - 1) & 3, lnext, 1, 1, b, c, NOST, ry);
+        half_a(NOEPI);
+        half_b(0, lnext, 2, 2, c, b, NOST, ry);
+
+        ym0 = tc.m0;
+        ybytes = static_cast<int>(static_cast<int64_t>(tc.mrows) * p.ldy * 2);
+        yn0 = tc.n0;
+        tc = tn;
+        lcur = lnext;
+    }
+
+    // the last tile's epilogue
+    const auto ry = __builtin_amdgcn_make_buffer_rsrc(p.y + ym0 * p.ldy, 0, ybytes, 0x00020000);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float g[4], u[4], sg[4], o[4];
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    sg_round2(acc[j][i][4 * q + e], acc[j][i][4 * q + e + 1], g[e], g[e + 1]);
+                    sg_round2(acc[j + 2][i][4 * q + e], acc[j + 2][i][4 * q + e + 1], u[e], u[e + 1]);
+                    sg_round2(sg_silu(g[e]), sg_silu(g[e + 1]), sg[e], sg[e + 1]);
+                    o[e] = sg[e] * u[e];
+                    o[e + 1] = sg[e + 1] * u[e + 1];
+                }
+                const sg_u32x2 w = {sg_pack(o[0], o[1]), sg_pack(o[2], o[3])};
+                const int col = yn0 + wn * 64 + 32 * j + 8 * q + 4 * hb;
+                __builtin_amdgcn_raw_buffer_store_b64(w, ry, yrow + i * 64 * static_cast<int>(p.ldy) + col * 2, 0, 0);
+            }
+        }
+    }
+    lds_wait_vm<0>();   // the last tile's unused loads
+}
+
 }  // namespace
 }  // namespace mogt
 
 using namespace mogt;
 
-extern "C" int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
-                                    int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype,
-                                    void* stream) {
+namespace {
+
+// path: 0 = by shape (persistent when d_in qualifies), 1 = one tile per
+// work-group, 2 = persistent
+int swiglu_launch(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows, int64_t d_in,
+                  int64_t hidden, int64_t ldx, int64_t ldy, int dtype, int path, void* stream) {
     clear_error();
+    if (path < 0 || path > 2) return set_error(MOGT_E_INVALID, "swiglu_gate: path must be 0, 1 or 2");
     if (dtype != MOGT_BF16) return set_error(MOGT_E_INVALID, "swiglu_gate: bf16 operands only");
     if (rows < 0 || d_in <= 0 || hidden <= 0) return set_error(MOGT_E_INVALID, "swiglu_gate: bad shape");
     if (d_in % SG_BK != 0 || hidden % SG_BN != 0)
@@ -331,7 +626,34 @@ extern "C" int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const voi
     prm.H = static_cast<int>(hidden);
     prm.n_mb = static_cast<int>(n_mb);
     prm.n_nb = static_cast<int>(n_nb);
-    hipLaunchKernelGGL(swiglu_gemm_kernel, dim3(static_cast<unsigned>(n_mb * n_nb)), dim3(SG_THREADS), 0,
+    const bool fits = d_in % (SG_NST * SG_BK) == 0 && d_in / SG_BK >= SGP_MIN_STAGES;
+    if (path == 2 && !fits)
+        return set_error(MOGT_E_INVALID, "swiglu_gate: the persistent schedule needs d_in %% %d == 0 and d_in >= %d",
+                         SG_NST * SG_BK, SGP_MIN_STAGES * SG_BK);
+    if (path == 1 || !fits) {
+        hipLaunchKernelGGL(swiglu_gemm_kernel, dim3(static_cast<unsigned>(n_mb * n_nb)), dim3(SG_THREADS), 0,
+                           static_cast<hipStream_t>(stream), prm);
+        return check_launch("swiglu_gemm_kernel");
+    }
+    int cus = 0;
+    const int rc = device_cu_count(cus);
+    if (rc != MOGT_OK) return rc;
+    const int64_t grid = n_mb * n_nb < cus ? n_mb * n_nb : cus;   // one work-group per CU (128 KB of LDS)
+    hipLaunchKernelGGL(swiglu_gemm_persistent_kernel, dim3(static_cast<unsigned>(grid)), dim3(SG_THREADS), 0,
                        static_cast<hipStream_t>(stream), prm);
-    return check_launch("swiglu_gemm_kernel");
+    return check_launch("swiglu_gemm_persistent_kernel");
+}
+
+}  // namespace
+
+extern "C" int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
+                                    int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype,
+                                    void* stream) {
+    return swiglu_launch(x, w_gate, w_up, y, rows, d_in, hidden, ldx, ldy, dtype, 0, stream);
+}
+
+extern "C" int mogt_swiglu_gate_fwd_cfg(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
+                                        int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, int path,
+                                        void* stream) {
+    return swiglu_launch(x, w_gate, w_up, y, rows, d_in, hidden, ldx, ldy, dtype, path, stream);
 }

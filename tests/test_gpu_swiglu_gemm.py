@@ -113,3 +113,53 @@ def test_swiglu_module_uses_the_fused_gate_without_grad(gpu):
     torch.cuda.synchronize()
     assert calls, "the no-grad bf16 forward did not take the fused gate"
     assert rel_err(to_np(fused), to_np(grad_path)) <= BF16_TOL
+
+
+@pytest.mark.parametrize("M,K,H,ldx,ldy", [(1000, 768, 3072, 768, 3072), (32768, 768, 3072, 768, 3072),
+                                           (300, 640, 256, 640, 256), (4096, 1024, 512, 1024, 512),
+                                           (513, 896, 384, 960, 388), (77, 768, 128, 768, 128)])
+def test_swiglu_gate_schedules_bit_identical(gpu, M, K, H, ldx, ldy):
+    """The persistent schedule (each CU's work-group streams its tiles' stages
+    back to back and runs a tile's gate math and stores inside the next tile's
+    main loop) against one tile per work-group: same roundings in the same
+    order, so the same bits.  Row tails, fewer tiles than CUs (M = 77, 300),
+    every stage count the persistent schedule takes up to 32, padded row
+    strides of x and y (the padding stays untouched)."""
+    announce(f"swiglu_gate schedules M={M} K={K} H={H} ldx={ldx} ldy={ldy}")
+    from mogt_amd import _lib
+
+    lib = _lib.load()
+    x, wg, wu = _operands(M, K, H, seed=M + 7 * K + H, dev=gpu)
+    xp = torch.zeros(M, ldx, dtype=torch.bfloat16, device=gpu)
+    xp[:, :K] = x
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    outs = []
+    for path in (1, 2, 0):
+        y = torch.full((M, ldy), 3.0, dtype=torch.bfloat16, device=gpu)
+        rc = lib.mogt_swiglu_gate_fwd_cfg(xp.data_ptr(), wg.data_ptr(), wu.data_ptr(), y.data_ptr(), M, K, H, ldx,
+                                          ldy, _lib.MOGT_BF16, path, stream)
+        _lib.check(rc, "mogt_swiglu_gate_fwd_cfg")
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert bool((outs[1][:, H:] == 3.0).all())
+    assert rel_err(to_np(outs[1][:, :H][:64].float()), _f64(x[:64], wg, wu)) <= BF16_TOL
+
+
+def test_swiglu_gate_persistent_refuses_other_depths(gpu):
+    """The persistent schedule needs d_in % 128 == 0 and d_in >= 640; forcing
+    it elsewhere is an error, and the default path takes the one-tile kernel."""
+    announce("swiglu_gate persistent schedule shape check")
+    from mogt_amd import _lib, ops
+
+    lib = _lib.load()
+    x, wg, wu = _operands(256, 96, 128, seed=1, dev=gpu)
+    y = torch.empty(256, 128, dtype=torch.bfloat16, device=gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    for K, xx, g_, u_ in [(96, x, wg, wu)] + [(k, *_operands(256, k, 128, seed=k, dev=gpu)) for k in (512, 704)]:
+        rc = lib.mogt_swiglu_gate_fwd_cfg(xx.data_ptr(), g_.data_ptr(), u_.data_ptr(), y.data_ptr(), 256, K, 128, K,
+                                          128, 1, 2, stream)
+        assert rc != 0, K
+    y0 = ops.swiglu_gate(x, wg, wu)
+    torch.cuda.synchronize()
+    assert rel_err(to_np(y0), _f64(x, wg, wu)) <= BF16_TOL
