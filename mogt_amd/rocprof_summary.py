@@ -138,6 +138,35 @@ def mfma_busy(c: dict) -> float | None:
     return busy / (SIMDS * active / XCDS)
 
 
+def per_step_lines(rows: list[dict], steps: int, top: int) -> list[str]:
+    """Kernel time per step of a run of `steps` steps (every dispatch of the
+    run, warm-up and set-up included, divided by `steps`): by group (this
+    library's kernels, library GEMMs, everything else), then by kernel."""
+    groups: dict = defaultdict(float)
+    per: dict = defaultdict(list)
+    for r in rows:
+        raw = r["Kernel_Name"]
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        name = short_name(raw)
+        if name.startswith(("Cijk_", "Custom_Cijk_")):
+            grp = "hipBLASLt GEMMs"
+        elif "mogt::" in raw:
+            grp = "HIP kernels of this library"
+        else:
+            grp = "PyTorch kernels and copies"
+        groups[grp] += us
+        per[display_name(name)].append(us)
+    total = sum(groups.values())
+    out = [f"{total / steps:.0f} us of kernels per step", "", "| Group | us per step | share |", "|---|---|---|"]
+    for g, us in sorted(groups.items(), key=lambda kv: -kv[1]):
+        out.append(f"| {g} | {us / steps:.0f} | {us / total:.0%} |")
+    out += ["", "| Kernel | Calls per step | Avg us | us per step |", "|---|---|---|---|"]
+    ranked = sorted(per.items(), key=lambda kv: -sum(kv[1]))
+    for name, d in ranked[:top or len(ranked)]:
+        out.append(f"| `{name[:100]}` | {len(d) / steps:.1f} | {statistics.mean(d):.1f} | {sum(d) / steps:.0f} |")
+    return out + [""]
+
+
 def summarize(args) -> str:
     from . import _build, _lib
 
@@ -164,6 +193,12 @@ def summarize(args) -> str:
                      f"WRITE_SIZE {wcopy:.1f} KiB; bytes = FETCH_SIZE x {fscale:.4f} + WRITE_SIZE x "
                      f"{wscale:.4f} (KiB x 1024).")
         lines.append("")
+
+    if args.per_step:
+        lines += per_step_lines(_csv(args.trace, "kernel_trace.csv"), args.per_step, args.top)
+        if args.note:
+            lines += [args.note, ""]
+        return "\n".join(lines)
 
     hdr = "| Kernel | WGs | WG size | VGPR | AGPR | LDS B | scratch B/lane | dispatches | avg us | median us | min us | max us |"
     sep = "|---|---|---|---|---|---|---|---|---|---|---|---|"
@@ -258,6 +293,8 @@ def main(argv=None) -> None:
                    help="substrings of the kernel names listed in the table (default: every kernel)")
     p.add_argument("--kernel", help="full short name of the kernel the key=value block describes")
     p.add_argument("--top", type=int, default=0, help="list only this many kernels (most total time first)")
+    p.add_argument("--per-step", type=int, default=0,
+                   help="instead of the kernel table: kernel time per step of a run of this many steps")
     p.add_argument("--algorithmic-bytes", type=int, default=0)
     p.add_argument("--sources", default="")
     p.add_argument("--bench-log")
