@@ -21,7 +21,7 @@
 //        sub-chunk's q, k, v are loaded into registers while this one computes.
 // K_A reads k and v with ordinary (cache-allocating) loads, so K_C usually finds
 // them in the Infinity Cache.  Layouts: f [B, L, H]; q, k, v, y [B, L, H, DH].
-#include "common.h"
+#include "lds_dma.h"
 
 namespace mogt {
 
@@ -551,6 +551,16 @@ constexpr int R1S_GROUPS_PER_CU = 3;   // resident one-launch work-groups per CU
 constexpr int R1S_NB = 16;            // aggregates loaded per batch of the slice scan
 constexpr int R1_SC1 = 16;            // buffer cache policy: agent-coherent (sc1)
 
+// One agent-coherent (sc1) dword per lane straight into LDS at lds + 4 * lane
+// (no register holds it).  m0 carries the LDS address; it is written here and
+// read only by the load that follows.
+__device__ __forceinline__ void r1_dma4_sc1(lds_i32x4 rsrc, int voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
 struct Rank1SParams {
     const void* f;
     const void* k;
@@ -719,6 +729,7 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
     __shared__ __attribute__((aligned(16))) float sE[R1_SUB][R1_T];
     __shared__ float sLcT[R1_SUB];
     __shared__ float sLcS[R1S_MAX_SC];
+    __shared__ float sCarry[R1_THREADS];   // slice scan: value handed from one part to the next
     __shared__ uint32_t sEpoch;
     __shared__ int sFail;
 
@@ -915,23 +926,46 @@ __global__ __launch_bounds__(R1_THREADS, 3) void rank1_single_kernel(Rank1SParam
         // slice [e0, e1) of every carried-in state: S_in(m + 1) = 2^LcS_m S_in(m) + agg_m
         const int E = (R1_DH * R1_DH + nsc - 1) / nsc;
         const int e0 = c * E, e1 = min(R1_DH * R1_DH, e0 + E);
-        for (int e = e0 + tid; e < e1; e += R1_THREADS) {
-            float Sv = 0.0f;
-            for (int m0 = 0; m0 < nsc - 1; m0 += R1S_NB) {
-                float av[R1S_NB];
+        // Every aggregate load of a thread's part in one batch, straight into
+        // LDS (the chain buffer, free until the carried-in state lands in it):
+        // the aggregates are cut into parts of R1S_NB, thread (part, el) of a
+        // round loads its part of element e0 + round * epr + el into
+        // sX[i * R1_THREADS + tid], and the parts continue the recurrence in
+        // turn from the value the previous part ended with: the same
+        // operations in the same order as one thread walking every aggregate.
+        const int nagg = nsc - 1, parts = (nagg + R1S_NB - 1) / R1S_NB;
+        const int epr = R1_THREADS / parts, rounds = (E + epr - 1) / epr;
+        const lds_i32x4 rAggD = lds_rsrc(aggSeq, static_cast<uint32_t>(nsc) * R1_DH * R1_DH * 4);
+        const uint32_t sxw = lds_addr(sX) + j * 256;   // this wave's 64 slots of a row of sX
+        for (int rd = 0; rd < rounds; ++rd) {
+            const int part = tid / epr, el = rd * epr + (tid - part * epr);
+            const bool act = part < parts && e0 + el < e1;
+            const int mb = part * R1S_NB;
+            // this wave's reads of its slots are done before the loads overwrite them
+            __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
 #pragma unroll
-                for (int i = 0; i < R1S_NB; ++i)   // past the published aggregates: out of range, reads 0
-                    av[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        rAgg, ((m0 + i < nsc - 1 ? m0 + i : nsc) * R1_DH * R1_DH + e) * 4, 0, R1_SC1));
+            for (int i = 0; i < R1S_NB; ++i)   // inactive lanes and past the aggregates: out of range, load 0
+                r1_dma4_sc1(rAggD, ((act && mb + i < nagg ? mb + i : nsc) * R1_DH * R1_DH + (act ? e0 + el : 0)) * 4,
+                            sxw + i * (R1_THREADS * 4));
+            lds_wait_vm<0>();   // each thread reads only the slots its own wave loaded
+            for (int q = 0; q < parts; ++q) {
+                if (act && part == q) {
+                    float Sv = q > 0 ? sCarry[el] : 0.0f;
+                    // offsets formed here from an opaque base, so none is held across the barriers
+                    int so = ((mb + 1) * R1_DH * R1_DH + e0 + el) * 4;
+                    asm volatile("" : "+v"(so));
 #pragma unroll
-                for (int i = 0; i < R1S_NB; ++i) {
-                    const int m = m0 + i;
-                    if (m < nsc - 1) {
-                        Sv = fmaf(exp2_hw(sLcS[m]), Sv, av[i]);
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sv), rSin,
-                                                              ((m + 1) * R1_DH * R1_DH + e) * 4, 0, R1_SC1);
+                    for (int i = 0; i < R1S_NB; ++i) {
+                        const int m = mb + i;
+                        if (m < nagg) {
+                            Sv = fmaf(exp2_hw(sLcS[m]), Sv, sX[i * R1_THREADS + tid]);
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sv), rSin, so + i * (R1_DH * R1_DH * 4),
+                                                                  0, R1_SC1);
+                        }
                     }
+                    if (q + 1 < parts) sCarry[el] = Sv;
                 }
+                if (q + 1 < parts) __syncthreads();
             }
         }
         wait_all_memory();

@@ -309,10 +309,11 @@ def test_checked_mode_reports_each_give_up_once(monkeypatch):
         ops._checked(ws, "scan")                  # one more
 
 
-@pytest.mark.parametrize("source", ["swiglu_gemm.hip", "wgrad_gemm.hip"])
+@pytest.mark.parametrize("source", ["swiglu_gemm.hip", "wgrad_gemm.hip", "rank1_scan.hip"])
 def test_gemm_m0_only_feeds_lds_dma(tmp_path, source):
-    """The bf16 GEMMs (fused SwiGLU, split-K weight gradient) set m0 in inline
-    assembly for their direct-to-LDS loads (clang warns that m0 is reserved).
+    """The bf16 GEMMs (fused SwiGLU, split-K weight gradient) and the rank-1
+    scan's carry exchange set m0 in inline assembly for their direct-to-LDS
+    loads (clang warns that m0 is reserved).
     On the code this build generates for gfx950: every write of m0 is one of
     those asm blocks, immediately followed by the load that reads it, and no
     other instruction of the kernel reads m0 (no LDS-direct, interpolation,
@@ -329,7 +330,7 @@ def test_gemm_m0_only_feeds_lds_dma(tmp_path, source):
     if not (shutil.which("hipcc") or Path("/opt/rocm/bin/hipcc").exists()):
         pytest.skip("hipcc not available")
     out = tmp_path / "gemm.s"
-    flags = [f for f in _build.HIPCC_FLAGS if f != "-fPIC"]
+    flags = [f for f in _build.HIPCC_FLAGS if f != "-fPIC"] + _build.FILE_FLAGS.get(source, [])
     cmd = [_build.hipcc(), *flags, f"-I{_build.INCLUDE}", "--cuda-device-only", "-S",
            str(_build.CSRC / source), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
