@@ -540,10 +540,12 @@ inline DiagTile pick_tile(int64_t B, int64_t L, int64_t D, const TileChoice* lis
 // D = 768, L = 8k..32k): chunks of 512 steps x 64 features, rows of 256 B, two
 // features per lane where the features and pointers allow.  A launch of 384
 // such chunks (1.5 generations of one group per CU) runs faster as 768 chunks
-// of 256 steps (L = 16k: 32.7 -> 30.7 us); short problems fall back to
-// shorter chunks so the grid still covers the GPU.
+// of 256 steps (L = 16k: 32.7 -> 30.7 us); a launch of fewer than 512 chunks
+// (one generation, under a group per CU) runs its 512-step chunks on 16 waves
+// of one feature per lane (L = 8k: 16.6 -> 16.0 us); short problems fall back
+// to shorter chunks so the grid still covers the GPU.
 inline DiagTile f32_tile(int64_t B, int64_t L, int64_t D, bool vec2) {
-    static const TileChoice v2[] = {{{2, 32, 32, 8}, 512}, {{2, 32, 32, 4}, 512}, {{2, 32, 32, 8}, 128},
+    static const TileChoice v2[] = {{{2, 32, 32, 8}, 512}, {{2, 32, 32, 4}, 512}, {{1, 64, 32, 16}, 128},
                                     {{2, 32, 16, 8}, 128}, {{2, 32, 8, 16}, 128}, {{1, 64, 8, 16}, 0}};
     static const TileChoice v1[] = {{{1, 64, 32, 16}, 128}, {{1, 64, 16, 16}, 128}, {{1, 64, 8, 16}, 0}};
     return vec2 ? pick_tile(B, L, D, v2, 6) : pick_tile(B, L, D, v1, 3);
