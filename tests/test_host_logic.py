@@ -176,6 +176,32 @@ def test_rocprof_summary_groups_and_calibrates(tmp_path):
     assert per[("k<1>", 8, 256)] == 150.0
 
 
+def test_rocprof_summary_per_step_table():
+    """The per-step kernel table: every dispatch divided by the step count,
+    grouped into this library's kernels, library GEMMs and the rest, kernels
+    ranked by total time."""
+    from mogt_amd import rocprof_summary as rs
+
+    def row(name, us, t0):
+        return dict(Kernel_Name=name, Start_Timestamp=str(t0), End_Timestamp=str(t0 + int(us * 1000)))
+
+    rows = [row("void mogt::swiglu_gemm_persistent_kernel(mogt::SwigluParams)", 300.0, 0),
+            row("void mogt::swiglu_gemm_persistent_kernel(mogt::SwigluParams)", 310.0, 10 ** 6),
+            row("Cijk_Ailk_Bljk_BBS_BH_MT256x256x64_MI16x16x1_SN", 80.0, 2 * 10 ** 6),
+            row("Cijk_Ailk_Bljk_BBS_BH_MT256x256x64_MI16x16x1_SN", 90.0, 3 * 10 ** 6),
+            row("void at::native::vectorized_gather_kernel<16, long>(char*)", 20.0, 4 * 10 ** 6)]
+    lines = rs.per_step_lines(rows, steps=2, top=0)
+    assert lines[0] == "400 us of kernels per step"
+    text = "\n".join(lines)
+    assert "| HIP kernels of this library | 305 | 76% |" in text
+    assert "| hipBLASLt GEMMs | 85 | 21% |" in text
+    assert "| PyTorch kernels and copies | 10 | 2% |" in text
+    kern = [ln for ln in lines if ln.startswith("| `")]
+    assert kern[0] == "| `swiglu_gemm_persistent_kernel` | 1.0 | 305.0 | 305 |"
+    assert kern[1] == "| `library GEMM MT256x256x64` | 1.0 | 85.0 | 85 |"
+    assert len(rs.per_step_lines(rows, steps=2, top=1)) == len(lines) - 2
+
+
 def test_rank1_buffer_ranges_stay_in_bounds():
     """Every buffer range the rank-1 kernels build (K_A's prefetches, the
     output and one-launch tiles, padding tiles past L) lies inside its tensor,
