@@ -408,6 +408,13 @@ int mogt_swiglu_gate_fwd(const void* x, const void* w_gate, const void* w_up, vo
 int mogt_swiglu_gate_fwd_cfg(const void* x, const void* w_gate, const void* w_up, void* y, int64_t rows,
                              int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, int path,
                              void* stream);
+/* mogt_swiglu_check_schedule: host-only self-check, no device work: walks the
+ *   persistent schedule's tile assignment for `rows` x `hidden` outputs on a
+ *   grid of `grid` work-groups (the CU count on a GPU) and returns 0 when every
+ *   tile, and every (row block, output block) it maps to, is taken by exactly
+ *   one work-group, else MOGT_E_INVALID naming the first violation.  No
+ *   counterpart in the reference.                                            */
+int mogt_swiglu_check_schedule(int64_t rows, int64_t hidden, int grid);
 /* mogt_linear_wgrad: dW = dY^T X, the weight gradient of a bias-free
  *   nn.Linear (model_mogt.py:25-27 w1, w2, w3, :57 phi_val, :61 theta_read;
  *   the grad_weight torch's linear backward forms), as a split-K GEMM on the

@@ -138,6 +138,7 @@ SIGNATURES: dict[str, tuple] = {
     "mogt_swiglu_gate_fwd_cfg": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
                  _c_int, _c_void_p]),
+    "mogt_swiglu_check_schedule": (_c_int, [_c_i64, _c_i64, _c_int]),
     "mogt_linear_wgrad": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
                  _c_void_p, _c_size, _c_void_p]),

@@ -42,6 +42,7 @@
 // tiles' stages back to back and runs a tile's epilogue inside the next tile's
 // main loop.  Both give bit-identical outputs.
 #include <type_traits>
+#include <vector>
 
 #include "lds_dma.h"
 
@@ -326,13 +327,40 @@ struct SgpTile {
     int mrows;
 };
 
-__device__ __forceinline__ void sgp_tile(const SwigluParams& p, int v, SgpTile& t) {
-    const int group = SG_GROUP_M * p.n_nb;
+// The persistent schedule's tiles of work-group `bid` of `grid`: its XCD
+// (ids = xcd mod 8; with fewer than 8 work-groups, each is its own group) owns
+// a contiguous run of the n tiles, dealt to that XCD's work-groups in turn;
+// the work-group takes tiles base, base + step, ... (count of them).  Shared by
+// the kernel and the host self-check (mogt_swiglu_check_schedule).
+struct SgpWalk {
+    int base, step, count;
+};
+
+__host__ __device__ inline SgpWalk sgp_walk(int n, int grid, int bid) {
+    const int nx = grid < 8 ? grid : 8;
+    const int xcd = bid % nx, loc = bid / nx;
+    const int nloc = (grid - xcd + nx - 1) / nx;
+    const int q = n / nx, rem = n - q * nx;
+    const int first = xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q;
+    const int xcount = q + (xcd < rem ? 1 : 0);
+    return SgpWalk{first + loc, nloc, loc < xcount ? (xcount - loc + nloc - 1) / nloc : 0};
+}
+
+// tile index -> (row block, output block): the 8-row-block walk of sg_tile
+__host__ __device__ inline void sgp_block(int n_mb, int n_nb, int v, int& mb, int& nb) {
+    const int group = SG_GROUP_M * n_nb;
     const int g = v / group, first = g * SG_GROUP_M;
-    const int gm = min(p.n_mb - first, SG_GROUP_M);
+    const int gm = (n_mb - first) < SG_GROUP_M ? (n_mb - first) : SG_GROUP_M;
     const int w = v - g * group;
-    t.m0 = static_cast<int64_t>(first + w % gm) * SG_BM;
-    t.n0 = (w / gm) * SG_BN;
+    mb = first + w % gm;
+    nb = w / gm;
+}
+
+__device__ __forceinline__ void sgp_tile(const SwigluParams& p, int v, SgpTile& t) {
+    int mb, nb;
+    sgp_block(p.n_mb, p.n_nb, v, mb, nb);
+    t.m0 = static_cast<int64_t>(mb) * SG_BM;
+    t.n0 = nb * SG_BN;
     const int64_t mr = p.rows - t.m0;
     t.mrows = static_cast<int>(mr < SG_BM ? mr : SG_BM);
 }
@@ -347,14 +375,8 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_persistent_kernel(Swig
 
     // tiles of this work-group: its XCD's contiguous run (ids = xcd mod 8), dealt
     // to the XCD's work-groups in turn
-    const int n = p.n_mb * p.n_nb;
-    const int bid = blockIdx.x;
-    const int xcd = bid & 7, loc = bid >> 3;
-    const int nloc = (static_cast<int>(gridDim.x) - xcd + 7) >> 3;
-    const int q8 = n >> 3, rem = n & 7;
-    const int xbase = xcd < rem ? xcd * (q8 + 1) : rem * (q8 + 1) + (xcd - rem) * q8;
-    const int xcount = q8 + (xcd < rem ? 1 : 0);
-    const int ntile = loc < xcount ? (xcount - loc + nloc - 1) / nloc : 0;
+    const SgpWalk walk = sgp_walk(p.n_mb * p.n_nb, static_cast<int>(gridDim.x), static_cast<int>(blockIdx.x));
+    const int ntile = walk.count;
     if (ntile == 0) return;
 
     const int nk = p.K / SG_BK;
@@ -503,7 +525,7 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_persistent_kernel(Swig
 
     SgpTile tc, tn;
     Ld lcur, lnext;
-    sgp_tile(p, xbase + loc, tc);
+    sgp_tile(p, walk.base, tc);
     make_ld(tc, lcur);
     issue(lcur, 0, 0);
     issue(lcur, 1, 1);
@@ -540,7 +562,7 @@ __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_persistent_kernel(Swig
             half_b((s + 2) & 3, lcur, s + 4, (s + 4) & 3, b, c, NOST, ry);
         }
         // the last three stages load the next tile's first three
-        sgp_tile(p, xbase + loc + (k + 1 < ntile ? k + 1 : k) * nloc, tn);
+        sgp_tile(p, walk.base + (k + 1 < ntile ? k + 1 : k) * walk.step, tn);
         make_ld(tn, lnext);
         half_a(NOEPI);
         half_b((nk - 2) & 3, lnext, 0, 0, c, b, NOST, ry);
@@ -656,4 +678,34 @@ extern "C" int mogt_swiglu_gate_fwd_cfg(const void* x, const void* w_gate, const
                                         int64_t d_in, int64_t hidden, int64_t ldx, int64_t ldy, int dtype, int path,
                                         void* stream) {
     return swiglu_launch(x, w_gate, w_up, y, rows, d_in, hidden, ldx, ldy, dtype, path, stream);
+}
+
+extern "C" int mogt_swiglu_check_schedule(int64_t rows, int64_t hidden, int grid) {
+    clear_error();
+    if (rows <= 0 || hidden <= 0 || hidden % SG_BN != 0 || grid <= 0)
+        return set_error(MOGT_E_INVALID, "swiglu_check_schedule: bad shape or grid");
+    const int64_t n_mb64 = (rows + SG_BM - 1) / SG_BM, n_nb64 = hidden / SG_BN;
+    if (n_mb64 * n_nb64 > (int64_t(1) << 24))
+        return set_error(MOGT_E_INVALID, "swiglu_check_schedule: too many tiles");
+    const int n_mb = static_cast<int>(n_mb64), n_nb = static_cast<int>(n_nb64), n = n_mb * n_nb;
+    std::vector<int> seen_v(n, 0), seen_b(n, 0);
+    for (int bid = 0; bid < grid; ++bid) {
+        const SgpWalk w = sgp_walk(n, grid, bid);
+        for (int k = 0; k < w.count; ++k) {
+            const int v = w.base + k * w.step;
+            if (v < 0 || v >= n)
+                return set_error(MOGT_E_INVALID, "swiglu schedule: work-group %d takes tile %d of %d", bid, v, n);
+            ++seen_v[v];
+            int mb, nb;
+            sgp_block(n_mb, n_nb, v, mb, nb);
+            if (mb < 0 || mb >= n_mb || nb < 0 || nb >= n_nb)
+                return set_error(MOGT_E_INVALID, "swiglu schedule: tile %d maps to block (%d, %d)", v, mb, nb);
+            ++seen_b[mb * n_nb + nb];
+        }
+    }
+    for (int v = 0; v < n; ++v)
+        if (seen_v[v] != 1 || seen_b[v] != 1)
+            return set_error(MOGT_E_INVALID, "swiglu schedule: tile %d taken %d times, block %d taken %d times", v,
+                             seen_v[v], v, seen_b[v]);
+    return MOGT_OK;
 }

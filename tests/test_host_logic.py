@@ -232,6 +232,23 @@ def _fake_device_workspace(monkeypatch):
     return ops, torch.device("cpu", 0)
 
 
+def test_swiglu_persistent_schedule_covers_every_tile_once():
+    """The persistent SwiGLU GEMM's tile assignment (a contiguous run per XCD,
+    dealt to that XCD's work-groups in turn, each tile mapped to its row and
+    output block): every tile taken by exactly one work-group, for CU counts of
+    other GPUs as well as MI355X's 256 and for fewer tiles than work-groups."""
+    from mogt_amd import _lib
+
+    lib = _lib.load()
+    for grid in (1, 3, 7, 8, 9, 37, 80, 104, 228, 255, 256, 304):
+        for rows in (1, 255, 256, 257, 300, 2049, 32768, 32768 + 100):
+            for hidden in (128, 384, 3072):
+                rc = lib.mogt_swiglu_check_schedule(rows, hidden, grid)
+                assert rc == 0, (grid, rows, hidden, lib.mogt_last_error())
+    assert lib.mogt_swiglu_check_schedule(0, 128, 256) != 0
+    assert lib.mogt_swiglu_check_schedule(100, 100, 256) != 0
+
+
 def test_lookback_workspaces_are_kept_apart_and_cleared_on_layout_change(monkeypatch):
     import pytest
 
