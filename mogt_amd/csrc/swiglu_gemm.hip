@@ -90,19 +90,40 @@ __device__ __forceinline__ void sg_round2(float lo, float hi, float& rlo, float&
     rhi = __uint_as_float(w & 0xffff0000u);
 }
 
-// block id -> (row block, output block)
-__device__ __forceinline__ void sg_tile(const SwigluParams& p, int& mb, int& nb) {
-    const int n = p.n_mb * p.n_nb;
-    const int bid = blockIdx.x;
-    const int q = n >> 3, rem = n & 7;
-    const int xcd = bid & 7, loc = bid >> 3;
-    const int v = xcd < rem ? xcd * (q + 1) + loc : rem * (q + 1) + (xcd - rem) * q + loc;
-    const int group = SG_GROUP_M * p.n_nb;
+// Tiles of work-group `bid` of `grid`: its XCD (ids = xcd mod 8; with fewer
+// than 8 work-groups, each is its own group) owns a contiguous run of the n
+// tiles, dealt to that XCD's work-groups in turn; the work-group takes tiles
+// base, base + step, ... (count of them).  One tile per work-group (grid = n)
+// and the persistent schedule (grid = min(n, CUs)) both use it, as does the
+// host self-check (mogt_swiglu_check_schedule).
+struct SgpWalk {
+    int base, step, count;
+};
+
+__host__ __device__ inline SgpWalk sgp_walk(int n, int grid, int bid) {
+    const int nx = grid < 8 ? grid : 8;
+    const int xcd = bid % nx, loc = bid / nx;
+    const int nloc = (grid - xcd + nx - 1) / nx;
+    const int q = n / nx, rem = n - q * nx;
+    const int first = xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q;
+    const int xcount = q + (xcd < rem ? 1 : 0);
+    return SgpWalk{first + loc, nloc, loc < xcount ? (xcount - loc + nloc - 1) / nloc : 0};
+}
+
+// tile index -> (row block, output block), 8 row blocks walked together
+__host__ __device__ inline void sgp_block(int n_mb, int n_nb, int v, int& mb, int& nb) {
+    const int group = SG_GROUP_M * n_nb;
     const int g = v / group, first = g * SG_GROUP_M;
-    const int gm = min(p.n_mb - first, SG_GROUP_M);
+    const int gm = (n_mb - first) < SG_GROUP_M ? (n_mb - first) : SG_GROUP_M;
     const int w = v - g * group;
     mb = first + w % gm;
     nb = w / gm;
+}
+
+// block id -> (row block, output block), one tile per work-group
+__device__ __forceinline__ void sg_tile(const SwigluParams& p, int& mb, int& nb) {
+    const int n = p.n_mb * p.n_nb;
+    sgp_block(p.n_mb, p.n_nb, sgp_walk(n, n, static_cast<int>(blockIdx.x)).base, mb, nb);
 }
 
 __global__ __launch_bounds__(SG_THREADS) void swiglu_gemm_kernel(SwigluParams p) {
@@ -327,34 +348,6 @@ struct SgpTile {
     int mrows;
 };
 
-// The persistent schedule's tiles of work-group `bid` of `grid`: its XCD
-// (ids = xcd mod 8; with fewer than 8 work-groups, each is its own group) owns
-// a contiguous run of the n tiles, dealt to that XCD's work-groups in turn;
-// the work-group takes tiles base, base + step, ... (count of them).  Shared by
-// the kernel and the host self-check (mogt_swiglu_check_schedule).
-struct SgpWalk {
-    int base, step, count;
-};
-
-__host__ __device__ inline SgpWalk sgp_walk(int n, int grid, int bid) {
-    const int nx = grid < 8 ? grid : 8;
-    const int xcd = bid % nx, loc = bid / nx;
-    const int nloc = (grid - xcd + nx - 1) / nx;
-    const int q = n / nx, rem = n - q * nx;
-    const int first = xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q;
-    const int xcount = q + (xcd < rem ? 1 : 0);
-    return SgpWalk{first + loc, nloc, loc < xcount ? (xcount - loc + nloc - 1) / nloc : 0};
-}
-
-// tile index -> (row block, output block): the 8-row-block walk of sg_tile
-__host__ __device__ inline void sgp_block(int n_mb, int n_nb, int v, int& mb, int& nb) {
-    const int group = SG_GROUP_M * n_nb;
-    const int g = v / group, first = g * SG_GROUP_M;
-    const int gm = (n_mb - first) < SG_GROUP_M ? (n_mb - first) : SG_GROUP_M;
-    const int w = v - g * group;
-    mb = first + w % gm;
-    nb = w / gm;
-}
 
 __device__ __forceinline__ void sgp_tile(const SwigluParams& p, int v, SgpTile& t) {
     int mb, nb;
@@ -688,24 +681,29 @@ extern "C" int mogt_swiglu_check_schedule(int64_t rows, int64_t hidden, int grid
     if (n_mb64 * n_nb64 > (int64_t(1) << 24))
         return set_error(MOGT_E_INVALID, "swiglu_check_schedule: too many tiles");
     const int n_mb = static_cast<int>(n_mb64), n_nb = static_cast<int>(n_nb64), n = n_mb * n_nb;
-    std::vector<int> seen_v(n, 0), seen_b(n, 0);
-    for (int bid = 0; bid < grid; ++bid) {
-        const SgpWalk w = sgp_walk(n, grid, bid);
-        for (int k = 0; k < w.count; ++k) {
-            const int v = w.base + k * w.step;
-            if (v < 0 || v >= n)
-                return set_error(MOGT_E_INVALID, "swiglu schedule: work-group %d takes tile %d of %d", bid, v, n);
-            ++seen_v[v];
-            int mb, nb;
-            sgp_block(n_mb, n_nb, v, mb, nb);
-            if (mb < 0 || mb >= n_mb || nb < 0 || nb >= n_nb)
-                return set_error(MOGT_E_INVALID, "swiglu schedule: tile %d maps to block (%d, %d)", v, mb, nb);
-            ++seen_b[mb * n_nb + nb];
+    // the persistent grid, then one tile per work-group
+    for (const int g : {grid, n}) {
+        std::vector<int> seen_v(n, 0), seen_b(n, 0);
+        for (int bid = 0; bid < g; ++bid) {
+            const SgpWalk w = sgp_walk(n, g, bid);
+            if (g == n && w.count != 1)
+                return set_error(MOGT_E_INVALID, "swiglu schedule: work-group %d of %d has %d tiles", bid, g, w.count);
+            for (int k = 0; k < w.count; ++k) {
+                const int v = w.base + k * w.step;
+                if (v < 0 || v >= n)
+                    return set_error(MOGT_E_INVALID, "swiglu schedule: work-group %d takes tile %d of %d", bid, v, n);
+                ++seen_v[v];
+                int mb, nb;
+                sgp_block(n_mb, n_nb, v, mb, nb);
+                if (mb < 0 || mb >= n_mb || nb < 0 || nb >= n_nb)
+                    return set_error(MOGT_E_INVALID, "swiglu schedule: tile %d maps to block (%d, %d)", v, mb, nb);
+                ++seen_b[mb * n_nb + nb];
+            }
         }
+        for (int v = 0; v < n; ++v)
+            if (seen_v[v] != 1 || seen_b[v] != 1)
+                return set_error(MOGT_E_INVALID, "swiglu schedule (grid %d): tile %d taken %d times, block %d taken %d "
+                                 "times", g, v, seen_v[v], v, seen_b[v]);
     }
-    for (int v = 0; v < n; ++v)
-        if (seen_v[v] != 1 || seen_b[v] != 1)
-            return set_error(MOGT_E_INVALID, "swiglu schedule: tile %d taken %d times, block %d taken %d times", v,
-                             seen_v[v], v, seen_b[v]);
     return MOGT_OK;
 }
